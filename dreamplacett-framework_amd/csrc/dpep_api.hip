@@ -1,0 +1,472 @@
+// dpep_api.hip -- the C ABI of libdpep.so (declared in include/dpep.h).
+//
+// A context owns every device buffer of one (M, N, nc_max, dtype) problem,
+// allocated once at creation; a step allocates nothing.  Launch sequence of
+// one step on the context's stream:
+//   k_init      density <- D0n (float atomics) or acc <- 0 (fixed point)
+//   k_scatter   cells -> bins
+//   k_row_dct   P1  (folds D0n / converts fixed point when deterministic)
+//   k_col_pass  P2
+//   k_row_inv   P3  -> field_x, field_y, potential
+//   k_gather    cells <- fields
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <new>
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/dpep.h"
+#include "dpep_internal.h"
+
+using namespace dpep;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                        \
+    do {                                                                     \
+        hipError_t e_ = (expr);                                              \
+        if (e_ != hipSuccess)                                                \
+            return fail(DPEP_ERR_HIP, "%s failed: %s", #expr,                 \
+                        hipGetErrorString(e_));                              \
+    } while (0)
+
+constexpr int kNumStages = 6;   // init, scatter, P1, P2, P3, gather
+
+bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+
+}  // namespace
+
+struct dpep_ctx {
+    int M = 0, N = 0, nc_max = 0, dtype = 0;
+    unsigned flags = 0;
+    int device = 0;
+    size_t esz = 4;
+    Grid grid{};
+    SpectralArgs sargs{};
+    void *d_px = nullptr, *d_py = nullptr, *d_sx = nullptr, *d_sy = nullptr;
+    void *d_d0n = nullptr, *d_density = nullptr, *d_potential = nullptr;
+    void *d_fx = nullptr, *d_fy = nullptr, *d_gx = nullptr, *d_gy = nullptr;
+    void *d_T = nullptr, *d_Ux = nullptr, *d_Uy = nullptr;
+    uint64_t* d_acc = nullptr;
+    void *d_twM = nullptr, *d_postM = nullptr, *d_twN = nullptr,
+         *d_postN = nullptr;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev[kNumStages + 1] = {};
+    hipEvent_t ev_x0 = nullptr, ev_x1 = nullptr;
+    int profiling = 0;
+    int nc = -1;                 // resident cells (-1: none uploaded)
+    int last_nc = 0;             // cells of the last computed step
+    int stepped = 0;
+    float h2d_ms = 0.f, d2h_den_ms = 0.f, d2h_out_ms = 0.f;
+};
+
+// ---------------------------------------------------------------------------
+// helpers
+// ---------------------------------------------------------------------------
+static int check_ctx(const dpep_ctx* c)
+{
+    if (!c) return fail(DPEP_ERR_ARG, "null context");
+    return DPEP_OK;
+}
+
+template <typename T>
+static std::vector<T> twiddles(int L)
+{
+    std::vector<T> v(2 * (size_t)L);
+    for (int m = 0; m < L; ++m) {
+        const double a = 2.0 * M_PI * (double)m / (double)L;
+        v[2 * m] = (T)cos(a);
+        v[2 * m + 1] = (T)-sin(a);
+    }
+    return v;
+}
+
+template <typename T>
+static std::vector<T> post_twiddles(int L)
+{
+    std::vector<T> v(2 * (size_t)(L / 2 + 1));
+    for (int k = 0; k <= L / 2; ++k) {
+        const double a = M_PI * (double)k / (2.0 * (double)L);
+        v[2 * k] = (T)cos(a);
+        v[2 * k + 1] = (T)-sin(a);
+    }
+    return v;
+}
+
+template <typename T>
+static int upload_tables(dpep_ctx* c)
+{
+    auto twM = twiddles<T>(c->M), twN = twiddles<T>(c->N);
+    auto poM = post_twiddles<T>(c->M), poN = post_twiddles<T>(c->N);
+    HIP_TRY(hipMalloc(&c->d_twM, twM.size() * sizeof(T)));
+    HIP_TRY(hipMalloc(&c->d_twN, twN.size() * sizeof(T)));
+    HIP_TRY(hipMalloc(&c->d_postM, poM.size() * sizeof(T)));
+    HIP_TRY(hipMalloc(&c->d_postN, poN.size() * sizeof(T)));
+    HIP_TRY(hipMemcpy(c->d_twM, twM.data(), twM.size() * sizeof(T), hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(c->d_twN, twN.data(), twN.size() * sizeof(T), hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(c->d_postM, poM.data(), poM.size() * sizeof(T), hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(c->d_postN, poN.data(), poN.size() * sizeof(T), hipMemcpyHostToDevice));
+    c->sargs.twM = c->d_twM;
+    c->sargs.postM = c->d_postM;
+    c->sargs.twN = c->d_twN;
+    c->sargs.postN = c->d_postN;
+    return DPEP_OK;
+}
+
+static void release(dpep_ctx* c)
+{
+    void* bufs[] = {c->d_px, c->d_py, c->d_sx, c->d_sy, c->d_d0n,
+                    c->d_density, c->d_potential, c->d_fx, c->d_fy, c->d_gx,
+                    c->d_gy, c->d_T, c->d_Ux, c->d_Uy, c->d_acc, c->d_twM,
+                    c->d_postM, c->d_twN, c->d_postN};
+    for (void* p : bufs)
+        if (p) (void)hipFree(p);
+    for (auto& e : c->ev)
+        if (e) (void)hipEventDestroy(e);
+    if (c->ev_x0) (void)hipEventDestroy(c->ev_x0);
+    if (c->ev_x1) (void)hipEventDestroy(c->ev_x1);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+}
+
+template <typename T>
+static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
+                    const T* sy, int nc, T* fx, T* fy, T* dens, T* phi,
+                    T* gx, T* gy, hipStream_t s)
+{
+    const bool det = (c->flags & DPEP_FLAG_DETERMINISTIC) != 0;
+    const bool gather = !(c->flags & DPEP_FLAG_NO_GATHER);
+    const size_t mn = (size_t)c->M * c->N;
+    uint64_t* acc = det ? c->d_acc : nullptr;
+    const bool prof = c->profiling != 0;
+    const T* d0n = (const T*)c->d_d0n;
+
+    // Every pointer a kernel dereferences must be set: a null here is a bug
+    // of this library, reported as an error instead of a device fault.
+    const SpectralArgs& a = c->sargs;
+    if (!a.twM || !a.postM || !a.twN || !a.postN || !d0n || !dens || !fx ||
+        !fy || !c->d_T || !c->d_Ux || !c->d_Uy || (a.potential && !phi) ||
+        (det && !acc) || (nc > 0 && (!px || !py || !sx || !sy)) ||
+        (nc > 0 && gather && (!gx || !gy)))
+        return fail(DPEP_ERR_STATE, "internal: a kernel argument is NULL");
+
+    HIP_TRY(hipEventRecord(c->ev[0], s));
+    HIP_TRY(launch_fill_init<T>(d0n, dens, acc, mn, s));
+    if (prof) HIP_TRY(hipEventRecord(c->ev[1], s));
+    HIP_TRY(launch_scatter<T>(px, py, sx, sy, nc, c->grid, dens, acc, s));
+    if (prof) HIP_TRY(hipEventRecord(c->ev[2], s));
+    HIP_TRY(launch_row_dct<T>(c->sargs, dens, acc, d0n, dens, (T*)c->d_T, s));
+    if (prof) HIP_TRY(hipEventRecord(c->ev[3], s));
+    HIP_TRY(launch_col_pass<T>(c->sargs, (T*)c->d_T, (T*)c->d_Ux, (T*)c->d_Uy, s));
+    if (prof) HIP_TRY(hipEventRecord(c->ev[4], s));
+    HIP_TRY(launch_row_inv<T>(c->sargs, (const T*)c->d_Ux, (const T*)c->d_Uy,
+                              (const T*)c->d_T, fx, fy, phi, s));
+    if (prof) HIP_TRY(hipEventRecord(c->ev[5], s));
+    if (gather)
+        HIP_TRY(launch_gather<T>(px, py, sx, sy, nc, c->grid, fx, fy, gx, gy, s));
+    HIP_TRY(hipEventRecord(c->ev[kNumStages], s));
+    c->last_nc = nc;
+    c->stepped = 1;
+    return DPEP_OK;
+}
+
+static int step_dispatch(dpep_ctx* c, const void* px, const void* py,
+                         const void* sx, const void* sy, int nc, void* fx,
+                         void* fy, void* dens, void* phi, void* gx, void* gy,
+                         hipStream_t s)
+{
+    if (!fx) fx = c->d_fx;
+    if (!fy) fy = c->d_fy;
+    if (!dens) dens = c->d_density;
+    if (!phi) phi = c->d_potential;
+    if (!gx) gx = c->d_gx;
+    if (!gy) gy = c->d_gy;
+    if (c->dtype == DPEP_DTYPE_F32)
+        return run_step<float>(c, (const float*)px, (const float*)py,
+                               (const float*)sx, (const float*)sy, nc,
+                               (float*)fx, (float*)fy, (float*)dens,
+                               (float*)phi, (float*)gx, (float*)gy, s);
+    return run_step<double>(c, (const double*)px, (const double*)py,
+                            (const double*)sx, (const double*)sy, nc,
+                            (double*)fx, (double*)fy, (double*)dens,
+                            (double*)phi, (double*)gx, (double*)gy, s);
+}
+
+static float elapsed(hipEvent_t a, hipEvent_t b)
+{
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, a, b) != hipSuccess) return 0.f;
+    return ms;
+}
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+int dpep_abi_version(void) { return DPEP_ABI_VERSION; }
+
+const char* dpep_build_info(void)
+{
+    return "dpep abi 1; HIP kernels for gfx950; scatter/P1/P2/P3/gather";
+}
+
+const char* dpep_last_error(void) { return g_last_error.c_str(); }
+
+int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
+                double yh, int dtype, unsigned flags, dpep_ctx** out)
+{
+    if (!out) return fail(DPEP_ERR_ARG, "out is NULL");
+    *out = nullptr;
+    if (dtype != DPEP_DTYPE_F32 && dtype != DPEP_DTYPE_F64)
+        return fail(DPEP_ERR_ARG, "dtype must be DPEP_DTYPE_F32 or DPEP_DTYPE_F64");
+    const int maxL = dtype == DPEP_DTYPE_F32 ? 8192 : 4096;
+    if (!is_pow2(M) || !is_pow2(N) || M < 8 || N < 8 || M > maxL || N > maxL)
+        return fail(DPEP_ERR_UNSUPPORTED,
+                    "num_bins_x=%d num_bins_y=%d: both must be powers of two in [8, %d]",
+                    M, N, maxL);
+    if (nc_max < 0) return fail(DPEP_ERR_ARG, "nc_max=%d must be >= 0", nc_max);
+    if (!(xh > xl) || !(yh > yl) || !isfinite(xl) || !isfinite(yl) ||
+        !isfinite(xh) || !isfinite(yh))
+        return fail(DPEP_ERR_ARG, "die [%g,%g]x[%g,%g] is empty or not finite",
+                    xl, xh, yl, yh);
+    if (flags & ~(DPEP_FLAG_DETERMINISTIC | DPEP_FLAG_NO_POTENTIAL |
+                  DPEP_FLAG_NO_STRETCH | DPEP_FLAG_NO_GATHER))
+        return fail(DPEP_ERR_ARG, "unknown flag bits 0x%x", flags);
+
+    static std::once_flag once;
+    static hipError_t prep_err = hipSuccess;
+    std::call_once(once, [] { prep_err = spectral_prepare(); });
+    if (prep_err != hipSuccess)
+        return fail(DPEP_ERR_HIP, "kernel attribute set-up failed: %s",
+                    hipGetErrorString(prep_err));
+
+    dpep_ctx* c = new (std::nothrow) dpep_ctx();
+    if (!c) return fail(DPEP_ERR_NOMEM, "host allocation failed");
+    c->M = M; c->N = N; c->nc_max = nc_max; c->dtype = dtype; c->flags = flags;
+    c->esz = dtype == DPEP_DTYPE_F32 ? 4 : 8;
+    Grid& g = c->grid;
+    g.M = M; g.N = N; g.xl = xl; g.yl = yl; g.xh = xh; g.yh = yh;
+    g.bsx = (xh - xl) / M;
+    g.bsy = (yh - yl) / N;
+    g.inv_ba = 1.0 / (g.bsx * g.bsy);
+    g.minw = M_SQRT2 * g.bsx;
+    g.minh = M_SQRT2 * g.bsy;
+    g.stretch = (flags & DPEP_FLAG_NO_STRETCH) ? 0 : 1;
+
+    SpectralArgs& a = c->sargs;
+    a.M = M; a.N = N;
+    a.tiles.TX = 2 * spectral_fpw(N, dtype);
+    a.tiles.TV = 2 * spectral_fpw(M, dtype);
+    a.wu_step = 2.0 * M_PI / M;
+    a.wv_step = 2.0 * M_PI / N * (g.bsx / g.bsy);
+    a.potential = (flags & DPEP_FLAG_NO_POTENTIAL) ? 0 : 1;
+
+    int rc = DPEP_OK;
+    auto step = [&]() -> int {
+        HIP_TRY(hipGetDevice(&c->device));
+        HIP_TRY(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+        for (auto& e : c->ev) HIP_TRY(hipEventCreate(&e));
+        HIP_TRY(hipEventCreate(&c->ev_x0));
+        HIP_TRY(hipEventCreate(&c->ev_x1));
+        const size_t mnb = (size_t)M * N * c->esz;
+        const size_t ncb = (size_t)(nc_max > 0 ? nc_max : 1) * c->esz;
+        void** cellbufs[] = {&c->d_px, &c->d_py, &c->d_sx, &c->d_sy, &c->d_gx, &c->d_gy};
+        for (void** p : cellbufs) HIP_TRY(hipMalloc(p, ncb));
+        void** mapbufs[] = {&c->d_d0n, &c->d_density, &c->d_fx, &c->d_fy,
+                            &c->d_T, &c->d_Ux, &c->d_Uy};
+        for (void** p : mapbufs) HIP_TRY(hipMalloc(p, mnb));
+        if (a.potential) HIP_TRY(hipMalloc(&c->d_potential, mnb));
+        if (flags & DPEP_FLAG_DETERMINISTIC)
+            HIP_TRY(hipMalloc((void**)&c->d_acc, (size_t)M * N * sizeof(uint64_t)));
+        HIP_TRY(hipMemset(c->d_d0n, 0, mnb));
+        return dtype == DPEP_DTYPE_F32 ? upload_tables<float>(c)
+                                       : upload_tables<double>(c);
+    };
+    rc = step();
+    if (rc != DPEP_OK) {
+        release(c);
+        delete c;
+        return rc;
+    }
+    *out = c;
+    return DPEP_OK;
+}
+
+int dpep_destroy(dpep_ctx* c)
+{
+    if (!c) return DPEP_OK;
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    release(c);
+    delete c;
+    return DPEP_OK;
+}
+
+int dpep_set_initial_density(dpep_ctx* c, const void* d0n)
+{
+    if (int rc = check_ctx(c)) return rc;
+    if (!d0n) return fail(DPEP_ERR_ARG, "initial density pointer is NULL");
+    const size_t bytes = (size_t)c->M * c->N * c->esz;
+    HIP_TRY(hipMemcpyAsync(c->d_d0n, d0n, bytes, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return DPEP_OK;
+}
+
+int dpep_set_cells(dpep_ctx* c, const void* px, const void* py,
+                   const void* sx, const void* sy, int nc)
+{
+    if (int rc = check_ctx(c)) return rc;
+    if (nc < 0 || nc > c->nc_max)
+        return fail(DPEP_ERR_ARG, "nc=%d outside [0, nc_max=%d]", nc, c->nc_max);
+    if (nc > 0 && (!px || !py || !sx || !sy))
+        return fail(DPEP_ERR_ARG, "cell array is NULL");
+    const size_t bytes = (size_t)nc * c->esz;
+    HIP_TRY(hipEventRecord(c->ev_x0, c->stream));
+    if (nc > 0) {
+        HIP_TRY(hipMemcpyAsync(c->d_px, px, bytes, hipMemcpyHostToDevice, c->stream));
+        HIP_TRY(hipMemcpyAsync(c->d_py, py, bytes, hipMemcpyHostToDevice, c->stream));
+        HIP_TRY(hipMemcpyAsync(c->d_sx, sx, bytes, hipMemcpyHostToDevice, c->stream));
+        HIP_TRY(hipMemcpyAsync(c->d_sy, sy, bytes, hipMemcpyHostToDevice, c->stream));
+    }
+    HIP_TRY(hipEventRecord(c->ev_x1, c->stream));
+    HIP_TRY(hipEventSynchronize(c->ev_x1));
+    c->h2d_ms = elapsed(c->ev_x0, c->ev_x1);
+    c->nc = nc;
+    return DPEP_OK;
+}
+
+int dpep_compute(dpep_ctx* c)
+{
+    if (int rc = check_ctx(c)) return rc;
+    if (c->nc < 0) return fail(DPEP_ERR_STATE, "dpep_set_cells was not called");
+    return step_dispatch(c, c->d_px, c->d_py, c->d_sx, c->d_sy, c->nc, nullptr,
+                         nullptr, nullptr, nullptr, nullptr, nullptr, c->stream);
+}
+
+int dpep_sync(dpep_ctx* c)
+{
+    if (int rc = check_ctx(c)) return rc;
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return DPEP_OK;
+}
+
+int dpep_get_outputs(dpep_ctx* c, void* density, void* potential,
+                     void* field_x, void* field_y, void* grad_x, void* grad_y)
+{
+    if (int rc = check_ctx(c)) return rc;
+    if (!c->stepped) return fail(DPEP_ERR_STATE, "no step has been computed");
+    if (potential && !c->d_potential)
+        return fail(DPEP_ERR_STATE, "context was created with DPEP_FLAG_NO_POTENTIAL");
+    if ((grad_x || grad_y) && (c->flags & DPEP_FLAG_NO_GATHER))
+        return fail(DPEP_ERR_STATE, "context was created with DPEP_FLAG_NO_GATHER");
+    const size_t mnb = (size_t)c->M * c->N * c->esz;
+    const size_t ncb = (size_t)c->last_nc * c->esz;
+    hipStream_t s = c->stream;
+    HIP_TRY(hipEventRecord(c->ev_x0, s));
+    if (density) HIP_TRY(hipMemcpyAsync(density, c->d_density, mnb, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipEventRecord(c->ev_x1, s));
+    HIP_TRY(hipEventSynchronize(c->ev_x1));
+    c->d2h_den_ms = elapsed(c->ev_x0, c->ev_x1);
+    HIP_TRY(hipEventRecord(c->ev_x0, s));
+    if (potential) HIP_TRY(hipMemcpyAsync(potential, c->d_potential, mnb, hipMemcpyDeviceToHost, s));
+    if (field_x) HIP_TRY(hipMemcpyAsync(field_x, c->d_fx, mnb, hipMemcpyDeviceToHost, s));
+    if (field_y) HIP_TRY(hipMemcpyAsync(field_y, c->d_fy, mnb, hipMemcpyDeviceToHost, s));
+    if (grad_x && ncb) HIP_TRY(hipMemcpyAsync(grad_x, c->d_gx, ncb, hipMemcpyDeviceToHost, s));
+    if (grad_y && ncb) HIP_TRY(hipMemcpyAsync(grad_y, c->d_gy, ncb, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipEventRecord(c->ev_x1, s));
+    HIP_TRY(hipEventSynchronize(c->ev_x1));
+    c->d2h_out_ms = elapsed(c->ev_x0, c->ev_x1);
+    return DPEP_OK;
+}
+
+int dpep_step(dpep_ctx* c, const void* px, const void* py, const void* sx,
+              const void* sy, int nc, void* field_x, void* field_y,
+              void* density, void* potential, void* grad_x, void* grad_y)
+{
+    int rc = dpep_set_cells(c, px, py, sx, sy, nc);
+    if (rc) return rc;
+    if ((rc = dpep_compute(c))) return rc;
+    return dpep_get_outputs(c, density, potential, field_x, field_y, grad_x,
+                            grad_y);
+}
+
+int dpep_step_device(dpep_ctx* c, const void* d_px, const void* d_py,
+                     const void* d_sx, const void* d_sy, int nc,
+                     void* d_field_x, void* d_field_y, void* d_density,
+                     void* d_potential, void* d_grad_x, void* d_grad_y,
+                     void* stream)
+{
+    if (int rc = check_ctx(c)) return rc;
+    if (nc < 0 || nc > c->nc_max)
+        return fail(DPEP_ERR_ARG, "nc=%d outside [0, nc_max=%d]", nc, c->nc_max);
+    if (nc > 0 && (!d_px || !d_py || !d_sx || !d_sy))
+        return fail(DPEP_ERR_ARG, "cell array is NULL");
+    if (d_potential && !c->sargs.potential)
+        return fail(DPEP_ERR_STATE, "context was created with DPEP_FLAG_NO_POTENTIAL");
+    hipStream_t s = stream ? (hipStream_t)stream : c->stream;
+    return step_dispatch(c, d_px, d_py, d_sx, d_sy, nc, d_field_x, d_field_y,
+                         d_density, d_potential, d_grad_x, d_grad_y, s);
+}
+
+int dpep_get_timings(dpep_ctx* c, float* out)
+{
+    if (int rc = check_ctx(c)) return rc;
+    if (!out) return fail(DPEP_ERR_ARG, "out is NULL");
+    if (!c->stepped) return fail(DPEP_ERR_STATE, "no step has been computed");
+    HIP_TRY(hipEventSynchronize(c->ev[kNumStages]));
+    for (int i = 0; i < DPEP_NUM_TIMINGS; ++i) out[i] = 0.f;
+    const float total = elapsed(c->ev[0], c->ev[kNumStages]);
+    out[0] = c->h2d_ms;
+    if (c->profiling) {
+        out[1] = elapsed(c->ev[0], c->ev[2]);              // init + scatter
+        out[5] = elapsed(c->ev[2], c->ev[5]);              // P1 + P2 + P3
+        out[2] = elapsed(c->ev[5], c->ev[kNumStages]);     // gather
+    } else {
+        out[5] = total;
+    }
+    out[3] = c->d2h_den_ms;
+    out[6] = c->d2h_out_ms;
+    out[8] = c->h2d_ms + total + c->d2h_den_ms + c->d2h_out_ms;
+    return DPEP_OK;
+}
+
+int dpep_get_kernel_times(dpep_ctx* c, float* out, int n)
+{
+    if (int rc = check_ctx(c)) return rc;
+    if (!out || n < 0) return fail(DPEP_ERR_ARG, "bad output buffer");
+    if (!c->stepped) return fail(DPEP_ERR_STATE, "no step has been computed");
+    if (!c->profiling)
+        return fail(DPEP_ERR_STATE, "per-kernel times need dpep_set_profiling(ctx, 1)");
+    HIP_TRY(hipEventSynchronize(c->ev[kNumStages]));
+    for (int i = 0; i < n; ++i) out[i] = 0.f;
+    for (int i = 0; i < kNumStages && i < n; ++i)
+        out[i] = 1000.f * elapsed(c->ev[i], c->ev[i + 1]);
+    return DPEP_OK;
+}
+
+int dpep_set_profiling(dpep_ctx* c, int enable)
+{
+    if (int rc = check_ctx(c)) return rc;
+    c->profiling = enable ? 1 : 0;
+    return DPEP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,282 @@
+// dpep_device.h -- device-side building blocks shared by the dpep kernels:
+// vector types, the per-cell stretch/span/overlap geometry, and the
+// LDS-resident mixed-radix Stockham FFT used by the spectral passes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dpep {
+
+// ---------------------------------------------------------------------------
+// Grid description passed by value to every kernel.
+// ---------------------------------------------------------------------------
+struct Grid {
+    int M, N;                 // bins along x (rows) and y (contiguous)
+    double xl, yl, xh, yh;    // die
+    double bsx, bsy;          // bin sizes
+    double inv_ba;            // 1 / (bsx * bsy)
+    double minw, minh;        // sqrt2 * bsx, sqrt2 * bsy (stretch floor)
+    int stretch;              // 1: DREAMPlace small-cell stretch
+};
+
+// Fixed-point scale of the deterministic accumulator: a bin's density
+// (area / bin area) is held as round(density * 2^36) in an unsigned 64-bit
+// word, exact for per-bin densities below 2^27.
+constexpr double kFixScale = 68719476736.0;          // 2^36
+constexpr double kFixInv = 1.0 / 68719476736.0;
+
+template <typename T> struct vec2;
+template <> struct vec2<float> { using type = float2; };
+template <> struct vec2<double> { using type = double2; };
+template <typename T> using vec2_t = typename vec2<T>::type;
+
+template <typename C>
+__device__ __forceinline__ C cadd(C a, C b) { return C{a.x + b.x, a.y + b.y}; }
+template <typename C>
+__device__ __forceinline__ C csub(C a, C b) { return C{a.x - b.x, a.y - b.y}; }
+template <typename C>
+__device__ __forceinline__ C cmul(C a, C b)
+{
+    return C{a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x};
+}
+template <typename C>
+__device__ __forceinline__ C cconj(C a) { return C{a.x, -a.y}; }
+// multiply by -i (forward) or +i (inverse)
+template <bool INV, typename C>
+__device__ __forceinline__ C cmul_mi(C a)
+{
+    return INV ? C{-a.y, a.x} : C{a.y, -a.x};
+}
+
+// ---------------------------------------------------------------------------
+// Cell geometry: stretch, bin span, 1-D overlap.  Evaluated in float64 with
+// contraction disabled so the GPU reproduces the float64 oracle's spans.
+// ---------------------------------------------------------------------------
+struct CellSpan {
+    double x, y, w, h, ratio;
+    int bxl, bxh, byl, byh;
+};
+
+__device__ __forceinline__ bool cell_span(double px, double py, double sx,
+                                          double sy, const Grid& g,
+                                          CellSpan& c)
+{
+#pragma clang fp contract(off)
+    if (!(isfinite(px) && isfinite(py) && isfinite(sx) && isfinite(sy)))
+        return false;
+    if (!(sx > 0.0 && sy > 0.0)) return false;
+    double w = sx, h = sy, x = px, y = py, ratio = 1.0;
+    if (g.stretch) {
+        w = sx > g.minw ? sx : g.minw;
+        h = sy > g.minh ? sy : g.minh;
+        x = px + 0.5 * (sx - w);
+        y = py + 0.5 * (sy - h);
+        ratio = (sx * sy) / (w * h);
+    }
+    double fxl = floor((x - g.xl) / g.bsx);
+    double fxh = floor((x + w - g.xl) / g.bsx);
+    double fyl = floor((y - g.yl) / g.bsy);
+    double fyh = floor((y + h - g.yl) / g.bsy);
+    fxl = fxl < 0.0 ? 0.0 : fxl;
+    fyl = fyl < 0.0 ? 0.0 : fyl;
+    fxh = fxh > (double)(g.M - 1) ? (double)(g.M - 1) : fxh;
+    fyh = fyh > (double)(g.N - 1) ? (double)(g.N - 1) : fyh;
+    if (fxl > fxh || fyl > fyh) return false;
+    c.x = x; c.y = y; c.w = w; c.h = h; c.ratio = ratio;
+    c.bxl = (int)fxl; c.bxh = (int)fxh;
+    c.byl = (int)fyl; c.byh = (int)fyh;
+    return true;
+}
+
+__device__ __forceinline__ double overlap_1d(double lo, double ext,
+                                             double origin, double bs, int k)
+{
+#pragma clang fp contract(off)
+    const double bl = origin + k * bs;
+    const double br = origin + (k + 1) * bs;
+    const double hi = lo + ext;
+    const double a = lo > bl ? lo : bl;
+    const double b = hi < br ? hi : br;
+    const double o = b - a;
+    return o > 0.0 ? o : 0.0;
+}
+
+// ---------------------------------------------------------------------------
+// LDS FFT.  One complex FFT of length L is computed by TPF = L / E threads,
+// each holding E = min(16, L) elements per stage.  Stages are radix 16 while
+// the remaining factor allows, then one radix 2/4/8 stage (Stockham autosort:
+// natural order in and out, in place through registers between barriers).
+// ---------------------------------------------------------------------------
+__host__ __device__ constexpr int fft_e(int L) { return L < 16 ? L : 16; }
+__host__ __device__ constexpr int lds_pad(int e) { return e + (e >> 5); }
+__host__ __device__ constexpr int lds_len(int L) { return L + (L >> 5); }
+
+// Makhoul's even/odd-reversed ordering: x[m] sits at position perm(m).
+template <int L>
+__device__ __forceinline__ int makhoul_pos(int m)
+{
+    return (m & 1) ? (L - 1 - (m >> 1)) : (m >> 1);
+}
+
+// In-register DFTs of size 2, 4, 8, 16 (natural order in and out).
+// Forward uses W = exp(-2 pi i / R); INV conjugates.
+template <bool INV, typename C>
+__device__ __forceinline__ void dft2(C& a, C& b)
+{
+    C t = csub(a, b);
+    a = cadd(a, b);
+    b = t;
+}
+
+template <bool INV, typename C>
+__device__ __forceinline__ void dft4(C& x0, C& x1, C& x2, C& x3)
+{
+    C a = cadd(x0, x2), b = csub(x0, x2);
+    C c = cadd(x1, x3), d = cmul_mi<INV>(csub(x1, x3));
+    x0 = cadd(a, c);
+    x2 = csub(a, c);
+    x1 = cadd(b, d);
+    x3 = csub(b, d);
+}
+
+// twiddle W_R^k for R in {8, 16}; k <= 9
+template <typename T, bool INV>
+__device__ __forceinline__ vec2_t<T> w16(int k)
+{
+    using C = vec2_t<T>;
+    const T c1 = (T)0.92387953251128675613, s1 = (T)0.38268343236508977173;
+    const T c2 = (T)0.70710678118654752440;
+    C w;
+    switch (k) {
+    case 0: w = C{(T)1, (T)0}; break;
+    case 1: w = C{c1, -s1}; break;
+    case 2: w = C{c2, -c2}; break;
+    case 3: w = C{s1, -c1}; break;
+    case 4: w = C{(T)0, (T)-1}; break;
+    case 5: w = C{-s1, -c1}; break;
+    case 6: w = C{-c2, -c2}; break;
+    case 7: w = C{-c1, -s1}; break;
+    case 8: w = C{(T)-1, (T)0}; break;
+    default: w = C{-c1, s1}; break;
+    }
+    if (INV) w.y = -w.y;
+    return w;
+}
+
+template <typename T, bool INV>
+__device__ __forceinline__ void dft8(vec2_t<T>* v)
+{
+    using C = vec2_t<T>;
+    // n = 2 n1 + n2, k = k1 + 4 k2
+    C e0 = v[0], e1 = v[2], e2 = v[4], e3 = v[6];
+    C o0 = v[1], o1 = v[3], o2 = v[5], o3 = v[7];
+    dft4<INV>(e0, e1, e2, e3);
+    dft4<INV>(o0, o1, o2, o3);
+    o1 = cmul(o1, w16<T, INV>(2));   // W8^1 = W16^2
+    o2 = cmul_mi<INV>(o2);           // W8^2
+    o3 = cmul(o3, w16<T, INV>(6));   // W8^3 = W16^6
+    v[0] = cadd(e0, o0); v[4] = csub(e0, o0);
+    v[1] = cadd(e1, o1); v[5] = csub(e1, o1);
+    v[2] = cadd(e2, o2); v[6] = csub(e2, o2);
+    v[3] = cadd(e3, o3); v[7] = csub(e3, o3);
+}
+
+template <typename T, bool INV>
+__device__ __forceinline__ void dft16(vec2_t<T>* v)
+{
+    using C = vec2_t<T>;
+    // n = 4 n1 + n2, k = k1 + 4 k2
+    C y[4][4];
+#pragma unroll
+    for (int n2 = 0; n2 < 4; ++n2) {
+        C a = v[n2], b = v[n2 + 4], c = v[n2 + 8], d = v[n2 + 12];
+        dft4<INV>(a, b, c, d);
+        y[n2][0] = a; y[n2][1] = b; y[n2][2] = c; y[n2][3] = d;
+    }
+#pragma unroll
+    for (int n2 = 1; n2 < 4; ++n2)
+#pragma unroll
+        for (int k1 = 1; k1 < 4; ++k1)
+            y[n2][k1] = cmul(y[n2][k1], w16<T, INV>(n2 * k1));
+#pragma unroll
+    for (int k1 = 0; k1 < 4; ++k1) {
+        C a = y[0][k1], b = y[1][k1], c = y[2][k1], d = y[3][k1];
+        dft4<INV>(a, b, c, d);
+        v[k1] = a; v[k1 + 4] = b; v[k1 + 8] = c; v[k1 + 12] = d;
+    }
+}
+
+template <typename T, int R, bool INV>
+__device__ __forceinline__ void dft_r(vec2_t<T>* v)
+{
+    if constexpr (R == 2) dft2<INV>(v[0], v[1]);
+    else if constexpr (R == 4) dft4<INV>(v[0], v[1], v[2], v[3]);
+    else if constexpr (R == 8) dft8<T, INV>(v);
+    else dft16<T, INV>(v);
+}
+
+// One Stockham stage over the FFT held in `buf` (LDS, padded indexing).
+// t: this thread's index within the FFT's TPF threads.  tw: exp(-2 pi i m/L).
+template <typename T, int L, int R, int NS, bool INV>
+__device__ __forceinline__ void fft_stage(vec2_t<T>* buf, int t,
+                                          const vec2_t<T>* __restrict__ tw)
+{
+    using C = vec2_t<T>;
+    constexpr int E = fft_e(L);
+    constexpr int TPF = L / E;
+    constexpr int NB = E / R;
+    C v[NB][R];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int j = t + TPF * b;
+#pragma unroll
+        for (int r = 0; r < R; ++r) v[b][r] = buf[lds_pad(j + r * (L / R))];
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int j = t + TPF * b;
+        const int k = j % NS;
+        if constexpr (NS > 1) {
+#pragma unroll
+            for (int r = 1; r < R; ++r) {
+                C w = tw[r * k * (L / (NS * R))];
+                if (INV) w.y = -w.y;
+                v[b][r] = cmul(v[b][r], w);
+            }
+        }
+        dft_r<T, R, INV>(v[b]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int j = t + TPF * b;
+        const int k = j % NS;
+        const int base = (j / NS) * NS * R + k;
+#pragma unroll
+        for (int r = 0; r < R; ++r) buf[lds_pad(base + r * NS)] = v[b][r];
+    }
+    __syncthreads();
+}
+
+template <typename T, int L, int NS, bool INV>
+__device__ __forceinline__ void fft_stages(vec2_t<T>* buf, int t,
+                                           const vec2_t<T>* __restrict__ tw)
+{
+    if constexpr (NS < L) {
+        constexpr int REM = L / NS;
+        constexpr int R = REM >= 16 ? 16 : REM;
+        fft_stage<T, L, R, NS, INV>(buf, t, tw);
+        fft_stages<T, L, NS * R, INV>(buf, t, tw);
+    }
+}
+
+// Full in-place FFT; caller must __syncthreads() before (data in LDS).
+template <typename T, int L, bool INV>
+__device__ __forceinline__ void fft_lds(vec2_t<T>* buf, int t,
+                                        const vec2_t<T>* __restrict__ tw)
+{
+    fft_stages<T, L, 1, INV>(buf, t, tw);
+}
+
+}  // namespace dpep

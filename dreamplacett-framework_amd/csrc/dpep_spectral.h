@@ -1,0 +1,392 @@
+// dpep_spectral.h -- kernels of the DCT-based Poisson solve (three row passes).
+//
+// Maths (reference host/density_scatter_ttnn_server_host.cpp:124-181,
+// :251-263, :281-295):
+//   A  = C_M rho C_N^T,          C_K[k,n] = (2/K) cos(pi k (n+1/2) / K)
+//   fx = (2 S_M)(A . Wx) I_N^T,  fy = (2 I_M)(A . Wy) S_N^T
+//   phi = I_M (A / D) I_N^T      (potential; not in the reference)
+// with I_K[k,0] = 1, I_K[k,n>0] = 2 cos(pi n (k+1/2)/K),
+// S_K[k,n] = sin(pi n (k+1/2)/K), w_u = 2 pi u / M,
+// w_v = 2 pi v / N * bsx / bsy, D = w_u^2 + w_v^2, Wx = w_u / 2D,
+// Wy = w_v / 2D, and all weights zero at (0,0).
+//
+// Each 1-D transform is one complex FFT of length L on two packed real
+// lines (Makhoul's even/odd reordering):
+//   DCT-II:  z = v1 + i v2, Z = FFT(z), X[k] = Re(e^{-i pi k/2L} V[k]) with
+//            V1 = (Z[k] + conj Z[L-k]) / 2, V2 = -i (Z[k] - conj Z[L-k]) / 2,
+//            and X[L-k] = -Im(e^{-i pi k/2L} V[k]).
+//   I_K:     V[k] = e^{i pi k/2L} (X[k] - i X[L-k]), z = IFFT(V) (unscaled),
+//            y[2n] = z[n], y[2n+1] = z[L-1-n].
+//   S_K:     S(X)[n] = (-1)^n / 2 * I(X')[n], X'[k] = X[L-k], X'[0] = 0.
+// A thread owns the index pair {s, L-s} (s = 0 owns {0, L/2}) so the pre- and
+// post-processing never crosses threads.
+//
+// Passes and HBM traffic (MN = M*N elements):
+//   P1  k_row_dct : rho rows (along y)  -> T        tiled      read MN, write MN
+//   P2  k_col_pass: T rows (along x)    -> Ux,Uy,Up tiled      read MN, write 3MN
+//                   (DCT-II, weights, three inverse transforms; Up overwrites T)
+//   P3  k_row_inv : Ux,Uy,Up rows (y)   -> fx, fy, phi         read 3MN, write 3MN
+// Tiles of TX x TV elements (TX = rows of a P1 workgroup, TV = rows of a P2
+// workgroup) make every global access a run of >= 128 contiguous bytes while
+// P1 and P2 write "transposed" relative to the rows they process.
+#pragma once
+
+#include "dpep_internal.h"
+
+namespace dpep {
+
+template <typename T>
+__host__ __device__ constexpr int fpw(int L)
+{
+    return sizeof(T) == 4 ? (L <= 2048 ? 4 : 2) : 2;
+}
+
+template <typename T>
+__device__ __forceinline__ T& comp(vec2_t<T>& c, int which)
+{
+    return which ? c.y : c.x;
+}
+
+template <typename T>
+__device__ __forceinline__ T spectral_weight(int round, int u, int v,
+                                             const SpectralArgs& a)
+{
+    if (u == 0 && v == 0) return (T)0;
+    const T wu = (T)u * (T)a.wu_step;
+    const T wv = (T)v * (T)a.wv_step;
+    const T inv = (T)1 / (wu * wu + wv * wv);
+    if (round == 0) return wu * inv * (T)0.5;
+    if (round == 1) return wv * inv * (T)0.5;
+    return inv;
+}
+
+// Forward post-processing of slot s for two packed rows: returns X at k and m
+// (x component = first row, y = second row).
+template <typename T, int L>
+__device__ __forceinline__ void dct_post(const vec2_t<T>* buf, int s,
+                                         const vec2_t<T>* __restrict__ post,
+                                         T scale, vec2_t<T>& Xk,
+                                         vec2_t<T>& Xm)
+{
+    using C = vec2_t<T>;
+    if (s == 0) {
+        const C z0 = buf[0];
+        const C zh = buf[lds_pad(L / 2)];
+        const T c45 = post[L / 2].x;
+        Xk = C{z0.x * scale, z0.y * scale};
+        Xm = C{zh.x * c45 * scale, zh.y * c45 * scale};
+    } else {
+        const C za = buf[lds_pad(s)];
+        const C zb = buf[lds_pad(L - s)];
+        const C v1 = C{(T)0.5 * (za.x + zb.x), (T)0.5 * (za.y - zb.y)};
+        const C v2 = C{(T)0.5 * (za.y + zb.y), (T)-0.5 * (za.x - zb.x)};
+        const C tw = post[s];
+        const C w1 = cmul(tw, v1);
+        const C w2 = cmul(tw, v2);
+        Xk = C{w1.x * scale, w2.x * scale};
+        Xm = C{-w1.y * scale, -w2.y * scale};
+    }
+}
+
+// Inverse pre-processing of slot s for one real spectrum given X[k], X[m]
+// (k = s, m = L - s; for s = 0: k = 0, m = L/2).  rev selects X'[k] = X[L-k].
+template <typename T, int L>
+__device__ __forceinline__ void inv_pre(int s, T xk, T xm, bool rev,
+                                        const vec2_t<T>* __restrict__ post,
+                                        vec2_t<T>& Vk, vec2_t<T>& Vm)
+{
+    using C = vec2_t<T>;
+    if (s == 0) {
+        Vk = C{rev ? (T)0 : xk, (T)0};
+        const C c = post[L / 2];
+        // conj(c) * (xm - i xm)
+        Vm = C{c.x * xm - c.y * xm, -c.x * xm - c.y * xm};
+    } else {
+        const T a = rev ? xm : xk;
+        const T b = rev ? xk : xm;
+        const C c = post[s];
+        // conj(c) * (a - i b)
+        Vk = C{c.x * a - c.y * b, -c.x * b - c.y * a};
+        // i * c * (b - i a) = i*(c.x b + c.y a) + ... expand:
+        // c*(b - i a) = (c.x b + c.y a) + i (c.y b - c.x a); times i:
+        Vm = C{-(c.y * b - c.x * a), c.x * b + c.y * a};
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ vec2_t<T> pack2(vec2_t<T> v1, vec2_t<T> v2)
+{
+    // v1 + i v2
+    return vec2_t<T>{v1.x - v2.y, v1.y + v2.x};
+}
+
+// ---------------------------------------------------------------------------
+// P1: forward DCT-II along y of 2F rows of rho; writes T (tiled).
+// SRC 0: rho read from density_in.  SRC 1: rho = d0n + acc * 2^-36, also
+// written to density_out (deterministic accumulation).
+// ---------------------------------------------------------------------------
+template <typename T, int L, int F, int SRC>
+__global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_dct(
+    SpectralArgs a, const T* __restrict__ density_in,
+    const uint64_t* __restrict__ acc, const T* __restrict__ d0n,
+    T* __restrict__ density_out, T* __restrict__ Tt)
+{
+    using C = vec2_t<T>;
+    constexpr int E = fft_e(L), TPF = L / E, NT = F * TPF, LP = lds_len(L);
+    constexpr int TX = 2 * F;
+    extern __shared__ __align__(16) unsigned char smem[];
+    C* sb = reinterpret_cast<C*>(smem);
+    const int tid = threadIdx.x, f = tid / TPF, t = tid % TPF;
+    C* buf = sb + f * LP;
+    const int x0 = blockIdx.x * TX;
+    const size_t base = (size_t)x0 * L;
+
+#pragma unroll 4
+    for (int e = tid; e < TX * L; e += NT) {
+        const int r = e / L, m = e % L;
+        T val;
+        if constexpr (SRC == 0) {
+            val = density_in[base + e];
+        } else {
+            val = (T)((double)d0n[base + e] + (double)acc[base + e] * kFixInv);
+            density_out[base + e] = val;
+        }
+        comp<T>(sb[(r >> 1) * LP + lds_pad(makhoul_pos<L>(m))], r & 1) = val;
+    }
+    __syncthreads();
+    fft_lds<T, L, false>(buf, t, reinterpret_cast<const C*>(a.twN));
+
+    const C* post = reinterpret_cast<const C*>(a.postN);
+    const T scale = (T)2 / (T)L;
+    C Xk[E / 2], Xm[E / 2];
+#pragma unroll
+    for (int i = 0; i < E / 2; ++i)
+        dct_post<T, L>(buf, t + TPF * i, post, scale, Xk[i], Xm[i]);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < E / 2; ++i) {
+        const int s = t + TPF * i;
+        buf[lds_pad(s)] = Xk[i];
+        buf[lds_pad(s == 0 ? L / 2 : L - s)] = Xm[i];
+    }
+    __syncthreads();
+
+    const int TV = a.tiles.TV;
+    const int lgTV = __builtin_ctz(TV);
+    const int lgTE = __builtin_ctz(TX) + lgTV;
+    T* out = Tt + base;
+#pragma unroll 4
+    for (int e = tid; e < TX * L; e += NT) {
+        const int bv = e >> lgTE;
+        const int w = e & ((1 << lgTE) - 1);
+        const int x_in = w >> lgTV;
+        const int v = (bv << lgTV) + (w & (TV - 1));
+        out[e] = comp<T>(sb[(x_in >> 1) * LP + lds_pad(v)], x_in & 1);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// P2: per pair of v-rows of T: DCT-II along x, spectral weights, then the
+// three inverse transforms along x; writes Ux, Uy and Up (Up over T) tiled.
+// ---------------------------------------------------------------------------
+template <typename T, int L, int F>
+__global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
+    SpectralArgs a, T* __restrict__ Tt, T* __restrict__ Ux,
+    T* __restrict__ Uy)
+{
+    using C = vec2_t<T>;
+    constexpr int E = fft_e(L), TPF = L / E, NT = F * TPF, LP = lds_len(L);
+    constexpr int TV = 2 * F;
+    extern __shared__ __align__(16) unsigned char smem[];
+    C* sb = reinterpret_cast<C*>(smem);
+    const int tid = threadIdx.x, f = tid / TPF, t = tid % TPF;
+    C* buf = sb + f * LP;
+    const int TX = a.tiles.TX;
+    const int lgTX = __builtin_ctz(TX);
+    const int NBV = a.N / TV;
+    const int b2 = blockIdx.x;
+    const int v0 = b2 * TV;
+    constexpr int lgTV = __builtin_ctz(TV);
+    const int tile_elems = TX * TV;
+    const int lgTE = lgTX + lgTV;
+
+    // load the tiles (bx, b2) for every bx
+#pragma unroll 4
+    for (int e = tid; e < L * TV; e += NT) {
+        const int bx = e >> lgTE;
+        const int w = e & (tile_elems - 1);
+        const int x = (bx << lgTX) + (w >> lgTV);
+        const int v_in = w & (TV - 1);
+        const T val = Tt[((size_t)bx * NBV + b2) * tile_elems + w];
+        comp<T>(sb[(v_in >> 1) * LP + lds_pad(makhoul_pos<L>(x))], v_in & 1) = val;
+    }
+    __syncthreads();
+    fft_lds<T, L, false>(buf, t, reinterpret_cast<const C*>(a.twM));
+
+    const C* post = reinterpret_cast<const C*>(a.postM);
+    const T scale = (T)2 / (T)L;
+    C Ak[E / 2], Am[E / 2];
+#pragma unroll
+    for (int i = 0; i < E / 2; ++i)
+        dct_post<T, L>(buf, t + TPF * i, post, scale, Ak[i], Am[i]);
+
+    const int v1 = v0 + 2 * f, v2 = v1 + 1;
+    const int nrounds = a.potential ? 3 : 2;
+    for (int round = 0; round < nrounds; ++round) {
+        const bool rev = (round == 0);
+        C Vk[E / 2], Vm[E / 2];
+#pragma unroll
+        for (int i = 0; i < E / 2; ++i) {
+            const int s = t + TPF * i;
+            const int k = s, m = (s == 0) ? L / 2 : L - s;
+            const T b1k = Ak[i].x * spectral_weight<T>(round, k, v1, a);
+            const T b1m = Am[i].x * spectral_weight<T>(round, m, v1, a);
+            const T b2k = Ak[i].y * spectral_weight<T>(round, k, v2, a);
+            const T b2m = Am[i].y * spectral_weight<T>(round, m, v2, a);
+            C p1k, p1m, p2k, p2m;
+            inv_pre<T, L>(s, b1k, b1m, rev, post, p1k, p1m);
+            inv_pre<T, L>(s, b2k, b2m, rev, post, p2k, p2m);
+            Vk[i] = pack2<T>(p1k, p2k);
+            Vm[i] = pack2<T>(p1m, p2m);
+        }
+        __syncthreads();   // previous round's readers of buf are done
+#pragma unroll
+        for (int i = 0; i < E / 2; ++i) {
+            const int s = t + TPF * i;
+            buf[lds_pad(s)] = Vk[i];
+            buf[lds_pad(s == 0 ? L / 2 : L - s)] = Vm[i];
+        }
+        __syncthreads();
+        fft_lds<T, L, true>(buf, t, reinterpret_cast<const C*>(a.twM));
+
+        T* dst = round == 0 ? Ux : (round == 1 ? Uy : Tt);
+        const T rscale = round == 1 ? (T)2 : (T)1;
+#pragma unroll 4
+        for (int e = tid; e < L * TV; e += NT) {
+            const int bx = e >> lgTE;
+            const int w = e & (tile_elems - 1);
+            const int x = (bx << lgTX) + (w >> lgTV);
+            const int v_in = w & (TV - 1);
+            T val = comp<T>(sb[(v_in >> 1) * LP + lds_pad(makhoul_pos<L>(x))], v_in & 1);
+            val *= rscale;
+            if (round == 0 && (x & 1)) val = -val;
+            dst[((size_t)bx * NBV + b2) * tile_elems + w] = val;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// P3: inverse transforms along y.  Blocks [0, M/F): one row per FFT, packs
+// (Ux row, reversed Uy row) -> fx and fy.  Blocks [M/F, M/F + M/2F): two rows
+// of Up per FFT -> phi.
+// ---------------------------------------------------------------------------
+template <typename T, int L, int F>
+__global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_inv(
+    SpectralArgs a, const T* __restrict__ Ux, const T* __restrict__ Uy,
+    const T* __restrict__ Up, T* __restrict__ fx, T* __restrict__ fy,
+    T* __restrict__ phi)
+{
+    using C = vec2_t<T>;
+    constexpr int E = fft_e(L), TPF = L / E, NT = F * TPF, LP = lds_len(L);
+    constexpr int TX = 2 * F;
+    extern __shared__ __align__(16) unsigned char smem[];
+    C* sb = reinterpret_cast<C*>(smem);
+    const int tid = threadIdx.x, f = tid / TPF, t = tid % TPF;
+    C* buf = sb + f * LP;
+    const int TV = a.tiles.TV;
+    const int lgTV = __builtin_ctz(TV);
+    const int NBV = L / TV;
+    const int nA = a.M / F;
+    const C* post = reinterpret_cast<const C*>(a.postN);
+    const C* tw = reinterpret_cast<const C*>(a.twN);
+
+    if ((int)blockIdx.x < nA) {
+        const int ab = blockIdx.x;
+        const int x0 = ab * F;
+        const int bx = ab >> 1, half = ab & 1;
+        const int chunk = F * TV;
+        const int lgCH = __builtin_ctz(F) + lgTV;
+#pragma unroll 4
+        for (int e = tid; e < F * L; e += NT) {
+            const int bv = e >> lgCH;
+            const int w = e & (chunk - 1);
+            const int xr = w >> lgTV;
+            const int v = (bv << lgTV) + (w & (TV - 1));
+            const size_t g = ((size_t)bx * NBV + bv) * (TX * TV) + half * chunk + w;
+            sb[xr * LP + lds_pad(v)] = C{Ux[g], Uy[g]};
+        }
+        __syncthreads();
+        C Vk[E / 2], Vm[E / 2];
+#pragma unroll
+        for (int i = 0; i < E / 2; ++i) {
+            const int s = t + TPF * i;
+            const C zk = buf[lds_pad(s)];
+            const C zm = buf[lds_pad(s == 0 ? L / 2 : L - s)];
+            C pxk, pxm, pyk, pym;
+            inv_pre<T, L>(s, zk.x, zm.x, false, post, pxk, pxm);
+            inv_pre<T, L>(s, zk.y, zm.y, true, post, pyk, pym);
+            Vk[i] = pack2<T>(pxk, pyk);
+            Vm[i] = pack2<T>(pxm, pym);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < E / 2; ++i) {
+            const int s = t + TPF * i;
+            buf[lds_pad(s)] = Vk[i];
+            buf[lds_pad(s == 0 ? L / 2 : L - s)] = Vm[i];
+        }
+        __syncthreads();
+        fft_lds<T, L, true>(buf, t, tw);
+        const size_t base = (size_t)x0 * L;
+#pragma unroll 4
+        for (int e = tid; e < F * L; e += NT) {
+            const int xr = e / L, y = e % L;
+            const C z = sb[xr * LP + lds_pad(makhoul_pos<L>(y))];
+            fx[base + e] = z.x;
+            fy[base + e] = (y & 1) ? (T)-0.5 * z.y : (T)0.5 * z.y;
+        }
+    } else {
+        const int bb = blockIdx.x - nA;
+        const int x0 = bb * TX;
+        const size_t base = (size_t)x0 * L;
+        const int lgTE = __builtin_ctz(TX) + lgTV;
+#pragma unroll 4
+        for (int e = tid; e < TX * L; e += NT) {
+            const int bv = e >> lgTE;
+            const int w = e & ((1 << lgTE) - 1);
+            const int x_in = w >> lgTV;
+            const int v = (bv << lgTV) + (w & (TV - 1));
+            comp<T>(sb[(x_in >> 1) * LP + lds_pad(v)], x_in & 1) = Up[base + e];
+        }
+        __syncthreads();
+        C Vk[E / 2], Vm[E / 2];
+#pragma unroll
+        for (int i = 0; i < E / 2; ++i) {
+            const int s = t + TPF * i;
+            const C zk = buf[lds_pad(s)];
+            const C zm = buf[lds_pad(s == 0 ? L / 2 : L - s)];
+            C pak, pam, pbk, pbm;
+            inv_pre<T, L>(s, zk.x, zm.x, false, post, pak, pam);
+            inv_pre<T, L>(s, zk.y, zm.y, false, post, pbk, pbm);
+            Vk[i] = pack2<T>(pak, pbk);
+            Vm[i] = pack2<T>(pam, pbm);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < E / 2; ++i) {
+            const int s = t + TPF * i;
+            buf[lds_pad(s)] = Vk[i];
+            buf[lds_pad(s == 0 ? L / 2 : L - s)] = Vm[i];
+        }
+        __syncthreads();
+        fft_lds<T, L, true>(buf, t, tw);
+#pragma unroll 4
+        for (int e = tid; e < TX * L; e += NT) {
+            const int r = e / L, y = e % L;
+            const C z = sb[(r >> 1) * LP + lds_pad(makhoul_pos<L>(y))];
+            phi[base + e] = (r & 1) ? z.y : z.x;
+        }
+    }
+}
+
+}  // namespace dpep

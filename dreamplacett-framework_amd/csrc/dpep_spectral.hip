@@ -1,0 +1,156 @@
+// dpep_spectral.hip -- host launchers of the spectral passes (kernels in
+// dpep_spectral.h).
+#include "dpep_spectral.h"
+
+namespace dpep {
+
+int spectral_fpw(int L, int dtype)
+{
+    return dtype == 0 ? fpw<float>(L) : fpw<double>(L);
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch over the supported lengths.
+// ---------------------------------------------------------------------------
+template <typename T, int L>
+constexpr size_t lds_bytes()
+{
+    return (size_t)fpw<T>(L) * lds_len(L) * sizeof(vec2_t<T>);
+}
+
+template <typename T, int L>
+constexpr int threads_of()
+{
+    return fpw<T>(L) * (L / fft_e(L));
+}
+
+template <typename T, typename Fn>
+static hipError_t dispatch_len(int L, Fn&& fn)
+{
+    switch (L) {
+    case 8: return fn(std::integral_constant<int, 8>{});
+    case 16: return fn(std::integral_constant<int, 16>{});
+    case 32: return fn(std::integral_constant<int, 32>{});
+    case 64: return fn(std::integral_constant<int, 64>{});
+    case 128: return fn(std::integral_constant<int, 128>{});
+    case 256: return fn(std::integral_constant<int, 256>{});
+    case 512: return fn(std::integral_constant<int, 512>{});
+    case 1024: return fn(std::integral_constant<int, 1024>{});
+    case 2048: return fn(std::integral_constant<int, 2048>{});
+    case 4096: return fn(std::integral_constant<int, 4096>{});
+    case 8192:
+        if constexpr (sizeof(T) == 4) return fn(std::integral_constant<int, 8192>{});
+        else return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+    }
+}
+
+template <typename T>
+hipError_t launch_row_dct(const SpectralArgs& a, const T* density_in,
+                          const uint64_t* acc, const T* d0n, T* density_out,
+                          T* Tt, hipStream_t s)
+{
+    return dispatch_len<T>(a.N, [&](auto lc) -> hipError_t {
+        constexpr int L = decltype(lc)::value;
+        constexpr int F = fpw<T>(L);
+        const dim3 grid(a.M / (2 * F)), block(threads_of<T, L>());
+        if (acc)
+            k_row_dct<T, L, F, 1><<<grid, block, lds_bytes<T, L>(), s>>>(a, density_in, acc, d0n, density_out, Tt);
+        else
+            k_row_dct<T, L, F, 0><<<grid, block, lds_bytes<T, L>(), s>>>(a, density_in, acc, d0n, density_out, Tt);
+        return hipGetLastError();
+    });
+}
+
+template <typename T>
+hipError_t launch_col_pass(const SpectralArgs& a, T* Tt, T* Ux, T* Uy,
+                           hipStream_t s)
+{
+    return dispatch_len<T>(a.M, [&](auto lc) -> hipError_t {
+        constexpr int L = decltype(lc)::value;
+        constexpr int F = fpw<T>(L);
+        const dim3 grid(a.N / (2 * F)), block(threads_of<T, L>());
+        k_col_pass<T, L, F><<<grid, block, lds_bytes<T, L>(), s>>>(a, Tt, Ux, Uy);
+        return hipGetLastError();
+    });
+}
+
+template <typename T>
+hipError_t launch_row_inv(const SpectralArgs& a, const T* Ux, const T* Uy,
+                          const T* Up, T* fx, T* fy, T* phi, hipStream_t s)
+{
+    return dispatch_len<T>(a.N, [&](auto lc) -> hipError_t {
+        constexpr int L = decltype(lc)::value;
+        constexpr int F = fpw<T>(L);
+        const int nA = a.M / F;
+        const int nB = a.potential ? a.M / (2 * F) : 0;
+        const dim3 grid(nA + nB), block(threads_of<T, L>());
+        k_row_inv<T, L, F><<<grid, block, lds_bytes<T, L>(), s>>>(a, Ux, Uy, Up, fx, fy, phi);
+        return hipGetLastError();
+    });
+}
+
+template <typename T, int L>
+static hipError_t prepare_len()
+{
+    constexpr int F = fpw<T>(L);
+    const int bytes = (int)lds_bytes<T, L>();
+    hipError_t e;
+    if ((e = hipFuncSetAttribute((const void*)k_row_dct<T, L, F, 0>,
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, bytes)))
+        return e;
+    if ((e = hipFuncSetAttribute((const void*)k_row_dct<T, L, F, 1>,
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, bytes)))
+        return e;
+    if ((e = hipFuncSetAttribute((const void*)k_col_pass<T, L, F>,
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, bytes)))
+        return e;
+    return hipFuncSetAttribute((const void*)k_row_inv<T, L, F>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+}
+
+template <typename T>
+static hipError_t prepare_type()
+{
+    hipError_t e;
+    if ((e = prepare_len<T, 8>())) return e;
+    if ((e = prepare_len<T, 16>())) return e;
+    if ((e = prepare_len<T, 32>())) return e;
+    if ((e = prepare_len<T, 64>())) return e;
+    if ((e = prepare_len<T, 128>())) return e;
+    if ((e = prepare_len<T, 256>())) return e;
+    if ((e = prepare_len<T, 512>())) return e;
+    if ((e = prepare_len<T, 1024>())) return e;
+    if ((e = prepare_len<T, 2048>())) return e;
+    if ((e = prepare_len<T, 4096>())) return e;
+    if constexpr (sizeof(T) == 4)
+        if ((e = prepare_len<T, 8192>())) return e;
+    return hipSuccess;
+}
+
+hipError_t spectral_prepare()
+{
+    hipError_t e = prepare_type<float>();
+    if (e) return e;
+    return prepare_type<double>();
+}
+
+template hipError_t launch_row_dct<float>(const SpectralArgs&, const float*,
+                                          const uint64_t*, const float*,
+                                          float*, float*, hipStream_t);
+template hipError_t launch_row_dct<double>(const SpectralArgs&, const double*,
+                                           const uint64_t*, const double*,
+                                           double*, double*, hipStream_t);
+template hipError_t launch_col_pass<float>(const SpectralArgs&, float*, float*,
+                                           float*, hipStream_t);
+template hipError_t launch_col_pass<double>(const SpectralArgs&, double*,
+                                            double*, double*, hipStream_t);
+template hipError_t launch_row_inv<float>(const SpectralArgs&, const float*,
+                                          const float*, const float*, float*,
+                                          float*, float*, hipStream_t);
+template hipError_t launch_row_inv<double>(const SpectralArgs&, const double*,
+                                           const double*, const double*,
+                                           double*, double*, double*,
+                                           hipStream_t);
+
+}  // namespace dpep

@@ -1,0 +1,155 @@
+/*
+ * dpep.h -- C ABI of libdpep.so, the MI355X (gfx950) electric-potential step
+ * of DREAMPlace: cell-to-bin density scatter, DCT-based Poisson solve, field
+ * maps and the per-cell field gather.
+ *
+ * The ABI replaces the device side of the reference's shared-memory server
+ * (host/density_scatter_ttnn_server_host.cpp) with plain functions over plain
+ * pointers; the reference-side bindings a maintainer adds (ctypes for the
+ * Python client, the C++ server loop) are listed in INTEGRATION.md.
+ *
+ * Conventions
+ *   - Maps are x-major: map[bx * N + by], M = num_bins_x rows of N = num_bins_y
+ *     (the reference's density layout, kernels/v11_accum_dm.cpp:386-398).
+ *   - px, py are lower-left corners; sx, sy are the cells' original sizes
+ *     (integration/scatter_ttnn_client.py:628-649).  The library applies
+ *     DREAMPlace's small-cell stretch itself (sqrt2 * bin, ratio = area /
+ *     stretched area) unless DPEP_FLAG_NO_STRETCH is set.
+ *   - Cells with a non-finite coordinate or a non-positive size contribute
+ *     nothing and receive zero force (the reference's zero padding,
+ *     docs/DREAMPLACE_TT_INTEGRATION.md:233-241).
+ *   - Element type of every array is the context's dtype: float for
+ *     DPEP_DTYPE_F32, double for DPEP_DTYPE_F64.
+ *   - Every function returns DPEP_OK or an error code; dpep_last_error()
+ *     gives the text of the calling thread's last error.
+ *   - A context is not thread-safe: one in-flight step per context.
+ */
+#ifndef DPEP_H
+#define DPEP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DPEP_ABI_VERSION 1
+
+/* status codes */
+#define DPEP_OK 0
+#define DPEP_ERR_ARG 1          /* invalid argument (bad size, NULL, ...)   */
+#define DPEP_ERR_HIP 2          /* HIP runtime failure                      */
+#define DPEP_ERR_STATE 3        /* call out of order (e.g. no cells yet)    */
+#define DPEP_ERR_NOMEM 4        /* device or host allocation failed         */
+#define DPEP_ERR_UNSUPPORTED 5  /* grid shape outside the supported set     */
+
+/* element types */
+#define DPEP_DTYPE_F32 0
+#define DPEP_DTYPE_F64 1
+
+/* flags for dpep_create */
+#define DPEP_FLAG_DETERMINISTIC 0x1u /* int64 fixed-point bin accumulation:
+                                        run-to-run bitwise reproducible    */
+#define DPEP_FLAG_NO_POTENTIAL 0x2u  /* skip the potential map             */
+#define DPEP_FLAG_NO_STRETCH 0x4u    /* no sqrt2*bin stretch, ratio = 1
+                                        (the TT path's semantics,
+                                        scatter_ttnn_client.py:628-649)    */
+#define DPEP_FLAG_NO_GATHER 0x8u     /* skip the per-cell force gather     */
+
+/* timing slots, the reference's 9-float shm header order
+ * (integration/scatter_ttnn_client.py:151-163): h2d, scatter, gather,
+ * d2h_den, upload, compute, download, fw, total.  Here: scatter = density
+ * scatter kernels, gather = per-cell force gather, compute = spectral solve
+ * kernels, h2d = cell upload, d2h_den = density download, download = field /
+ * potential / force download, upload = initial-density upload (0 per step),
+ * fw = 0 (filled by the shm server), total = sum.  Milliseconds, measured
+ * with HIP events on the context's stream.                                 */
+#define DPEP_NUM_TIMINGS 9
+
+typedef struct dpep_ctx dpep_ctx;
+
+/* Library version and the gfx target it was built for. */
+int dpep_abi_version(void);
+const char* dpep_build_info(void);
+
+/* Text of the calling thread's last error ("" if none). */
+const char* dpep_last_error(void);
+
+/* Creates a context on the current HIP device: allocates every device buffer
+ * for nc_max cells and an M x N grid (no allocation happens per step),
+ * builds the twiddle tables and the stream.  M and N must be powers of two in
+ * [8, 8192].  Replaces the reference server's start-up: argument parsing
+ * (host/density_scatter_ttnn_server_host.cpp:324-339), device buffer set-up
+ * (:404-483) and TTNNDCTSolver::init (:236-269). */
+int dpep_create(int num_bins_x, int num_bins_y, int nc_max, double xl,
+                double yl, double xh, double yh, int dtype, unsigned flags,
+                dpep_ctx** out);
+
+/* Releases the context and its device memory. */
+int dpep_destroy(dpep_ctx* ctx);
+
+/* Uploads initial_density_map / bin_area (M*N elements, host memory), the
+ * fixed-cell density folded into every step's density.  Replaces shm slot 3
+ * (integration/scatter_ttnn_client.py:786-795) and the server's host fold
+ * (host/density_scatter_ttnn_server_host.cpp:1770-1777).  Until called the
+ * initial density is zero. */
+int dpep_set_initial_density(dpep_ctx* ctx, const void* d0n);
+
+/* Uploads nc <= nc_max cells (host memory) into the context's device
+ * buffers.  Replaces the server's H2D (:1335-1349). */
+int dpep_set_cells(dpep_ctx* ctx, const void* px, const void* py,
+                   const void* sx, const void* sy, int nc);
+
+/* Runs one step on the resident cells into the context's device outputs,
+ * asynchronously on the context's stream.  Replaces the scatter, accumulate,
+ * fold and TTNN solve of the server loop (:1629-1781). */
+int dpep_compute(dpep_ctx* ctx);
+
+/* Waits for the context's stream. */
+int dpep_sync(dpep_ctx* ctx);
+
+/* Copies the last step's outputs to host memory (waits first).  Any pointer
+ * may be NULL.  density, potential, field_x, field_y: M*N; grad_x, grad_y:
+ * nc (the per-cell gather ratio * sum tx*ty*field, sign left to the caller).
+ * Replaces the server's D2H and field write (:1678, :1785-1789). */
+int dpep_get_outputs(dpep_ctx* ctx, void* density, void* potential,
+                     void* field_x, void* field_y, void* grad_x,
+                     void* grad_y);
+
+/* set_cells + compute + get_outputs: one whole step on host buffers, the
+ * server loop body (:1326-1815). */
+int dpep_step(dpep_ctx* ctx, const void* px, const void* py, const void* sx,
+              const void* sy, int nc, void* field_x, void* field_y,
+              void* density, void* potential, void* grad_x, void* grad_y);
+
+/* One step on caller-owned device memory, asynchronous on `stream`
+ * (a hipStream_t; NULL = the context's stream).  Inputs px..sy hold nc
+ * cells.  Outputs may be NULL, in which case they land in the context's own
+ * buffers.  No counterpart in the reference (its positions always crossed
+ * PCIe); it is the zero-copy entry point for callers already on the GPU. */
+int dpep_step_device(dpep_ctx* ctx, const void* d_px, const void* d_py,
+                     const void* d_sx, const void* d_sy, int nc,
+                     void* d_field_x, void* d_field_y, void* d_density,
+                     void* d_potential, void* d_grad_x, void* d_grad_y,
+                     void* stream);
+
+/* Per-stage milliseconds of the last step (DPEP_NUM_TIMINGS floats), the
+ * values the reference server wrote into the shm header (:1798-1808). */
+int dpep_get_timings(dpep_ctx* ctx, float* out);
+
+/* Per-kernel average durations of the last step in microseconds, measured
+ * with HIP events around each launch on the context's stream:
+ * [0] init, [1] scatter, [2] row DCT, [3] column DCT + inverse,
+ * [4] row inverse, [5] gather.  n = number of floats in out (<= 8). */
+int dpep_get_kernel_times(dpep_ctx* ctx, float* out, int n);
+
+/* Enables (1) or disables (0) per-kernel event timing (adds events between
+ * launches; off by default). */
+int dpep_set_profiling(dpep_ctx* ctx, int enable);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DPEP_H */

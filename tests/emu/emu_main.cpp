@@ -1,0 +1,186 @@
+// CPU emulation of one electric-potential step with libdpep's kernel source
+// (csrc/dpep_scatter.h, csrc/dpep_spectral.h) under AddressSanitizer.
+// Every global buffer is malloc'd at its exact size and the LDS tail beyond
+// the launch's dynamic size is poisoned, so any out-of-bounds index aborts
+// with a report.  Results are compared with the float64 oracle.
+// Usage: emu_main <f32|f64> M N ncells [det] [nopot]
+#include <sanitizer/asan_interface.h>
+#include <stdio.h>
+#include <stdlib.h>
+
+#include <functional>
+#include <random>
+#include <thread>
+#include <vector>
+
+#include "dpep_scatter.h"
+#include "dpep_spectral.h"
+
+thread_local dim3 threadIdx, blockIdx;
+dim3 blockDim, gridDim;
+std::barrier<>* emu_barrier = nullptr;
+namespace dpep {
+alignas(16) unsigned char smem[163840];
+int spectral_fpw(int L, int dtype) { return dtype == 0 ? fpw<float>(L) : fpw<double>(L); }
+}
+
+extern "C" {
+int oracle_density(const double*, const double*, const double*, const double*, long, int, int,
+                   double, double, double, double, int, const double*, double*);
+int oracle_solve_fft(const double*, int, int, double, double, double*, double*, double*);
+int oracle_gather(const double*, const double*, const double*, const double*, long, int, int,
+                  double, double, double, double, int, const double*, const double*, double*,
+                  double*);
+}
+
+static void launch(unsigned grid, unsigned block, size_t shm, const std::function<void()>& body)
+{
+    blockDim = dim3(block);
+    gridDim = dim3(grid);
+    if (shm > sizeof(dpep::smem)) { fprintf(stderr, "LDS %zu too big\n", shm); abort(); }
+    for (unsigned b = 0; b < grid; ++b) {
+        ASAN_UNPOISON_MEMORY_REGION(dpep::smem, sizeof(dpep::smem));
+        memset(dpep::smem, 0xA5, sizeof(dpep::smem));
+        ASAN_POISON_MEMORY_REGION(dpep::smem + shm, sizeof(dpep::smem) - shm);
+        std::barrier<> bar(block);
+        emu_barrier = &bar;
+        std::vector<std::thread> ts;
+        ts.reserve(block);
+        for (unsigned t = 0; t < block; ++t)
+            ts.emplace_back([&, t, b] { threadIdx = dim3(t); blockIdx = dim3(b); body(); });
+        for (auto& th : ts) th.join();
+    }
+    ASAN_UNPOISON_MEMORY_REGION(dpep::smem, sizeof(dpep::smem));
+}
+
+template <typename T>
+static T* exact(size_t n) { return (T*)malloc(n * sizeof(T) + (n == 0)); }
+
+template <typename T>
+static std::vector<T> table(int L, bool post)
+{
+    const int n = post ? L / 2 + 1 : L;
+    std::vector<T> v(2 * (size_t)n);
+    for (int m = 0; m < n; ++m) {
+        const double a = post ? M_PI * m / (2.0 * L) : 2.0 * M_PI * m / L;
+        v[2 * m] = (T)cos(a);
+        v[2 * m + 1] = (T)-sin(a);
+    }
+    return v;
+}
+
+template <typename T, int LM, int LN>
+static int run(int nc, bool det, bool pot)
+{
+    using namespace dpep;
+    const int M = LM, N = LN;
+    const size_t mn = (size_t)M * N;
+    const double xl = 0, yl = 0, xh = 100.0 * M / 8, yh = 80.0 * N / 8;
+    Grid g{};
+    g.M = M; g.N = N; g.xl = xl; g.yl = yl; g.xh = xh; g.yh = yh;
+    g.bsx = (xh - xl) / M; g.bsy = (yh - yl) / N; g.inv_ba = 1.0 / (g.bsx * g.bsy);
+    g.minw = M_SQRT2 * g.bsx; g.minh = M_SQRT2 * g.bsy; g.stretch = 1;
+    std::mt19937_64 rng(1234);
+    std::uniform_real_distribution<double> U(0, 1);
+    T* px = exact<T>(nc); T* py = exact<T>(nc); T* sx = exact<T>(nc); T* sy = exact<T>(nc);
+    for (int i = 0; i < nc; ++i) {
+        sx[i] = (T)(g.bsx * (0.3 + 3 * U(rng)));
+        sy[i] = (T)(g.bsy * (0.3 + 2 * U(rng)));
+        px[i] = (T)(xl + (xh - xl) * (1.1 * U(rng) - 0.05));   // some outside the die
+        py[i] = (T)(yl + (yh - yl) * (1.1 * U(rng) - 0.05));
+    }
+    if (nc > 2) { sx[0] = 0; sy[1] = -1; sx[2] = (T)(3 * (xh - xl)); px[2] = (T)(xl - (xh - xl)); }
+    T* d0n = exact<T>(mn); T* dens = exact<T>(mn); T* phi = pot ? exact<T>(mn) : nullptr;
+    T* fx = exact<T>(mn); T* fy = exact<T>(mn); T* Tt = exact<T>(mn); T* Ux = exact<T>(mn);
+    T* Uy = exact<T>(mn); T* gx = exact<T>(nc); T* gy = exact<T>(nc);
+    uint64_t* acc = det ? exact<uint64_t>(mn) : nullptr;
+    for (size_t i = 0; i < mn; ++i) d0n[i] = (T)(0.5 * U(rng));
+    auto twM = table<T>(M, false), twN = table<T>(N, false);
+    auto poM = table<T>(M, true), poN = table<T>(N, true);
+    T* d_twM = exact<T>(twM.size()); memcpy(d_twM, twM.data(), twM.size() * sizeof(T));
+    T* d_twN = exact<T>(twN.size()); memcpy(d_twN, twN.data(), twN.size() * sizeof(T));
+    T* d_poM = exact<T>(poM.size()); memcpy(d_poM, poM.data(), poM.size() * sizeof(T));
+    T* d_poN = exact<T>(poN.size()); memcpy(d_poN, poN.data(), poN.size() * sizeof(T));
+    SpectralArgs a{};
+    a.M = M; a.N = N;
+    a.tiles.TX = 2 * fpw<T>(N); a.tiles.TV = 2 * fpw<T>(M);
+    a.wu_step = 2 * M_PI / M; a.wv_step = 2 * M_PI / N * (g.bsx / g.bsy);
+    a.potential = pot; a.twM = d_twM; a.postM = d_poM; a.twN = d_twN; a.postN = d_poN;
+
+    const unsigned ib = (unsigned)((mn + 255) / 256);
+    launch(ib < 8192 ? ib : 8192, 256, 0, [&] { k_init<T>(d0n, dens, acc, mn); });
+    if (nc > 0) {
+        if (det) launch((nc + 255) / 256, 256, 0, [&] { k_scatter<T, true>(px, py, sx, sy, nc, g, dens, acc); });
+        else launch((nc + 255) / 256, 256, 0, [&] { k_scatter<T, false>(px, py, sx, sy, nc, g, dens, acc); });
+    }
+    {
+        constexpr int F = fpw<T>(LN);
+        const size_t shm = (size_t)F * lds_len(LN) * sizeof(vec2_t<T>);
+        const unsigned nt = F * (LN / fft_e(LN));
+        if (det) launch(M / (2 * F), nt, shm, [&] { k_row_dct<T, LN, F, 1>(a, dens, acc, d0n, dens, Tt); });
+        else launch(M / (2 * F), nt, shm, [&] { k_row_dct<T, LN, F, 0>(a, dens, acc, d0n, dens, Tt); });
+    }
+    {
+        constexpr int F = fpw<T>(LM);
+        const size_t shm = (size_t)F * lds_len(LM) * sizeof(vec2_t<T>);
+        launch(N / (2 * F), F * (LM / fft_e(LM)), shm, [&] { k_col_pass<T, LM, F>(a, Tt, Ux, Uy); });
+    }
+    {
+        constexpr int F = fpw<T>(LN);
+        const size_t shm = (size_t)F * lds_len(LN) * sizeof(vec2_t<T>);
+        const unsigned grid = M / F + (pot ? M / (2 * F) : 0);
+        launch(grid, F * (LN / fft_e(LN)), shm, [&] { k_row_inv<T, LN, F>(a, Ux, Uy, Tt, fx, fy, phi); });
+    }
+    if (nc > 0)
+        launch((nc + 255) / 256, 256, 0, [&] { k_gather<T>(px, py, sx, sy, nc, g, fx, fy, gx, gy); });
+
+    // oracle
+    std::vector<double> dpx(nc), dpy(nc), dsx(nc), dsy(nc), dd0(mn), rho(mn), rphi(mn), rfx(mn), rfy(mn), rgx(nc), rgy(nc);
+    for (int i = 0; i < nc; ++i) { dpx[i] = px[i]; dpy[i] = py[i]; dsx[i] = sx[i]; dsy[i] = sy[i]; }
+    for (size_t i = 0; i < mn; ++i) dd0[i] = d0n[i];
+    oracle_density(dpx.data(), dpy.data(), dsx.data(), dsy.data(), nc, M, N, xl, yl, xh, yh, 1, dd0.data(), rho.data());
+    oracle_solve_fft(rho.data(), M, N, g.bsx, g.bsy, rphi.data(), rfx.data(), rfy.data());
+    oracle_gather(dpx.data(), dpy.data(), dsx.data(), dsy.data(), nc, M, N, xl, yl, xh, yh, 1, rfx.data(), rfy.data(), rgx.data(), rgy.data());
+    auto linf = [](const T* x, const double* r, size_t n) {
+        double m = 0, d = 0;
+        for (size_t i = 0; i < n; ++i) { m = fmax(m, fabs(r[i])); d = fmax(d, fabs((double)x[i] - r[i])); }
+        return d / (m > 0 ? m : 1);
+    };
+    auto l2 = [](const T* x, const double* r, size_t n) {
+        double m = 0, d = 0;
+        for (size_t i = 0; i < n; ++i) { m += r[i] * r[i]; d += ((double)x[i] - r[i]) * ((double)x[i] - r[i]); }
+        return sqrt(d) / (m > 0 ? sqrt(m) : 1);
+    };
+    const double e_d = linf(dens, rho.data(), mn), e_p = pot ? linf(phi, rphi.data(), mn) : 0.0;
+    const double e_fx = l2(fx, rfx.data(), mn), e_fy = l2(fy, rfy.data(), mn);
+    const double e_gx = nc ? l2(gx, rgx.data(), nc) : 0.0, e_gy = nc ? l2(gy, rgy.data(), nc) : 0.0;
+    printf("emu %s M=%d N=%d nc=%d det=%d pot=%d: density %.2e potential %.2e fx %.2e fy %.2e gx %.2e gy %.2e\n",
+           sizeof(T) == 4 ? "f32" : "f64", M, N, nc, det, pot, e_d, e_p, e_fx, e_fy, e_gx, e_gy);
+    const double tl = sizeof(T) == 4 ? 1e-5 : 1e-11, tf = sizeof(T) == 4 ? 1e-4 : 1e-10;
+    const bool ok = e_d <= tl && e_p <= tl && e_fx <= tf && e_fy <= tf && e_gx <= tf && e_gy <= tf;
+    return ok ? 0 : 3;
+}
+
+template <typename T>
+static int dispatch(int M, int N, int nc, bool det, bool pot)
+{
+#define CASE(a, b) if (M == a && N == b) return run<T, a, b>(nc, det, pot);
+    CASE(8, 8) CASE(16, 16) CASE(8, 32) CASE(32, 8) CASE(64, 64) CASE(16, 128) CASE(128, 16)
+    CASE(256, 256) CASE(512, 512) CASE(64, 2048) CASE(2048, 64) CASE(16, 4096) CASE(4096, 16)
+#undef CASE
+    fprintf(stderr, "unsupported shape\n");
+    return 2;
+}
+
+int main(int argc, char** argv)
+{
+    if (argc < 5) { fprintf(stderr, "usage: %s f32|f64 M N nc [det] [nopot]\n", argv[0]); return 2; }
+    const bool f64 = !strcmp(argv[1], "f64");
+    const int M = atoi(argv[2]), N = atoi(argv[3]), nc = atoi(argv[4]);
+    bool det = false, pot = true;
+    for (int i = 5; i < argc; ++i) {
+        if (!strcmp(argv[i], "det")) det = true;
+        if (!strcmp(argv[i], "nopot")) pot = false;
+    }
+    return f64 ? dispatch<double>(M, N, nc, det, pot) : dispatch<float>(M, N, nc, det, pot);
+}

@@ -1,0 +1,57 @@
+// Host stand-in for <hip/hip_runtime.h>, used ONLY by tests/emu: it lets the
+// kernel headers of libdpep (csrc/dpep_*.h) compile as plain C++ so the test
+// can run every kernel on the CPU -- one std::thread per GPU thread, a
+// std::barrier per __syncthreads -- under AddressSanitizer with exact-size
+// buffers.  It is a bounds and logic checker for the kernel source, not an
+// execution path of the product.
+#pragma once
+#include <atomic>
+#include <barrier>
+#include <cmath>
+#include <cstddef>
+#include <cstdint>
+#include <cstring>
+#include <type_traits>
+#include <utility>
+
+#define __global__
+#define __device__
+#define __host__
+#define __forceinline__ inline
+#define __launch_bounds__(...)
+#define __shared__
+#define __align__(n) __attribute__((aligned(n)))
+
+struct dim3 {
+    unsigned x = 1, y = 1, z = 1;
+    dim3() = default;
+    dim3(unsigned a, unsigned b = 1, unsigned c = 1) : x(a), y(b), z(c) {}
+};
+struct float2 { float x, y; };
+struct double2 { double x, y; };
+
+extern thread_local dim3 threadIdx, blockIdx;
+extern dim3 blockDim, gridDim;
+extern std::barrier<>* emu_barrier;
+inline void __syncthreads() { emu_barrier->arrive_and_wait(); }
+
+using std::floor;
+using std::isfinite;
+
+inline unsigned long long __double2ull_rn(double x)
+{
+    return (unsigned long long)std::nearbyint(x);
+}
+template <class T>
+inline T unsafeAtomicAdd(T* p, T v)
+{
+    std::atomic_ref<T> r(*p);
+    return r.fetch_add(v);
+}
+inline unsigned long long atomicAdd(unsigned long long* p, unsigned long long v)
+{
+    return __atomic_fetch_add(p, v, __ATOMIC_RELAXED);
+}
+
+typedef int hipError_t;
+typedef void* hipStream_t;
