@@ -1,0 +1,193 @@
+#!/usr/bin/env python3
+"""bench.py -- ms per electric-potential step (scatter + DCT solve + field
+maps + per-cell field gather) on one MI355X, with the HBM roofline of the
+dominant kernel and the CPU baseline timed on the same host.
+
+    python bench.py [--steps K] [--warmup W] [--config 3]
+
+Workload (default): 1.1M movable cells (lognormal widths, height 12), 1300
+macros folded into the fixed density, die 27000 x 27000, 2048 x 2048 bins,
+80 % uniform + 20 % in four Gaussian clusters, seed 0 -- synthetic data of
+the benchmark's shape.  Cell arrays and the fixed density are resident in
+HBM before the timed region; one step = one dpep_compute() on them.
+
+Prints ONE JSON line (the driver's contract).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "dreamplacett-framework_amd")
+ORACLE = os.path.join(ROOT, "oracle")
+for _p in (PKG, ORACLE):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
+METRIC = ("ms per potential step (scatter+DCT+field), 1.1M cells @2048^2; "
+          "% HBM peak")
+
+
+def kernel_bytes(nc, M, N, esz, potential=True):
+    """Algorithmic bytes per launch of each kernel (the minimum each must
+    move given its inputs and outputs)."""
+    mn = M * N
+    nmaps = 3 if potential else 2
+    return {
+        "init": 2 * esz * mn,                          # read D0, write rho
+        "scatter": 4 * esz * nc + esz * mn,            # read cells, write rho
+        "row_dct": 2 * esz * mn,                       # read rho, write T
+        "col_pass": (1 + nmaps) * esz * mn,            # read T, write U*
+        "row_inv": 2 * nmaps * esz * mn,               # read U*, write maps
+        "gather": 6 * esz * nc + 2 * esz * mn,         # cells, fields, forces
+    }
+
+
+def step_bytes(nc, M, N, esz, potential=True):
+    """The step's byte model: 10 e Nc + 16 e MN (e = element size), i.e.
+    40 Nc + 64 MN at float32; 12 e MN less without the potential."""
+    return 10 * esz * nc + (16 if potential else 13) * esz * M * N
+
+
+def cpu_baseline(w, seconds, max_steps=20):
+    import pyoracle
+    cb = pyoracle.CpuBaseline(w.M, w.N, w.xl, w.yl, w.xh, w.yh)
+    px, py, sx, sy = w.cells(np.float32)
+    d0 = w.d0n.astype(np.float32)
+    cb.step(px, py, sx, sy, d0)                     # warm-up
+    times, stages = [], []
+    t_start = time.perf_counter()
+    while len(times) < max_steps and (time.perf_counter() - t_start) < seconds:
+        t0 = time.perf_counter()
+        r = cb.step(px, py, sx, sy, d0)
+        times.append((time.perf_counter() - t0) * 1e3)
+        stages.append(r["stage_ms"])
+    cb.close()
+    med = float(np.median(times))
+    st = {k: float(np.median([s[k] for s in stages])) for k in stages[0]}
+    return {
+        "value": round(med, 3),
+        "unit": "ms per step",
+        "cores": pyoracle.CpuBaseline.threads(),
+        "kind": "port",
+        "sample": (f"{len(times)} full steps of the same workload "
+                   f"({w.nc} cells, {w.M}x{w.N}) after 1 warm-up, median; "
+                   f"float32 OpenMP scatter + FFT DCT + gather"),
+        "stage_ms": {k: round(v, 3) for k, v in st.items()},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__,
+                                 formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--dtype", choices=["f32", "f64"], default="f32")
+    ap.add_argument("--deterministic", action="store_true")
+    ap.add_argument("--no-potential", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="wall-clock budget of the CPU-baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-profile", action="store_true",
+                    help="skip the per-kernel event pass (for rocprofv3 runs)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures one GPU only (the step's "
+              "multi-GPU sharding is a design, not an implementation); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import dpep
+    from dpep import workloads
+
+    t0 = time.perf_counter()
+    w = workloads.make(args.config, seed=0)
+    gen_s = time.perf_counter() - t0
+    dtype = np.float32 if args.dtype == "f32" else np.float64
+    esz = np.dtype(dtype).itemsize
+    potential = not args.no_potential
+    px, py, sx, sy = w.cells(dtype)
+
+    ctx = dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh, dtype=dtype,
+                       deterministic=args.deterministic, potential=potential)
+    ctx.set_initial_density(w.d0n.astype(dtype))
+    ctx.set_cells(px, py, sx, sy)          # inputs resident in HBM from here
+    for _ in range(args.warmup):
+        ctx.compute()
+    ctx.sync()
+
+    # timed region: exactly K steps, synchronised on both sides
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ctx.compute()
+    ctx.sync()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    kt = None
+    if not args.no_profile:
+        # same K steps again with HIP events between launches on the
+        # context's stream: per-kernel average durations
+        ctx.set_profiling(args.steps)
+        for _ in range(args.steps):
+            ctx.compute()
+        ctx.sync()
+        kt = ctx.kernel_times_us()
+        ctx.set_profiling(0)
+    ctx.close()
+
+    bstep = step_bytes(w.nc, w.M, w.N, esz, potential)
+    kb = kernel_bytes(w.nc, w.M, w.N, esz, potential)
+    roof = None
+    if kt:
+        dom = max((k for k in kb), key=lambda k: kt[k])
+        ach = kb[dom] / (kt[dom] * 1e-6)
+        roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach / 1e9, 1),
+                "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK, 4), "traffic": None,
+                "algorithmic_bytes": kb[dom], "avg_us": round(kt[dom], 2)}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(w, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": round(ms, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64" if dtype == np.float64 else "f32",
+        "data": "synthetic (seeded placement of the benchmark's shape)",
+        "config": {
+            "workload": f"{w.name}: {w.nc} cells, {w.meta.get('macros', 0)} macros, "
+                        f"die {w.xh:g}x{w.yh:g}, {w.M}x{w.N} bins",
+            "cells": w.nc, "bins_x": w.M, "bins_y": w.N,
+            "deterministic": bool(args.deterministic), "potential": potential,
+            "gather": True,
+        },
+        "hbm_fraction_step": round(bstep / (ms * 1e-3) / HBM_PEAK, 4),
+        "step_bytes": bstep,
+        "roofline": roof,
+        "kernel_us": {k: round(v, 2) for k, v in kt.items()} if kt else None,
+        "cpu_baseline": cpu,
+        "workload_gen_s": round(gen_s, 2),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

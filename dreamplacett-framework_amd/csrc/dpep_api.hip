@@ -72,7 +72,11 @@ struct dpep_ctx {
     hipStream_t stream = nullptr;
     hipEvent_t ev[kNumStages + 1] = {};
     hipEvent_t ev_x0 = nullptr, ev_x1 = nullptr;
+    // per-kernel profiling: a ring of `prof_slots` event sets, one per step
+    std::vector<hipEvent_t> prof_ev;   // prof_slots * (kNumStages + 1)
     int profiling = 0;
+    int prof_slots = 0;
+    long prof_steps = 0;               // steps recorded since enabling
     int nc = -1;                 // resident cells (-1: none uploaded)
     int last_nc = 0;             // cells of the last computed step
     int stepped = 0;
@@ -142,6 +146,9 @@ static void release(dpep_ctx* c)
         if (p) (void)hipFree(p);
     for (auto& e : c->ev)
         if (e) (void)hipEventDestroy(e);
+    for (auto& e : c->prof_ev)
+        if (e) (void)hipEventDestroy(e);
+    c->prof_ev.clear();
     if (c->ev_x0) (void)hipEventDestroy(c->ev_x0);
     if (c->ev_x1) (void)hipEventDestroy(c->ev_x1);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -168,21 +175,28 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
         (nc > 0 && gather && (!gx || !gy)))
         return fail(DPEP_ERR_STATE, "internal: a kernel argument is NULL");
 
+    // with profiling on, this step's stage boundaries go to ring slot `ps`
+    hipEvent_t* pe = prof ? &c->prof_ev[(size_t)(c->prof_steps % c->prof_slots) *
+                                         (kNumStages + 1)]
+                          : nullptr;
     HIP_TRY(hipEventRecord(c->ev[0], s));
+    if (prof) HIP_TRY(hipEventRecord(pe[0], s));
     HIP_TRY(launch_fill_init<T>(d0n, dens, acc, mn, s));
-    if (prof) HIP_TRY(hipEventRecord(c->ev[1], s));
+    if (prof) HIP_TRY(hipEventRecord(pe[1], s));
     HIP_TRY(launch_scatter<T>(px, py, sx, sy, nc, c->grid, dens, acc, s));
-    if (prof) HIP_TRY(hipEventRecord(c->ev[2], s));
+    if (prof) HIP_TRY(hipEventRecord(pe[2], s));
     HIP_TRY(launch_row_dct<T>(c->sargs, dens, acc, d0n, dens, (T*)c->d_T, s));
-    if (prof) HIP_TRY(hipEventRecord(c->ev[3], s));
+    if (prof) HIP_TRY(hipEventRecord(pe[3], s));
     HIP_TRY(launch_col_pass<T>(c->sargs, (T*)c->d_T, (T*)c->d_Ux, (T*)c->d_Uy, s));
-    if (prof) HIP_TRY(hipEventRecord(c->ev[4], s));
+    if (prof) HIP_TRY(hipEventRecord(pe[4], s));
     HIP_TRY(launch_row_inv<T>(c->sargs, (const T*)c->d_Ux, (const T*)c->d_Uy,
                               (const T*)c->d_T, fx, fy, phi, s));
-    if (prof) HIP_TRY(hipEventRecord(c->ev[5], s));
+    if (prof) HIP_TRY(hipEventRecord(pe[5], s));
     if (gather)
         HIP_TRY(launch_gather<T>(px, py, sx, sy, nc, c->grid, fx, fy, gx, gy, s));
+    if (prof) HIP_TRY(hipEventRecord(pe[kNumStages], s));
     HIP_TRY(hipEventRecord(c->ev[kNumStages], s));
+    if (prof) c->prof_steps++;
     c->last_nc = nc;
     c->stepped = 1;
     return DPEP_OK;
@@ -271,6 +285,7 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
     g.minw = M_SQRT2 * g.bsx;
     g.minh = M_SQRT2 * g.bsy;
     g.stretch = (flags & DPEP_FLAG_NO_STRETCH) ? 0 : 1;
+    g.fix_scale = ldexp(1.0, fix_exponent(nc_max));
 
     SpectralArgs& a = c->sargs;
     a.M = M; a.N = N;
@@ -279,6 +294,7 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
     a.wu_step = 2.0 * M_PI / M;
     a.wv_step = 2.0 * M_PI / N * (g.bsx / g.bsy);
     a.potential = (flags & DPEP_FLAG_NO_POTENTIAL) ? 0 : 1;
+    a.fix_inv = 1.0 / g.fix_scale;
 
     int rc = DPEP_OK;
     auto step = [&]() -> int {
@@ -435,10 +451,12 @@ int dpep_get_timings(dpep_ctx* c, float* out)
     for (int i = 0; i < DPEP_NUM_TIMINGS; ++i) out[i] = 0.f;
     const float total = elapsed(c->ev[0], c->ev[kNumStages]);
     out[0] = c->h2d_ms;
-    if (c->profiling) {
-        out[1] = elapsed(c->ev[0], c->ev[2]);              // init + scatter
-        out[5] = elapsed(c->ev[2], c->ev[5]);              // P1 + P2 + P3
-        out[2] = elapsed(c->ev[5], c->ev[kNumStages]);     // gather
+    if (c->profiling && c->prof_steps > 0) {
+        const hipEvent_t* pe = &c->prof_ev[(size_t)((c->prof_steps - 1) % c->prof_slots) *
+                                           (kNumStages + 1)];
+        out[1] = elapsed(pe[0], pe[2]);              // init + scatter
+        out[5] = elapsed(pe[2], pe[5]);              // P1 + P2 + P3
+        out[2] = elapsed(pe[5], pe[kNumStages]);     // gather
     } else {
         out[5] = total;
     }
@@ -453,19 +471,39 @@ int dpep_get_kernel_times(dpep_ctx* c, float* out, int n)
     if (int rc = check_ctx(c)) return rc;
     if (!out || n < 0) return fail(DPEP_ERR_ARG, "bad output buffer");
     if (!c->stepped) return fail(DPEP_ERR_STATE, "no step has been computed");
-    if (!c->profiling)
-        return fail(DPEP_ERR_STATE, "per-kernel times need dpep_set_profiling(ctx, 1)");
+    if (!c->profiling || c->prof_steps == 0)
+        return fail(DPEP_ERR_STATE,
+                    "no profiled step: call dpep_set_profiling(ctx, slots) first");
     HIP_TRY(hipEventSynchronize(c->ev[kNumStages]));
     for (int i = 0; i < n; ++i) out[i] = 0.f;
-    for (int i = 0; i < kNumStages && i < n; ++i)
-        out[i] = 1000.f * elapsed(c->ev[i], c->ev[i + 1]);
+    const long steps = c->prof_steps < c->prof_slots ? c->prof_steps : c->prof_slots;
+    for (long k = 0; k < steps; ++k) {
+        const hipEvent_t* pe = &c->prof_ev[(size_t)k * (kNumStages + 1)];
+        for (int i = 0; i < kNumStages && i < n; ++i)
+            out[i] += 1000.f * elapsed(pe[i], pe[i + 1]);
+        if (n > kNumStages) out[kNumStages] += 1000.f * elapsed(pe[0], pe[kNumStages]);
+    }
+    for (int i = 0; i < n && i <= kNumStages; ++i) out[i] /= (float)steps;
     return DPEP_OK;
 }
 
-int dpep_set_profiling(dpep_ctx* c, int enable)
+int dpep_set_profiling(dpep_ctx* c, int slots)
 {
     if (int rc = check_ctx(c)) return rc;
-    c->profiling = enable ? 1 : 0;
+    if (slots < 0 || slots > 65536)
+        return fail(DPEP_ERR_ARG, "slots=%d outside [0, 65536]", slots);
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    for (auto& e : c->prof_ev)
+        if (e) (void)hipEventDestroy(e);
+    c->prof_ev.clear();
+    c->profiling = 0;
+    c->prof_slots = 0;
+    c->prof_steps = 0;
+    if (slots == 0) return DPEP_OK;
+    c->prof_ev.assign((size_t)slots * (kNumStages + 1), nullptr);
+    for (auto& e : c->prof_ev) HIP_TRY(hipEventCreate(&e));
+    c->prof_slots = slots;
+    c->profiling = 1;
     return DPEP_OK;
 }
 

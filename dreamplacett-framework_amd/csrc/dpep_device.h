@@ -17,14 +17,22 @@ struct Grid {
     double bsx, bsy;          // bin sizes
     double inv_ba;            // 1 / (bsx * bsy)
     double minw, minh;        // sqrt2 * bsx, sqrt2 * bsy (stretch floor)
+    double fix_scale;         // 2^fix_exponent(nc_max) (deterministic mode)
     int stretch;              // 1: DREAMPlace small-cell stretch
 };
 
-// Fixed-point scale of the deterministic accumulator: a bin's density
-// (area / bin area) is held as round(density * 2^36) in an unsigned 64-bit
-// word, exact for per-bin densities below 2^27.
-constexpr double kFixScale = 68719476736.0;          // 2^36
-constexpr double kFixInv = 1.0 / 68719476736.0;
+// Fixed-point scale of the deterministic accumulator: each contribution
+// ratio * tx * ty / bin_area is at most 1 (tx <= bsx, ty <= bsy, ratio <= 1),
+// so a bin's sum is below nc_max and round(v * 2^f) with
+// f = 62 - ceil(log2(nc_max)) (capped to [20, 52]) never overflows the
+// unsigned 64-bit word.  fix_exponent() is shared by host and device.
+__host__ __device__ inline int fix_exponent(int nc_max)
+{
+    int lg = 0;
+    while (lg < 31 && (1ll << lg) < (long long)(nc_max > 1 ? nc_max : 1)) ++lg;
+    int f = 62 - lg;
+    return f > 52 ? 52 : (f < 20 ? 20 : f);
+}
 
 template <typename T> struct vec2;
 template <> struct vec2<float> { using type = float2; };

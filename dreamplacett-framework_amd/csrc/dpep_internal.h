@@ -26,6 +26,7 @@ struct SpectralArgs {
     double wu_step;     // 2 pi / M
     double wv_step;     // 2 pi / N * bsx / bsy
     int potential;      // compute the potential map
+    double fix_inv;     // 1 / Grid::fix_scale (deterministic mode)
     const void* twM;    // exp(-2 pi i m / M), m < M
     const void* postM;  // exp(-i pi k / 2M), k <= M/2
     const void* twN;

@@ -7,7 +7,8 @@
 // span loop) and adds ratio * tx * ty / bin_area into every covered bin:
 // native float atomics into a map pre-loaded with the fixed-cell density, or
 // (deterministic mode) unsigned 64-bit fixed-point atomics into a zeroed map
-// that the first spectral pass converts and folds.
+// that the first spectral pass converts and folds (scale 2^f, f chosen
+// per context so the sum cannot overflow; see fix_exponent).
 //
 // Gather: one thread per cell sums ratio * tx * ty * field over the same span
 // (the consumer of ctx.field_map_x/y, integration/scatter_ttnn_client.py:
@@ -56,7 +57,7 @@ __global__ __launch_bounds__(256) void k_scatter(
             const double v = stx * ty;
             if constexpr (FIXED) {
                 atomicAdd((unsigned long long*)&acc[row + h],
-                          (unsigned long long)__double2ull_rn(v * kFixScale));
+                          (unsigned long long)__double2ull_rn(v * g.fix_scale));
             } else {
                 unsafeAtomicAdd(&density[row + h], (T)v);
             }

@@ -122,7 +122,7 @@ __device__ __forceinline__ vec2_t<T> pack2(vec2_t<T> v1, vec2_t<T> v2)
 
 // ---------------------------------------------------------------------------
 // P1: forward DCT-II along y of 2F rows of rho; writes T (tiled).
-// SRC 0: rho read from density_in.  SRC 1: rho = d0n + acc * 2^-36, also
+// SRC 0: rho read from density_in.  SRC 1: rho = d0n + acc * 2^-f, also
 // written to density_out (deterministic accumulation).
 // ---------------------------------------------------------------------------
 template <typename T, int L, int F, int SRC>
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_dct(
         if constexpr (SRC == 0) {
             val = density_in[base + e];
         } else {
-            val = (T)((double)d0n[base + e] + (double)acc[base + e] * kFixInv);
+            val = (T)((double)d0n[base + e] + (double)acc[base + e] * a.fix_inv);
             density_out[base + e] = val;
         }
         comp<T>(sb[(r >> 1) * LP + lds_pad(makhoul_pos<L>(m))], r & 1) = val;

@@ -33,7 +33,8 @@ DPEP_FLAG_NO_GATHER = 0x8
 NUM_TIMINGS = 9
 TIMING_KEYS = ("h2d", "scatter", "gather", "d2h_den", "upload", "compute",
                "download", "fw", "total")
-KERNEL_KEYS = ("init", "scatter", "row_dct", "col_pass", "row_inv", "gather")
+KERNEL_KEYS = ("init", "scatter", "row_dct", "col_pass", "row_inv", "gather",
+               "step")
 
 # Every symbol include/dpep.h declares, with (restype, argtypes).
 _vp = ctypes.c_void_p
@@ -226,8 +227,9 @@ class Context:
         self.compute()
         return self.get_outputs()
 
-    def set_profiling(self, enable: bool) -> None:
-        _check(self._lib.dpep_set_profiling(self.handle, 1 if enable else 0),
+    def set_profiling(self, slots: int) -> None:
+        """slots > 0: record per-kernel HIP events for up to `slots` steps."""
+        _check(self._lib.dpep_set_profiling(self.handle, int(slots)),
                "dpep_set_profiling", self._lib)
 
     def timings(self) -> Dict[str, float]:

@@ -138,15 +138,16 @@ int dpep_step_device(dpep_ctx* ctx, const void* d_px, const void* d_py,
  * values the reference server wrote into the shm header (:1798-1808). */
 int dpep_get_timings(dpep_ctx* ctx, float* out);
 
-/* Per-kernel average durations of the last step in microseconds, measured
- * with HIP events around each launch on the context's stream:
+/* Per-kernel average durations in microseconds over the steps recorded
+ * since profiling was enabled (at most `slots` of them), measured with HIP
+ * events around each launch on the stream the kernels run on:
  * [0] init, [1] scatter, [2] row DCT, [3] column DCT + inverse,
- * [4] row inverse, [5] gather.  n = number of floats in out (<= 8). */
+ * [4] row inverse, [5] gather, [6] whole step.  n = floats in out. */
 int dpep_get_kernel_times(dpep_ctx* ctx, float* out, int n);
 
-/* Enables (1) or disables (0) per-kernel event timing (adds events between
- * launches; off by default). */
-int dpep_set_profiling(dpep_ctx* ctx, int enable);
+/* slots > 0 enables per-kernel event timing for a ring of `slots` steps
+ * (adds one event between launches); 0 disables (the default). */
+int dpep_set_profiling(dpep_ctx* ctx, int slots);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,50 @@
+"""Runs libdpep's kernel source on the CPU (tests/emu): every kernel of a
+step, one std::thread per GPU thread, under AddressSanitizer with exact-size
+buffers and a poisoned LDS tail, compared with the float64 oracle.  Catches
+out-of-bounds indexing and transform mistakes without a GPU."""
+import os
+import shutil
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+
+CLANG = "/opt/rocm/llvm/bin/clang++"
+CLANGC = "/opt/rocm/llvm/bin/clang"
+
+
+@pytest.fixture(scope="module")
+def emu(tmp_path_factory):
+    if not os.path.exists(CLANG):
+        pytest.skip("ROCm clang++ not available")
+    d = tmp_path_factory.mktemp("emu")
+    obj = d / "oracle.o"
+    subprocess.run([CLANGC, "-O1", "-g", "-fsanitize=address", "-c",
+                    os.path.join(ROOT, "oracle", "dpep_oracle.c"), "-o", str(obj)],
+                   check=True)
+    exe = d / "emu_main"
+    subprocess.run([CLANG, "-std=c++20", "-O1", "-g", "-fsanitize=address",
+                    "-fno-omit-frame-pointer",
+                    "-I", os.path.join(ROOT, "tests", "emu"),
+                    "-I", os.path.join(ROOT, "dreamplacett-framework_amd", "csrc"),
+                    "-I", os.path.join(ROOT, "include"),
+                    os.path.join(ROOT, "tests", "emu", "emu_main.cpp"), str(obj),
+                    "-o", str(exe), "-lpthread", "-lm"], check=True)
+    return str(exe)
+
+
+CASES = [
+    "f32 8 8 50", "f32 16 16 200", "f32 8 32 60 nopot", "f32 16 128 300",
+    "f32 128 16 300 det", "f64 8 8 40", "f64 64 64 300 det", "f32 256 256 2000",
+    "f32 16 4096 300", "f64 16 4096 100",
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_kernels_in_bounds_and_accurate(emu, case):
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=1")
+    r = subprocess.run([emu] + case.split(), capture_output=True, text=True,
+                       timeout=600, env=env)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+    assert "emu " in r.stdout

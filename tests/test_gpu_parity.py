@@ -1,0 +1,284 @@
+"""GPU parity: libdpep.so on the MI355X against the float64 oracle, through
+the C ABI (ctypes), on the same seeded inputs.
+
+Tolerances (the step's contract):
+  float32: density and potential rel L-inf <= 1e-5; field_x/y and per-cell
+           forces rel L2 <= 1e-4.
+  float64: density and potential rel L-inf <= 1e-10; fields and forces rel
+           L2 <= 1e-9 (fixed-point mode: quantum 2^-36 of a bin density).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import rel_l2, rel_linf
+
+pytestmark = pytest.mark.gpu
+
+TOL = {np.float32: (1e-5, 1e-4), np.float64: (1e-10, 1e-9)}
+
+
+def check(out, ref, dtype, tag=""):
+    tl, tf = TOL[dtype]
+    errs = {}
+    for k in ("density", "potential"):
+        if k in out and k in ref:
+            errs[k] = rel_linf(out[k], ref[k])
+            assert errs[k] <= tl, f"{tag} {k} rel Linf {errs[k]:.3e} > {tl}"
+    for k in ("field_x", "field_y", "grad_x", "grad_y"):
+        if k in out and k in ref:
+            errs[k] = rel_l2(out[k], ref[k])
+            assert errs[k] <= tf, f"{tag} {k} rel L2 {errs[k]:.3e} > {tf}"
+    return errs
+
+
+def run_gpu(w, dtype=np.float32, cells=None, **kw):
+    import dpep
+    px, py, sx, sy = cells if cells is not None else w.cells(dtype)
+    with dpep.Context(w.M, w.N, max(len(px), 1), w.xl, w.yl, w.xh, w.yh,
+                      dtype=dtype, **kw) as ctx:
+        ctx.set_initial_density(w.d0n.astype(dtype))
+        return ctx.step(px, py, sx, sy)
+
+
+def run_oracle(oracle, w, dtype=np.float32, cells=None, stretch=True):
+    px, py, sx, sy = cells if cells is not None else w.cells(dtype)
+    return oracle.step(px, py, sx, sy, w.M, w.N, w.xl, w.yl, w.xh, w.yh,
+                       d0n=w.d0n.astype(dtype), stretch=stretch)
+
+
+# --------------------------------------------------------------------------
+# spectral solve alone (no cells; the density is the uploaded D0)
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("M,N", [(8, 8), (16, 64), (64, 16), (512, 512),
+                                 (2048, 2048), (4096, 4096), (8192, 8)])
+def test_solve_random_density(oracle, dtype, M, N):
+    import dpep
+    if dtype == np.float64 and max(M, N) > 4096:
+        pytest.skip("float64 grids are limited to 4096")
+    rng = np.random.default_rng(M + 3 * N)
+    d0 = rng.random((M, N)).astype(dtype)
+    with dpep.Context(M, N, 1, 0.0, 0.0, 70.0, 50.0, dtype=dtype) as ctx:
+        ctx.set_initial_density(d0)
+        out = ctx.step(*[np.zeros(0, dtype)] * 4)
+    phi, fx, fy = oracle.solve(d0.astype(np.float64), 70.0 / M, 50.0 / N)
+    check(out, {"density": d0, "potential": phi, "field_x": fx, "field_y": fy},
+          dtype, f"{M}x{N}")
+
+
+@pytest.mark.parametrize("u0,v0", [(3, 5), (0, 1), (1, 0), (31, 17)])
+def test_solve_single_mode_closed_form(u0, v0):
+    import dpep
+    M, N, bsx, bsy = 64, 32, 2.0, 3.0
+    t = np.arange(M)[:, None] + 0.5
+    s = np.arange(N)[None, :] + 0.5
+    rho = np.cos(np.pi * u0 * t / M) * np.cos(np.pi * v0 * s / N)
+    with dpep.Context(M, N, 1, 0.0, 0.0, M * bsx, N * bsy, dtype=np.float64) as ctx:
+        ctx.set_initial_density(rho)
+        out = ctx.step(*[np.zeros(0)] * 4)
+    wu = 2 * np.pi * u0 / M
+    wv = 2 * np.pi * v0 / N * bsx / bsy
+    D = wu * wu + wv * wv
+    amp = (2.0 if u0 == 0 else 1.0) * (2.0 if v0 == 0 else 1.0)
+    cu, cv = (1.0 if u0 == 0 else 2.0), (1.0 if v0 == 0 else 2.0)
+    sx_ = np.sin(np.pi * u0 * t / M) * np.cos(np.pi * v0 * s / N)
+    sy_ = np.cos(np.pi * u0 * t / M) * np.sin(np.pi * v0 * s / N)
+    np.testing.assert_allclose(out["potential"], amp * cu * cv / D * rho, atol=1e-10)
+    np.testing.assert_allclose(out["field_x"], amp * cv * wu / D * sx_, atol=1e-10)
+    np.testing.assert_allclose(out["field_y"], amp * cu * wv / D * sy_, atol=1e-10)
+
+
+# --------------------------------------------------------------------------
+# full steps against the oracle
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("cfg,cells,grid", [(1, 30000, 128), (2, 30000, 512),
+                                            (3, 40000, 256), (5, 60000, 64)])
+@pytest.mark.parametrize("det", [False, True])
+def test_small_configs(oracle, cfg, cells, grid, det):
+    from dpep import workloads
+    w = workloads.small(cfg, seed=11, cells=cells, grid=grid)
+    check(run_gpu(w, deterministic=det), run_oracle(oracle, w), np.float32,
+          f"C{cfg} small det={det}")
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4])
+def test_full_size_configs(oracle, cfg):
+    from dpep import workloads
+    w = workloads.make(cfg, seed=0)
+    errs = check(run_gpu(w), run_oracle(oracle, w), np.float32, f"C{cfg}")
+    print(f"C{cfg} full: " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
+
+
+def test_float64_mode(oracle):
+    from dpep import workloads
+    w = workloads.small(5, seed=3, cells=100000, grid=512)
+    for det in (False, True):
+        check(run_gpu(w, np.float64, deterministic=det),
+              run_oracle(oracle, w, np.float64), np.float64, f"f64 det={det}")
+
+
+def test_no_stretch_semantics(oracle):
+    """DPEP_FLAG_NO_STRETCH reproduces the TT path's density (original sizes,
+    ratio 1: scatter_ttnn_client.py:628-649)."""
+    from dpep import workloads
+    w = workloads.small(3, seed=4, cells=30000, grid=256)
+    check(run_gpu(w, stretch=False), run_oracle(oracle, w, stretch=False),
+          np.float32, "no-stretch")
+
+
+# --------------------------------------------------------------------------
+# determinism
+# --------------------------------------------------------------------------
+def test_deterministic_mode_is_bitwise_reproducible_and_order_free():
+    from dpep import workloads
+    w = workloads.small(2, seed=5, cells=200000, grid=512)   # hot centre bins
+    a = run_gpu(w, deterministic=True)
+    b = run_gpu(w, deterministic=True)
+    for k in a:
+        assert np.array_equal(a[k], b[k]), k
+    p = np.random.default_rng(0).permutation(w.nc)
+    cells = tuple(np.ascontiguousarray(c[p]) for c in w.cells(np.float32))
+    c = run_gpu(w, deterministic=True, cells=cells)
+    for k in ("density", "potential", "field_x", "field_y"):
+        assert np.array_equal(a[k], c[k]), k
+
+
+# --------------------------------------------------------------------------
+# edge cases of the boundary
+# --------------------------------------------------------------------------
+def test_edge_cells(oracle):
+    from dpep import workloads
+    w = workloads.small(3, seed=6, cells=5000, grid=64)
+    px, py, sx, sy = [a.copy() for a in w.cells(np.float32)]
+    bs = w.bsx
+    # zero / negative sizes, NaN / inf positions, outside the die, wider than
+    # the die, exactly on bin edges, straddling the die corner
+    px[:12] = [0, 10, np.nan, 100, -5 * w.xh, 2 * w.xh, -3 * bs, 0, 5 * bs, 7 * bs, w.xh - 1, 1]
+    py[:12] = [0, 10, 5, np.inf, 10, 10, 5 * bs, 0, 5 * bs, 3 * bs, w.yh - 1, 1]
+    sx[:12] = [0, -1, 3, 3, 4, 4, 3 * w.xh, w.xh, bs, 2 * bs, 30, 1e-3]
+    sy[:12] = [5, 5, 3, 3, 4, 4, 12, w.yh, bs, 12, 30, 1e-3]
+    cells = (px, py, sx, sy)
+    out = run_gpu(w, cells=cells)
+    ref = run_oracle(oracle, w, cells=cells)
+    check(out, ref, np.float32, "edge")
+    assert np.all(np.isfinite(out["grad_x"])) and np.all(np.isfinite(out["density"]))
+    assert out["grad_x"][0] == 0 and out["grad_x"][1] == 0 and out["grad_x"][2] == 0
+
+
+def test_no_cells_and_shrinking_cell_count(oracle):
+    import dpep
+    from dpep import workloads
+    w = workloads.small(3, seed=7, cells=20000, grid=128)
+    cells = w.cells(np.float32)
+    with dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh) as ctx:
+        ctx.set_initial_density(w.d0n.astype(np.float32))
+        out0 = ctx.step(*[np.zeros(0, np.float32)] * 4)
+        ref0 = run_oracle(oracle, w, cells=[np.zeros(0)] * 4)
+        check(out0, ref0, np.float32, "empty")
+        full = ctx.step(*cells)
+        check(full, run_oracle(oracle, w), np.float32, "full")
+        half = tuple(c[: w.nc // 2] for c in cells)
+        out = ctx.step(*half)
+        check(out, run_oracle(oracle, w, cells=half), np.float32, "half")
+        assert out["grad_x"].shape == (w.nc // 2,)
+        with pytest.raises(ValueError):
+            ctx.set_cells(*[np.zeros(w.nc + 1, np.float32)] * 4)
+
+
+def test_timings_and_kernel_times():
+    import dpep
+    from dpep import workloads
+    w = workloads.small(3, seed=8, cells=50000, grid=256)
+    with dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh) as ctx:
+        ctx.set_cells(*w.cells(np.float32))
+        ctx.set_profiling(4)
+        for _ in range(4):
+            ctx.compute()
+        ctx.sync()
+        kt = ctx.kernel_times_us()
+        t = ctx.timings()
+    assert set(kt) == set(dpep.KERNEL_KEYS)
+    assert all(v > 0 for v in kt.values())
+    assert kt["step"] >= kt["scatter"]
+    assert set(t) == set(dpep.TIMING_KEYS) and t["total"] > 0
+
+
+def test_step_device_matches_host_step():
+    """dpep_step_device on caller-owned device buffers (allocated through the
+    same HIP runtime libdpep links) equals the host-buffer step."""
+    import dpep
+    from dpep import workloads
+    lib = dpep.load_library()
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    hip.hipFree.argtypes = [ctypes.c_void_p]
+    H2D, D2H = 1, 2
+    w = workloads.small(3, seed=9, cells=30000, grid=256)
+    cells = w.cells(np.float32)
+    ref = run_gpu(w)
+    bufs = []
+
+    def dev(nbytes):
+        p = ctypes.c_void_p()
+        assert hip.hipMalloc(ctypes.byref(p), nbytes) == 0
+        bufs.append(p)
+        return p
+
+    try:
+        dc = []
+        for a in cells:
+            p = dev(a.nbytes)
+            assert hip.hipMemcpy(p, a.ctypes.data, a.nbytes, H2D) == 0
+            dc.append(p)
+        mnb = w.M * w.N * 4
+        dfx, dfy, dden, dphi = dev(mnb), dev(mnb), dev(mnb), dev(mnb)
+        dgx, dgy = dev(w.nc * 4), dev(w.nc * 4)
+        with dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh) as ctx:
+            ctx.set_initial_density(w.d0n.astype(np.float32))
+            rc = lib.dpep_step_device(ctx.handle, *dc, w.nc, dfx, dfy, dden, dphi,
+                                      dgx, dgy, None)
+            assert rc == 0, dpep.last_error()
+            ctx.sync()
+        got = {}
+        for name, p, n in (("field_x", dfx, w.M * w.N), ("field_y", dfy, w.M * w.N),
+                           ("density", dden, w.M * w.N), ("potential", dphi, w.M * w.N),
+                           ("grad_x", dgx, w.nc), ("grad_y", dgy, w.nc)):
+            h = np.empty(n, np.float32)
+            assert hip.hipMemcpy(h.ctypes.data, p, n * 4, D2H) == 0
+            got[name] = h.reshape(ref[name].shape)
+    finally:
+        for p in bufs:
+            hip.hipFree(p)
+    for k in got:
+        np.testing.assert_allclose(got[k], ref[k], rtol=1e-6, atol=1e-6 * np.abs(ref[k]).max())
+
+
+# --------------------------------------------------------------------------
+# convergence-loop configuration: 100 consecutive steps
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_c5_hundred_steps(oracle, dtype):
+    import dpep
+    from dpep import workloads
+    w = workloads.config5()
+    px, py = w.px.copy(), w.py.copy()
+    sx, sy = w.sx.astype(dtype), w.sy.astype(dtype)
+    ba = w.bsx * w.bsy
+    with dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh, dtype=dtype) as ctx:
+        ctx.set_initial_density(w.d0n.astype(dtype))
+        for step in range(100):
+            px, py = workloads.c5_displace(w, px, py, step)
+            cells = (px.astype(dtype), py.astype(dtype), sx, sy)
+            out = ctx.step(*cells)
+            # size-independent invariant every step: all cells lie inside the
+            # die, so the density carries exactly the cells' area
+            mass = out["density"].astype(np.float64).sum() * ba
+            area = float((sx.astype(np.float64) * sy).sum())
+            assert mass == pytest.approx(area, rel=1e-5 if dtype == np.float32 else 1e-11)
+            if step % 20 == 19 or step == 0:
+                ref = oracle.step(*cells, w.M, w.N, w.xl, w.yl, w.xh, w.yh,
+                                  d0n=w.d0n.astype(dtype))
+                check(out, ref, dtype, f"C5 step {step}")
