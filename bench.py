@@ -39,8 +39,11 @@ def kernel_bytes(nc, M, N, esz, potential=True):
     mn = M * N
     nmaps = 3 if potential else 2
     return {
-        "init": 2 * esz * mn,                          # read D0, write rho
-        "scatter": 4 * esz * nc + esz * mn,            # read cells, write rho
+        "bin_count": 4 * esz * nc,                     # read cells
+        "bin_scan": 0,                                 # strip table only
+        "bin_fill": 4 * esz * nc,                      # read cells (+ sorted entries: scratch)
+        "strip_acc": 2 * esz * mn,                     # read D0, write rho (+ entries: scratch)
+        "strip_red": 0,                                # split strips only
         "row_dct": 2 * esz * mn,                       # read rho, write T
         "col_pass": (1 + nmaps) * esz * mn,            # read T, write U*
         "row_inv": 2 * nmaps * esz * mn,               # read U*, write maps

@@ -3,12 +3,12 @@
 // A context owns every device buffer of one (M, N, nc_max, dtype) problem,
 // allocated once at creation; a step allocates nothing.  Launch sequence of
 // one step on the context's stream:
-//   k_init      density <- D0n (float atomics) or acc <- 0 (fixed point)
-//   k_scatter   cells -> bins
-//   k_row_dct   P1  (folds D0n / converts fixed point when deterministic)
+//   k_bin_count, k_bin_scan, k_bin_fill   counting sort of cells into strips
+//   k_strip_acc, k_strip_red              LDS strip accumulation, D0 fold
+//   k_row_dct   P1  (converts the fixed-point map when deterministic)
 //   k_col_pass  P2
 //   k_row_inv   P3  -> field_x, field_y, potential
-//   k_gather    cells <- fields
+//   k_gather_bin     cells <- fields
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -49,7 +49,8 @@ int fail(int code, const char* fmt, ...)
                         hipGetErrorString(e_));                              \
     } while (0)
 
-constexpr int kNumStages = 6;   // init, scatter, P1, P2, P3, gather
+// bin_count, bin_scan, bin_fill, strip_acc, strip_red, P1, P2, P3, gather
+constexpr int kNumStages = 9;
 
 bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
@@ -67,6 +68,8 @@ struct dpep_ctx {
     void *d_fx = nullptr, *d_fy = nullptr, *d_gx = nullptr, *d_gy = nullptr;
     void *d_T = nullptr, *d_Ux = nullptr, *d_Uy = nullptr;
     uint64_t* d_acc = nullptr;
+    BinPlan plan{};
+    BinArgs bins{};
     void *d_twM = nullptr, *d_postM = nullptr, *d_twN = nullptr,
          *d_postN = nullptr;
     hipStream_t stream = nullptr;
@@ -138,10 +141,13 @@ static int upload_tables(dpep_ctx* c)
 
 static void release(dpep_ctx* c)
 {
+    const BinArgs& b = c->bins;
     void* bufs[] = {c->d_px, c->d_py, c->d_sx, c->d_sy, c->d_d0n,
                     c->d_density, c->d_potential, c->d_fx, c->d_fy, c->d_gx,
                     c->d_gy, c->d_T, c->d_Ux, c->d_Uy, c->d_acc, c->d_twM,
-                    c->d_postM, c->d_twN, c->d_postN};
+                    c->d_postM, c->d_twN, c->d_postN, b.cnt, b.strip_off,
+                    b.nch, b.item_start, b.items, b.nitems, b.eidx, b.entries,
+                    b.big_list, b.big_count, b.bigflag, b.B, b.partial};
     for (void* p : bufs)
         if (p) (void)hipFree(p);
     for (auto& e : c->ev)
@@ -161,7 +167,6 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
 {
     const bool det = (c->flags & DPEP_FLAG_DETERMINISTIC) != 0;
     const bool gather = !(c->flags & DPEP_FLAG_NO_GATHER);
-    const size_t mn = (size_t)c->M * c->N;
     uint64_t* acc = det ? c->d_acc : nullptr;
     const bool prof = c->profiling != 0;
     const T* d0n = (const T*)c->d_d0n;
@@ -169,31 +174,37 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
     // Every pointer a kernel dereferences must be set: a null here is a bug
     // of this library, reported as an error instead of a device fault.
     const SpectralArgs& a = c->sargs;
+    const BinArgs& b = c->bins;
     if (!a.twM || !a.postM || !a.twN || !a.postN || !d0n || !dens || !fx ||
         !fy || !c->d_T || !c->d_Ux || !c->d_Uy || (a.potential && !phi) ||
         (det && !acc) || (nc > 0 && (!px || !py || !sx || !sy)) ||
-        (nc > 0 && gather && (!gx || !gy)))
+        (gather && (!gx || !gy)) || !b.cnt || !b.strip_off || !b.nch ||
+        !b.item_start || !b.items || !b.nitems || !b.eidx || !b.entries ||
+        !b.big_list || !b.big_count || !b.bigflag || !b.B || !b.partial)
         return fail(DPEP_ERR_STATE, "internal: a kernel argument is NULL");
+    if (nc > c->nc_max)
+        return fail(DPEP_ERR_ARG, "nc=%d exceeds nc_max=%d", nc, c->nc_max);
 
-    // with profiling on, this step's stage boundaries go to ring slot `ps`
+    // with profiling on, this step's stage boundaries go to one ring slot
     hipEvent_t* pe = prof ? &c->prof_ev[(size_t)(c->prof_steps % c->prof_slots) *
                                          (kNumStages + 1)]
                           : nullptr;
     HIP_TRY(hipEventRecord(c->ev[0], s));
     if (prof) HIP_TRY(hipEventRecord(pe[0], s));
-    HIP_TRY(launch_fill_init<T>(d0n, dens, acc, mn, s));
-    if (prof) HIP_TRY(hipEventRecord(pe[1], s));
-    HIP_TRY(launch_scatter<T>(px, py, sx, sy, nc, c->grid, dens, acc, s));
-    if (prof) HIP_TRY(hipEventRecord(pe[2], s));
+    HIP_TRY(launch_bin_scatter<T>(px, py, sx, sy, nc, c->grid, c->bins, d0n,
+                                  dens, acc, gather ? gx : nullptr,
+                                  gather ? gy : nullptr, s, prof ? pe + 1 : nullptr));
+    if (prof) HIP_TRY(hipEventRecord(pe[5], s));
     HIP_TRY(launch_row_dct<T>(c->sargs, dens, acc, d0n, dens, (T*)c->d_T, s));
-    if (prof) HIP_TRY(hipEventRecord(pe[3], s));
+    if (prof) HIP_TRY(hipEventRecord(pe[6], s));
     HIP_TRY(launch_col_pass<T>(c->sargs, (T*)c->d_T, (T*)c->d_Ux, (T*)c->d_Uy, s));
-    if (prof) HIP_TRY(hipEventRecord(pe[4], s));
+    if (prof) HIP_TRY(hipEventRecord(pe[7], s));
     HIP_TRY(launch_row_inv<T>(c->sargs, (const T*)c->d_Ux, (const T*)c->d_Uy,
                               (const T*)c->d_T, fx, fy, phi, s));
-    if (prof) HIP_TRY(hipEventRecord(pe[5], s));
+    if (prof) HIP_TRY(hipEventRecord(pe[8], s));
     if (gather)
-        HIP_TRY(launch_gather<T>(px, py, sx, sy, nc, c->grid, fx, fy, gx, gy, s));
+        HIP_TRY(launch_bin_gather<T>(px, py, sx, sy, nc, c->grid, c->bins, fx, fy,
+                                     gx, gy, s));
     if (prof) HIP_TRY(hipEventRecord(pe[kNumStages], s));
     HIP_TRY(hipEventRecord(c->ev[kNumStages], s));
     if (prof) c->prof_steps++;
@@ -268,7 +279,10 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
 
     static std::once_flag once;
     static hipError_t prep_err = hipSuccess;
-    std::call_once(once, [] { prep_err = spectral_prepare(); });
+    std::call_once(once, [] {
+        prep_err = spectral_prepare();
+        if (prep_err == hipSuccess) prep_err = bin_prepare();
+    });
     if (prep_err != hipSuccess)
         return fail(DPEP_ERR_HIP, "kernel attribute set-up failed: %s",
                     hipGetErrorString(prep_err));
@@ -314,6 +328,30 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
         if (flags & DPEP_FLAG_DETERMINISTIC)
             HIP_TRY(hipMalloc((void**)&c->d_acc, (size_t)M * N * sizeof(uint64_t)));
         HIP_TRY(hipMemset(c->d_d0n, 0, mnb));
+        // strip binning
+        const size_t accb = (flags & DPEP_FLAG_DETERMINISTIC) ? 8 : c->esz;
+        BinPlan& p = c->plan;
+        p = make_bin_plan(M, N, nc_max, accb);
+        BinArgs& b = c->bins;
+        b.S = p.S; b.R = p.R; b.lgR = p.lgR; b.G1 = 1; b.CH = p.CH; b.Wmax = p.Wmax;
+        HIP_TRY(hipMalloc((void**)&b.cnt, (size_t)p.G1max * p.S * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.strip_off, (size_t)(p.S + 1) * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.nch, (size_t)p.S * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.item_start, (size_t)p.S * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.items, (size_t)p.Wmax * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.nitems, sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.eidx, p.cap * sizeof(unsigned)));
+        HIP_TRY(hipMalloc(&b.entries, p.cap * 4 * c->esz));
+        HIP_TRY(hipMalloc((void**)&b.big_list, (size_t)(nc_max > 0 ? nc_max : 1) * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.big_count, sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.bigflag, (size_t)p.S * sizeof(unsigned)));
+        HIP_TRY(hipMalloc(&b.B, (size_t)M * N * accb));
+        HIP_TRY(hipMalloc(&b.partial, p.partial_elems * accb));
+        // B and the strip flags must start at zero; each step leaves them so.
+        HIP_TRY(hipMemset(b.B, 0, (size_t)M * N * accb));
+        HIP_TRY(hipMemset(b.bigflag, 0, (size_t)p.S * sizeof(unsigned)));
+        HIP_TRY(hipMemset(b.big_count, 0, sizeof(unsigned)));
+        HIP_TRY(hipDeviceSynchronize());
         return dtype == DPEP_DTYPE_F32 ? upload_tables<float>(c)
                                        : upload_tables<double>(c);
     };
@@ -454,9 +492,9 @@ int dpep_get_timings(dpep_ctx* c, float* out)
     if (c->profiling && c->prof_steps > 0) {
         const hipEvent_t* pe = &c->prof_ev[(size_t)((c->prof_steps - 1) % c->prof_slots) *
                                            (kNumStages + 1)];
-        out[1] = elapsed(pe[0], pe[2]);              // init + scatter
-        out[5] = elapsed(pe[2], pe[5]);              // P1 + P2 + P3
-        out[2] = elapsed(pe[5], pe[kNumStages]);     // gather
+        out[1] = elapsed(pe[0], pe[5]);              // binning + accumulation
+        out[5] = elapsed(pe[5], pe[8]);              // P1 + P2 + P3
+        out[2] = elapsed(pe[8], pe[kNumStages]);     // gather
     } else {
         out[5] = total;
     }

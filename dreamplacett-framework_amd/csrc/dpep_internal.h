@@ -35,13 +35,6 @@ struct SpectralArgs {
 
 // Launchers (return hipError_t of the launch).  T = float or double.
 template <typename T>
-hipError_t launch_fill_init(const T* d0n, T* density, uint64_t* acc,
-                            size_t mn, hipStream_t s);
-template <typename T>
-hipError_t launch_scatter(const T* px, const T* py, const T* sx, const T* sy,
-                          int nc, const Grid& g, T* density, uint64_t* acc,
-                          hipStream_t s);
-template <typename T>
 hipError_t launch_row_dct(const SpectralArgs& a, const T* density_in,
                           const uint64_t* acc, const T* d0n, T* density_out,
                           T* Tt, hipStream_t s);
@@ -51,12 +44,83 @@ hipError_t launch_col_pass(const SpectralArgs& a, T* Tt, T* Ux, T* Uy,
 template <typename T>
 hipError_t launch_row_inv(const SpectralArgs& a, const T* Ux, const T* Uy,
                           const T* Up, T* fx, T* fy, T* phi, hipStream_t s);
-template <typename T>
-hipError_t launch_gather(const T* px, const T* py, const T* sx, const T* sy,
-                         int nc, const Grid& g, const T* fx, const T* fy,
-                         T* gx, T* gy, hipStream_t s);
+// ---------------------------------------------------------------------------
+// Strip binning (kernels in dpep_bin.h)
+// ---------------------------------------------------------------------------
+constexpr int kBinThreads = 512;       // K1 / K3 workgroup size
+constexpr int kCellsPerThread = 16;    // K1 / K3 cells per thread
+constexpr int kCellsPerGroup = kBinThreads * kCellsPerThread;
+constexpr int kAccThreads = 512;       // K4 / K4r workgroup size
+constexpr int kScanThreads = 1024;     // K2 (one workgroup)
+constexpr unsigned kSecondStrip = 0x80000000u;
 
-// Sets the dynamic-LDS limits of every spectral kernel instance (once).
+// Shared between host (sizing) and device.
+struct BinArgs {
+    int S, R, lgR;          // strips, rows per strip, log2 R
+    int G1;                 // K1/K3 workgroups of this step
+    int CH;                 // entries per K4 work item (chunk)
+    int Wmax;               // capacity of the work-item list
+    unsigned* cnt;          // [G1max][S] counts, then bases (in place)
+    unsigned* strip_off;    // [S + 1] entry offset of each strip
+    unsigned* nch;          // [S] chunks per strip
+    unsigned* item_start;   // [S] first work item of each strip
+    unsigned* items;        // [Wmax] strip | chunk << 16
+    unsigned* nitems;       // [1]
+    unsigned* eidx;         // [2 nc_max] cell index | kSecondStrip
+    void* entries;          // [2 nc_max] vec4 (px, py, sx, sy)
+    unsigned* big_list;     // [nc_max] tall cells
+    unsigned* big_count;    // [1]
+    unsigned* bigflag;      // [S] strip has rows in B
+    void* B;                // [M*N] accumulator type, zero between steps
+    void* partial;          // [Wmax][R*N] accumulator type
+};
+
+// Host-side sizing of the binning buffers (shared with the CPU emulator).
+struct BinPlan {
+    int S, R, lgR, G1max, CH, Wmax;
+    size_t cap;             // entries (2 per cell)
+    size_t acc_bytes;       // accumulator element size
+    size_t partial_elems;   // Wmax * R * N
+};
+
+inline BinPlan make_bin_plan(int M, int N, int nc_max, size_t acc_bytes)
+{
+    BinPlan p{};
+    p.acc_bytes = acc_bytes;
+    int R = 8;
+    while (R > 1 && (size_t)R * N * acc_bytes > 65536) R >>= 1;
+    if (R > M) R = M;
+    p.R = R;
+    p.lgR = 0;
+    while ((1 << p.lgR) < R) ++p.lgR;
+    p.S = M / R;
+    const long long nc = nc_max > 1 ? nc_max : 1;
+    p.G1max = (int)((nc + kCellsPerGroup - 1) / kCellsPerGroup);
+    p.cap = (size_t)(2 * nc);
+    long long ch = (long long)(3.0 * 1.15 * (double)nc / p.S) + 1;
+    if (ch < 8192) ch = 8192;
+    ch = (ch + kAccThreads - 1) / kAccThreads * kAccThreads;
+    p.CH = (int)ch;
+    p.Wmax = p.S + (int)((p.cap + ch - 1) / ch) + 1;
+    p.partial_elems = (size_t)p.Wmax * R * N;
+    return p;
+}
+
+// Strip-binned scatter (K1..K4r) and gather; ev (nullable) receives 4
+// events recorded after K1, K2, K3 and K4.
+template <typename T>
+hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
+                              const T* sy, int nc, const Grid& g, BinArgs b,
+                              const T* d0n, T* dens, uint64_t* acc, T* gx,
+                              T* gy, hipStream_t s, hipEvent_t* ev);
+template <typename T>
+hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
+                             const T* sy, int nc, const Grid& g,
+                             const BinArgs& b, const T* fx, const T* fy,
+                             T* gx, T* gy, hipStream_t s);
+
+// Sets the dynamic-LDS limits of every spectral / binning kernel (once).
 hipError_t spectral_prepare();
+hipError_t bin_prepare();
 
 }  // namespace dpep

@@ -1,9 +1,9 @@
 // CPU emulation of one electric-potential step with libdpep's kernel source
-// (csrc/dpep_scatter.h, csrc/dpep_spectral.h) under AddressSanitizer.
+// (csrc/dpep_bin.h, csrc/dpep_spectral.h) under AddressSanitizer.
 // Every global buffer is malloc'd at its exact size and the LDS tail beyond
 // the launch's dynamic size is poisoned, so any out-of-bounds index aborts
 // with a report.  Results are compared with the float64 oracle.
-// Usage: emu_main <f32|f64> M N ncells [det] [nopot]
+// Usage: emu_main <f32|f64> M N ncells [det] [nopot] [ch=<entries>] [tall]
 #include <sanitizer/asan_interface.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -13,7 +13,7 @@
 #include <thread>
 #include <vector>
 
-#include "dpep_scatter.h"
+#include "dpep_bin.h"
 #include "dpep_spectral.h"
 
 thread_local dim3 threadIdx, blockIdx;
@@ -70,7 +70,7 @@ static std::vector<T> table(int L, bool post)
 }
 
 template <typename T, int LM, int LN>
-static int run(int nc, bool det, bool pot)
+static int run(int nc, bool det, bool pot, int ch, bool tall)
 {
     using namespace dpep;
     const int M = LM, N = LN;
@@ -91,6 +91,8 @@ static int run(int nc, bool det, bool pot)
         py[i] = (T)(yl + (yh - yl) * (1.1 * U(rng) - 0.05));
     }
     if (nc > 2) { sx[0] = 0; sy[1] = -1; sx[2] = (T)(3 * (xh - xl)); px[2] = (T)(xl - (xh - xl)); }
+    if (tall)   // a tenth of the cells spans 3..40 rows
+        for (int i = 3; i < nc; i += 10) sx[i] = (T)(g.bsx * (3 + 37 * U(rng)));
     T* d0n = exact<T>(mn); T* dens = exact<T>(mn); T* phi = pot ? exact<T>(mn) : nullptr;
     T* fx = exact<T>(mn); T* fy = exact<T>(mn); T* Tt = exact<T>(mn); T* Ux = exact<T>(mn);
     T* Uy = exact<T>(mn); T* gx = exact<T>(nc); T* gy = exact<T>(nc);
@@ -108,11 +110,47 @@ static int run(int nc, bool det, bool pot)
     a.wu_step = 2 * M_PI / M; a.wv_step = 2 * M_PI / N * (g.bsx / g.bsy);
     a.potential = pot; a.fix_inv = 1.0 / g.fix_scale; a.twM = d_twM; a.postM = d_poM; a.twN = d_twN; a.postN = d_poN;
 
-    const unsigned ib = (unsigned)((mn + 255) / 256);
-    launch(ib < 8192 ? ib : 8192, 256, 0, [&] { k_init<T>(d0n, dens, acc, mn); });
-    if (nc > 0) {
-        if (det) launch((nc + 255) / 256, 256, 0, [&] { k_scatter<T, true>(px, py, sx, sy, nc, g, dens, acc); });
-        else launch((nc + 255) / 256, 256, 0, [&] { k_scatter<T, false>(px, py, sx, sy, nc, g, dens, acc); });
+    // strip binning buffers, exact sizes
+    const size_t accb = det ? 8 : sizeof(T);
+    BinPlan p = make_bin_plan(M, N, nc, accb);
+    if (ch > 0) {
+        p.CH = ch;
+        p.Wmax = p.S + (int)((p.cap + ch - 1) / ch) + 1;
+        p.partial_elems = (size_t)p.Wmax * p.R * N;
+    }
+    BinArgs b{};
+    b.S = p.S; b.R = p.R; b.lgR = p.lgR; b.CH = p.CH; b.Wmax = p.Wmax;
+    b.G1 = (nc + kCellsPerGroup - 1) / kCellsPerGroup;
+    if (b.G1 < 1) b.G1 = 1;
+    b.cnt = exact<unsigned>((size_t)b.G1 * p.S);
+    b.strip_off = exact<unsigned>(p.S + 1);
+    b.nch = exact<unsigned>(p.S);
+    b.item_start = exact<unsigned>(p.S);
+    b.items = exact<unsigned>(p.Wmax);
+    b.nitems = exact<unsigned>(1);
+    b.eidx = exact<unsigned>(p.cap);
+    b.entries = exact<vec4_t<T>>(p.cap);
+    b.big_list = exact<unsigned>(nc > 0 ? nc : 1);
+    b.big_count = exact<unsigned>(1);
+    b.bigflag = exact<unsigned>(p.S);
+    b.B = malloc(mn * accb);
+    b.partial = malloc(p.partial_elems * accb);
+    memset(b.B, 0, mn * accb);
+    memset(b.bigflag, 0, p.S * sizeof(unsigned));
+    *b.big_count = 0;
+    const size_t hist = (size_t)p.S * sizeof(unsigned);
+    const size_t tile = (size_t)p.R * N * accb;
+    for (int rep = 0; rep < 2; ++rep) {   // two steps: B / flags must be clean again
+        launch(b.G1, kBinThreads, hist, [&] { k_bin_count<T>(px, py, sx, sy, nc, g, b); });
+        launch(1, kScanThreads, (size_t)(p.S + 2048) * sizeof(unsigned), [&] { k_bin_scan(b); });
+        if (det) launch(b.G1, kBinThreads, hist, [&] { k_bin_fill<T, true>(px, py, sx, sy, nc, g, b, gx, gy); });
+        else launch(b.G1, kBinThreads, hist, [&] { k_bin_fill<T, false>(px, py, sx, sy, nc, g, b, gx, gy); });
+        if (det) launch(p.Wmax, kAccThreads, tile, [&] { k_strip_acc<T, true>(g, b, d0n, dens, acc); });
+        else launch(p.Wmax, kAccThreads, tile, [&] { k_strip_acc<T, false>(g, b, d0n, dens, acc); });
+        if (det) launch(p.S, kAccThreads, 0, [&] { k_strip_red<T, true>(g, b, d0n, dens, acc); });
+        else launch(p.S, kAccThreads, 0, [&] { k_strip_red<T, false>(g, b, d0n, dens, acc); });
+        for (int s2 = 0; s2 < p.S; ++s2)
+            if (b.bigflag[s2]) { fprintf(stderr, "bigflag left set\n"); return 4; }
     }
     {
         constexpr int F = fpw<T>(LN);
@@ -132,8 +170,18 @@ static int run(int nc, bool det, bool pot)
         const unsigned grid = M / F + (pot ? M / (2 * F) : 0);
         launch(grid, F * (LN / fft_e(LN)), shm, [&] { k_row_inv<T, LN, F>(a, Ux, Uy, Tt, fx, fy, phi); });
     }
-    if (nc > 0)
-        launch((nc + 255) / 256, 256, 0, [&] { k_gather<T>(px, py, sx, sy, nc, g, fx, fy, gx, gy); });
+    if (nc > 0) {
+        unsigned gb = (unsigned)((nc * 5 / 4 + 255) / 256);
+        if (gb > 64) gb = 64;
+        launch(gb, 256, 0, [&] { k_gather_bin<T>(px, py, sx, sy, g, b, fx, fy, gx, gy); });
+    }
+    {
+        const unsigned char* Bb = (const unsigned char*)b.B;
+        for (size_t i = 0; i < mn * accb; ++i)
+            if (Bb[i]) { fprintf(stderr, "side map B not re-zeroed at byte %zu (row %zu)\n", i, i / accb / N); return 4; }
+    }
+    printf("emu plan S=%d R=%d CH=%d Wmax=%d items=%u big=%u entries=%u\n", p.S, p.R, p.CH,
+           p.Wmax, *b.nitems, *b.big_count, b.strip_off[p.S]);
 
     // oracle
     std::vector<double> dpx(nc), dpy(nc), dsx(nc), dsy(nc), dd0(mn), rho(mn), rphi(mn), rfx(mn), rfy(mn), rgx(nc), rgy(nc);
@@ -163,9 +211,9 @@ static int run(int nc, bool det, bool pot)
 }
 
 template <typename T>
-static int dispatch(int M, int N, int nc, bool det, bool pot)
+static int dispatch(int M, int N, int nc, bool det, bool pot, int ch, bool tall)
 {
-#define CASE(a, b) if (M == a && N == b) return run<T, a, b>(nc, det, pot);
+#define CASE(a, b) if (M == a && N == b) return run<T, a, b>(nc, det, pot, ch, tall);
     CASE(8, 8) CASE(16, 16) CASE(8, 32) CASE(32, 8) CASE(64, 64) CASE(16, 128) CASE(128, 16)
     CASE(256, 256) CASE(512, 512) CASE(64, 2048) CASE(2048, 64) CASE(16, 4096) CASE(4096, 16)
 #undef CASE
@@ -178,10 +226,14 @@ int main(int argc, char** argv)
     if (argc < 5) { fprintf(stderr, "usage: %s f32|f64 M N nc [det] [nopot]\n", argv[0]); return 2; }
     const bool f64 = !strcmp(argv[1], "f64");
     const int M = atoi(argv[2]), N = atoi(argv[3]), nc = atoi(argv[4]);
-    bool det = false, pot = true;
+    bool det = false, pot = true, tall = false;
+    int ch = 0;
     for (int i = 5; i < argc; ++i) {
         if (!strcmp(argv[i], "det")) det = true;
         if (!strcmp(argv[i], "nopot")) pot = false;
+        if (!strcmp(argv[i], "tall")) tall = true;
+        if (!strncmp(argv[i], "ch=", 3)) ch = atoi(argv[i] + 3);
     }
-    return f64 ? dispatch<double>(M, N, nc, det, pot) : dispatch<float>(M, N, nc, det, pot);
+    return f64 ? dispatch<double>(M, N, nc, det, pot, ch, tall)
+               : dispatch<float>(M, N, nc, det, pot, ch, tall);
 }

@@ -12,6 +12,7 @@
 #include <cstdint>
 #include <cstring>
 #include <type_traits>
+#include <algorithm>
 #include <utility>
 
 #define __global__
@@ -29,6 +30,10 @@ struct dim3 {
 };
 struct float2 { float x, y; };
 struct double2 { double x, y; };
+struct float4 { float x, y, z, w; };
+struct double4 { double x, y, z, w; };
+using std::max;
+using std::min;
 
 extern thread_local dim3 threadIdx, blockIdx;
 extern dim3 blockDim, gridDim;
@@ -52,6 +57,13 @@ inline unsigned long long atomicAdd(unsigned long long* p, unsigned long long v)
 {
     return __atomic_fetch_add(p, v, __ATOMIC_RELAXED);
 }
+inline unsigned atomicAdd(unsigned* p, unsigned v)
+{
+    return __atomic_fetch_add(p, v, __ATOMIC_RELAXED);
+}
+inline float atomicAdd(float* p, float v) { return unsafeAtomicAdd(p, v); }
+inline double atomicAdd(double* p, double v) { return unsafeAtomicAdd(p, v); }
 
 typedef int hipError_t;
 typedef void* hipStream_t;
+typedef void* hipEvent_t;

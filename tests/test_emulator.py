@@ -1,7 +1,9 @@
 """Runs libdpep's kernel source on the CPU (tests/emu): every kernel of a
 step, one std::thread per GPU thread, under AddressSanitizer with exact-size
 buffers and a poisoned LDS tail, compared with the float64 oracle.  Catches
-out-of-bounds indexing and transform mistakes without a GPU."""
+out-of-bounds indexing, cross-wave races (threads really run concurrently)
+and transform mistakes without a GPU.  Each case runs two steps and checks
+that the side map and strip flags are left clean for the next step."""
 import os
 import shutil
 import subprocess
@@ -34,10 +36,13 @@ def emu(tmp_path_factory):
     return str(exe)
 
 
+# ch=<n> forces n entries per strip work item (exercises the split-strip
+# reduce); tall gives a tenth of the cells a span of 3..40 rows (side map B).
 CASES = [
-    "f32 8 8 50", "f32 16 16 200", "f32 8 32 60 nopot", "f32 16 128 300",
-    "f32 128 16 300 det", "f64 8 8 40", "f64 64 64 300 det", "f32 256 256 2000",
-    "f32 16 4096 300", "f64 16 4096 100",
+    "f32 8 8 50", "f32 16 16 200 tall", "f32 8 32 60 nopot", "f32 16 128 3000 ch=128",
+    "f32 128 16 300 det", "f64 8 8 40", "f64 64 64 1000 det ch=100 tall",
+    "f32 64 64 2000 ch=64 tall", "f32 64 64 2000 ch=64 tall det", "f32 256 256 2000",
+    "f32 16 4096 2000 tall", "f64 16 4096 100",
 ]
 
 
