@@ -20,7 +20,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/dpep.h"
+#include "dpep.h"
 #include "dpep_internal.h"
 
 using namespace dpep;
@@ -67,7 +67,6 @@ struct dpep_ctx {
     void *d_d0n = nullptr, *d_density = nullptr, *d_potential = nullptr;
     void *d_fx = nullptr, *d_fy = nullptr, *d_gx = nullptr, *d_gy = nullptr;
     void *d_T = nullptr, *d_Ux = nullptr, *d_Uy = nullptr;
-    uint64_t* d_acc = nullptr;
     BinPlan plan{};
     BinArgs bins{};
     void *d_twM = nullptr, *d_postM = nullptr, *d_twN = nullptr,
@@ -144,10 +143,10 @@ static void release(dpep_ctx* c)
     const BinArgs& b = c->bins;
     void* bufs[] = {c->d_px, c->d_py, c->d_sx, c->d_sy, c->d_d0n,
                     c->d_density, c->d_potential, c->d_fx, c->d_fy, c->d_gx,
-                    c->d_gy, c->d_T, c->d_Ux, c->d_Uy, c->d_acc, c->d_twM,
-                    c->d_postM, c->d_twN, c->d_postN, b.cnt, b.strip_off,
-                    b.nch, b.item_start, b.items, b.nitems, b.eidx, b.entries,
-                    b.big_list, b.big_count, b.bigflag, b.B, b.partial};
+                    c->d_gy, c->d_T, c->d_Ux, c->d_Uy, c->d_twM,
+                    c->d_postM, c->d_twN, c->d_postN, b.cnt, b.xtot, b.xoff, b.strip_off,
+                    b.nch, b.item_start, b.items, b.nitems, b.recs, b.pos, b.pos2, b.gtmp,
+                    b.bigflag, b.B, b.partial};
     for (void* p : bufs)
         if (p) (void)hipFree(p);
     for (auto& e : c->ev)
@@ -165,9 +164,7 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
                     const T* sy, int nc, T* fx, T* fy, T* dens, T* phi,
                     T* gx, T* gy, hipStream_t s)
 {
-    const bool det = (c->flags & DPEP_FLAG_DETERMINISTIC) != 0;
     const bool gather = !(c->flags & DPEP_FLAG_NO_GATHER);
-    uint64_t* acc = det ? c->d_acc : nullptr;
     const bool prof = c->profiling != 0;
     const T* d0n = (const T*)c->d_d0n;
 
@@ -177,10 +174,11 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
     const BinArgs& b = c->bins;
     if (!a.twM || !a.postM || !a.twN || !a.postN || !d0n || !dens || !fx ||
         !fy || !c->d_T || !c->d_Ux || !c->d_Uy || (a.potential && !phi) ||
-        (det && !acc) || (nc > 0 && (!px || !py || !sx || !sy)) ||
+        !b.xtot || !b.xoff ||
+        (nc > 0 && (!px || !py || !sx || !sy)) ||
         (gather && (!gx || !gy)) || !b.cnt || !b.strip_off || !b.nch ||
-        !b.item_start || !b.items || !b.nitems || !b.eidx || !b.entries ||
-        !b.big_list || !b.big_count || !b.bigflag || !b.B || !b.partial)
+        !b.item_start || !b.items || !b.nitems || !b.recs || !b.pos || !b.pos2 ||
+        !b.gtmp || !b.bigflag || !b.B || !b.partial)
         return fail(DPEP_ERR_STATE, "internal: a kernel argument is NULL");
     if (nc > c->nc_max)
         return fail(DPEP_ERR_ARG, "nc=%d exceeds nc_max=%d", nc, c->nc_max);
@@ -192,10 +190,9 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
     HIP_TRY(hipEventRecord(c->ev[0], s));
     if (prof) HIP_TRY(hipEventRecord(pe[0], s));
     HIP_TRY(launch_bin_scatter<T>(px, py, sx, sy, nc, c->grid, c->bins, d0n,
-                                  dens, acc, gather ? gx : nullptr,
-                                  gather ? gy : nullptr, s, prof ? pe + 1 : nullptr));
+                                  dens, s, prof ? pe + 1 : nullptr));
     if (prof) HIP_TRY(hipEventRecord(pe[5], s));
-    HIP_TRY(launch_row_dct<T>(c->sargs, dens, acc, d0n, dens, (T*)c->d_T, s));
+    HIP_TRY(launch_row_dct<T>(c->sargs, dens, (T*)c->d_T, s));
     if (prof) HIP_TRY(hipEventRecord(pe[6], s));
     HIP_TRY(launch_col_pass<T>(c->sargs, (T*)c->d_T, (T*)c->d_Ux, (T*)c->d_Uy, s));
     if (prof) HIP_TRY(hipEventRecord(pe[7], s));
@@ -296,6 +293,8 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
     g.bsx = (xh - xl) / M;
     g.bsy = (yh - yl) / N;
     g.inv_ba = 1.0 / (g.bsx * g.bsy);
+    g.inv_bsx = 1.0 / g.bsx;
+    g.inv_bsy = 1.0 / g.bsy;
     g.minw = M_SQRT2 * g.bsx;
     g.minh = M_SQRT2 * g.bsy;
     g.stretch = (flags & DPEP_FLAG_NO_STRETCH) ? 0 : 1;
@@ -308,7 +307,6 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
     a.wu_step = 2.0 * M_PI / M;
     a.wv_step = 2.0 * M_PI / N * (g.bsx / g.bsy);
     a.potential = (flags & DPEP_FLAG_NO_POTENTIAL) ? 0 : 1;
-    a.fix_inv = 1.0 / g.fix_scale;
 
     int rc = DPEP_OK;
     auto step = [&]() -> int {
@@ -325,32 +323,32 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
                             &c->d_T, &c->d_Ux, &c->d_Uy};
         for (void** p : mapbufs) HIP_TRY(hipMalloc(p, mnb));
         if (a.potential) HIP_TRY(hipMalloc(&c->d_potential, mnb));
-        if (flags & DPEP_FLAG_DETERMINISTIC)
-            HIP_TRY(hipMalloc((void**)&c->d_acc, (size_t)M * N * sizeof(uint64_t)));
         HIP_TRY(hipMemset(c->d_d0n, 0, mnb));
         // strip binning
-        const size_t accb = (flags & DPEP_FLAG_DETERMINISTIC) ? 8 : c->esz;
+        const size_t accb = sizeof(unsigned long long);
         BinPlan& p = c->plan;
-        p = make_bin_plan(M, N, nc_max, accb);
+        p = make_bin_plan(M, N, nc_max, c->esz);
         BinArgs& b = c->bins;
         b.S = p.S; b.R = p.R; b.lgR = p.lgR; b.G1 = 1; b.CH = p.CH; b.Wmax = p.Wmax;
         HIP_TRY(hipMalloc((void**)&b.cnt, (size_t)p.G1max * p.S * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.xtot, (size_t)kCountSlots * p.S * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.xoff, (size_t)kCountSlots * p.S * sizeof(unsigned)));
+        HIP_TRY(hipMemset(b.xtot, 0, (size_t)kCountSlots * p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.strip_off, (size_t)(p.S + 1) * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.nch, (size_t)p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.item_start, (size_t)p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.items, (size_t)p.Wmax * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.nitems, sizeof(unsigned)));
-        HIP_TRY(hipMalloc((void**)&b.eidx, p.cap * sizeof(unsigned)));
-        HIP_TRY(hipMalloc(&b.entries, p.cap * 4 * c->esz));
-        HIP_TRY(hipMalloc((void**)&b.big_list, (size_t)(nc_max > 0 ? nc_max : 1) * sizeof(unsigned)));
-        HIP_TRY(hipMalloc((void**)&b.big_count, sizeof(unsigned)));
+        HIP_TRY(hipMalloc(&b.recs, p.cap * p.rec_bytes));
+        HIP_TRY(hipMalloc((void**)&b.pos, (size_t)(nc_max > 0 ? nc_max : 1) * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.pos2, (size_t)(nc_max > 0 ? nc_max : 1) * sizeof(unsigned)));
+        HIP_TRY(hipMalloc(&b.gtmp, p.cap * 2 * c->esz));
         HIP_TRY(hipMalloc((void**)&b.bigflag, (size_t)p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc(&b.B, (size_t)M * N * accb));
         HIP_TRY(hipMalloc(&b.partial, p.partial_elems * accb));
         // B and the strip flags must start at zero; each step leaves them so.
         HIP_TRY(hipMemset(b.B, 0, (size_t)M * N * accb));
         HIP_TRY(hipMemset(b.bigflag, 0, (size_t)p.S * sizeof(unsigned)));
-        HIP_TRY(hipMemset(b.big_count, 0, sizeof(unsigned)));
         HIP_TRY(hipDeviceSynchronize());
         return dtype == DPEP_DTYPE_F32 ? upload_tables<float>(c)
                                        : upload_tables<double>(c);

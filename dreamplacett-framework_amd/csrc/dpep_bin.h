@@ -1,25 +1,45 @@
 // dpep_bin.h -- strip-binned density scatter and field gather.
 //
-// The bin map is cut into S strips of R consecutive rows (R * N accumulator
-// words fit a 64 KB LDS tile).  A counting sort puts every cell into the
-// strip(s) its x-span touches; each strip is then accumulated in LDS by the
+// The bin map is cut into S strips of R consecutive rows (R * N uint64
+// accumulators fit a 128 KB LDS tile).  A counting sort puts every cell into
+// the strip(s) its x-span touches; each strip is accumulated in LDS by the
 // workgroup that owns it and flushed with plain coalesced stores, the fixed
 // density folded in on the way.  No global atomics on the common path.
 //
-//   k_bin_count   per-workgroup strip histograms (cnt[g][s])          K1
-//   k_bin_scan    strip offsets, per-workgroup bases, chunk list      K2
-//   k_bin_fill    cells -> strip-sorted entries; tall cells -> B      K3
+//   k_bin_count   per-workgroup strip histograms; each nonzero count  K1
+//                 is added to one of kCountSlots totals per strip and
+//                 the returned old total is the workgroup's base
+//   k_bin_scan    strip offsets, slot offsets, chunk list (1 group)   K2
+//   k_bin_fill    cells -> strip-sorted records; tall cells -> B      K3
 //   k_strip_acc   one work item = (strip, chunk): LDS accumulate,     K4
 //                 flush rho = D0 + tile (+B) or a partial slot
 //   k_strip_red   strips split into several chunks: sum partials      K4r
-//   k_gather_bin  forces from the fields, walking the sorted entries  G
+//   k_gather_bin  one work item = (strip, chunk): the strip's field   G1
+//                 rows staged in LDS, each record's partial force over
+//                 the rows of this strip, in record order
+//   k_gather_out  forces back to cell order: sum of the (one or two)  G2
+//                 partials, tall cells gathered directly
+//
+// Accumulation is fixed point everywhere: round(v * 2^f) added as uint64
+// (LDS, the side map B, partial slots), with f = fix_exponent(nc_max) so a
+// bin's sum cannot overflow (each contribution is <= 1).  Integer sums are
+// exact and independent of order, so the density -- and everything computed
+// from it -- is bitwise reproducible run to run.  (On gfx950 ds_add_u64 also
+// runs about seven times faster than ds_add_f32.)
+//
+// K3 evaluates each cell's stretch and span once, in float64, and stores a
+// record in bin units relative to its first bin's edges (offsets dx, dy in
+// [0, 1), stretched extents w, h) with the packed span, the area ratio and
+// the cell index: K4 and G1 then need only short arithmetic on small
+// numbers, which float32 carries to ~1e-7 of a bin (absolute die coordinates
+// would not).  K3 also writes pos[i] and pos2[i], the records of cell i (in
+// cell order, coalesced), so G2 can write the forces in cell order instead
+// of G1 scattering them.
 //
 // A cell whose span covers more than R rows ("tall") skips the sort: K3 adds
 // it with global atomics into the side map B (zero between steps), marks the
 // strips it touches, and K4/K4r fold and re-zero those rows of B.  Every
-// other cell touches at most two strips, so the entry arrays hold 2*nc_max.
-// Deterministic mode accumulates round(v * 2^f) in uint64 everywhere (LDS,
-// B, partials); the sums are then independent of order.
+// other cell touches at most two strips, so the record array holds 2*nc_max.
 #pragma once
 
 #include <type_traits>
@@ -32,6 +52,50 @@ template <typename T> struct vec4;
 template <> struct vec4<float> { using type = float4; };
 template <> struct vec4<double> { using type = double4; };
 template <typename T> using vec4_t = typename vec4<T>::type;
+
+// Strip record: geometry in bin units relative to the edges of bin
+// (bxl, byl); bxl | nx << 16, byl | ny << 16 (nx = bxh - bxl, ny = byh - byl);
+// the stretch's area ratio; the cell index (| kSecondStrip for the copy in
+// the second strip of a cell that crosses a strip boundary).
+template <typename T> struct Rec;
+template <> struct alignas(32) Rec<float> {
+    float4 g;           // dx, dy, w, h
+    uint4 m;            // A, B, ratio bits, index
+    __device__ __forceinline__ float ratio() const { return __uint_as_float(m.z); }
+    __device__ __forceinline__ unsigned index() const { return m.w; }
+    __device__ __forceinline__ void set(float4 geo, unsigned A, unsigned B, double r, unsigned idx)
+    {
+        g = geo;
+        m = uint4{A, B, __float_as_uint((float)r), idx};
+    }
+};
+template <> struct alignas(64) Rec<double> {
+    double4 g;
+    double r;
+    unsigned A, B, idx, pad;
+    __device__ __forceinline__ double ratio() const { return r; }
+    __device__ __forceinline__ unsigned index() const { return idx; }
+    __device__ __forceinline__ void set(double4 geo, unsigned a, unsigned b_, double rr, unsigned i)
+    {
+        g = geo;
+        r = rr;
+        A = a;
+        B = b_;
+        idx = i;
+        pad = 0u;
+    }
+};
+static_assert(sizeof(Rec<float>) == 32 && sizeof(Rec<double>) == 64,
+              "record sizes are part of the buffer plan (make_bin_plan)");
+template <typename T> __device__ __forceinline__ unsigned rec_A(const Rec<T>& r);
+template <> __device__ __forceinline__ unsigned rec_A(const Rec<float>& r) { return r.m.x; }
+template <> __device__ __forceinline__ unsigned rec_A(const Rec<double>& r) { return r.A; }
+template <typename T> __device__ __forceinline__ unsigned rec_B(const Rec<T>& r);
+template <> __device__ __forceinline__ unsigned rec_B(const Rec<float>& r) { return r.m.y; }
+template <> __device__ __forceinline__ unsigned rec_B(const Rec<double>& r) { return r.B; }
+
+constexpr unsigned kPosTall = 0xFFFFFFFFu;     // pos[i]: tall cell (side map)
+constexpr unsigned kPosNone = 0xFFFFFFFEu;     // pos[i]: contributes nothing
 
 // Strips [s0, s1] a cell occupies and whether it is tall.
 __device__ __forceinline__ void cell_strips(const CellSpan& c, int R, int lgR,
@@ -51,6 +115,11 @@ __device__ __forceinline__ bool load_span(const T* px, const T* py,
                      (double)sy[i], g, c);
 }
 
+__device__ __forceinline__ unsigned long long to_fixed(double v, double scale)
+{
+    return (unsigned long long)__double2ull_rn(v * scale);
+}
+
 // ---------------------------------------------------------------------------
 // K1: per-workgroup strip histogram.
 // ---------------------------------------------------------------------------
@@ -66,10 +135,22 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_count(
     for (int s = tid; s < b.S; s += kBinThreads) hist[s] = 0u;
     __syncthreads();
     const int c0 = blockIdx.x * kCellsPerGroup;
-    const int c1 = min(c0 + kCellsPerGroup, nc);
-    for (int i = c0 + tid; i < c1; i += kBinThreads) {
+    // all loads of this thread's cells first (independent, in flight together)
+    T cx[kCellsPerThread], cy[kCellsPerThread], cw[kCellsPerThread], ch[kCellsPerThread];
+#pragma unroll
+    for (int j = 0; j < kCellsPerThread; ++j) {
+        const int i = c0 + tid + j * kBinThreads;
+        const bool ok = i < nc;
+        cx[j] = ok ? px[i] : (T)0;
+        cy[j] = ok ? py[i] : (T)0;
+        cw[j] = ok ? sx[i] : (T)0;
+        ch[j] = ok ? sy[i] : (T)0;
+    }
+#pragma unroll
+    for (int j = 0; j < kCellsPerThread; ++j) {
         CellSpan c;
-        if (!load_span(px, py, sx, sy, i, g, c)) continue;
+        if (!cell_span((double)cx[j], (double)cy[j], (double)cw[j], (double)ch[j], g, c))
+            continue;
         int s0, s1;
         bool tall;
         cell_strips(c, b.R, b.lgR, s0, s1, tall);
@@ -78,8 +159,14 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_count(
         if (s1 != s0) atomicAdd(&hist[s1], 1u);
     }
     __syncthreads();
+    // workgroup g adds into slot g % kCountSlots: a label only, it spreads the
+    // atomics over kCountSlots addresses per strip
     unsigned* row = b.cnt + (size_t)blockIdx.x * b.S;
-    for (int s = tid; s < b.S; s += kBinThreads) row[s] = hist[s];
+    unsigned* slot = b.xtot + (size_t)(blockIdx.x % kCountSlots) * b.S;
+    for (int s = tid; s < b.S; s += kBinThreads) {
+        const unsigned h = hist[s];
+        row[s] = h ? atomicAdd(&slot[s], h) : 0u;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -108,29 +195,25 @@ __device__ __forceinline__ unsigned block_exclusive_scan(unsigned v,
 
 __global__ __launch_bounds__(kScanThreads) void k_bin_scan(BinArgs b)
 {
-    // LDS: tot[S] | part[4][256] | tmp[1024]
+    // LDS: tot[S] | tmp[1024]
     extern __shared__ __align__(16) unsigned char smem[];
     unsigned* tot = reinterpret_cast<unsigned*>(smem);
-    unsigned* part = tot + b.S;
-    unsigned* tmp = part + 4 * 256;
+    unsigned* tmp = tot + b.S;
     const int tid = threadIdx.x;
-    const int S = b.S, G1 = b.G1;
-    const int q = tid >> 8, lane = tid & 255;
-    const int gq0 = (G1 * q) / 4, gq1 = (G1 * (q + 1)) / 4;
+    const int S = b.S;
 
-    // pass 1: totals per strip, in blocks of 256 strips
-    for (int sb = 0; sb < S; sb += 256) {
-        const int s = sb + lane;
-        unsigned acc = 0u;
-        if (s < S)
-            for (int gg = gq0; gg < gq1; ++gg) acc += b.cnt[(size_t)gg * S + s];
-        part[q * 256 + lane] = acc;
-        __syncthreads();
-        if (q == 0 && s < S)
-            tot[s] = part[lane] + part[256 + lane] + part[512 + lane] + part[768 + lane];
-        __syncthreads();
+    // strip totals = sum of the slot totals
+    for (int s = tid; s < S; s += kScanThreads) {
+        unsigned v[kCountSlots];
+#pragma unroll
+        for (int x = 0; x < kCountSlots; ++x) v[x] = b.xtot[(size_t)x * S + s];
+        unsigned t = 0u;
+#pragma unroll
+        for (int x = 0; x < kCountSlots; ++x) t += v[x];
+        tot[s] = t;
     }
-    // pass 2: exclusive scan of tot -> strip_off (each thread a run of strips)
+    __syncthreads();
+    // exclusive scan of the totals (each thread a run of strips)
     const int per = (S + kScanThreads - 1) / kScanThreads;
     const int r0 = min(tid * per, S), r1 = min(r0 + per, S);
     unsigned run = 0u;
@@ -142,35 +225,23 @@ __global__ __launch_bounds__(kScanThreads) void k_bin_scan(BinArgs b)
         b.strip_off[s] = base;
         tot[s] = base;          // tot now holds the strip offsets
         base += t;
-        // chunks of this strip
         const unsigned n = (t + (unsigned)b.CH - 1u) / (unsigned)b.CH;
         b.nch[s] = n > 1u ? n : 1u;
     }
-    if (tid == 0) {
-        b.strip_off[S] = total;
-        *b.big_count = 0u;
-    }
+    if (tid == 0) b.strip_off[S] = total;
     __syncthreads();
-    // pass 3: per-workgroup bases, 4 contiguous g-blocks per strip
-    for (int sb = 0; sb < S; sb += 256) {
-        const int s = sb + lane;
-        unsigned acc = 0u;
-        if (s < S)
-            for (int gg = gq0; gg < gq1; ++gg) acc += b.cnt[(size_t)gg * S + s];
-        part[q * 256 + lane] = acc;
-        __syncthreads();
-        if (s < S) {
-            unsigned off = tot[s];
-            for (int qq = 0; qq < q; ++qq) off += part[qq * 256 + lane];
-            for (int gg = gq0; gg < gq1; ++gg) {
-                const unsigned v = b.cnt[(size_t)gg * S + s];
-                b.cnt[(size_t)gg * S + s] = off;
-                off += v;
-            }
+    // slot offsets; the slot totals are consumed here and left at zero
+    for (int s = tid; s < S; s += kScanThreads) {
+        unsigned off = tot[s];
+#pragma unroll
+        for (int x = 0; x < kCountSlots; ++x) {
+            const unsigned v = b.xtot[(size_t)x * S + s];
+            b.xoff[(size_t)x * S + s] = off;
+            b.xtot[(size_t)x * S + s] = 0u;
+            off += v;
         }
-        __syncthreads();
     }
-    // pass 4: work items (strip, chunk)
+    // work items (strip, chunk)
     unsigned nrun = 0u;
     for (int s = r0; s < r1; ++s) nrun += b.nch[s];
     unsigned ntotal;
@@ -186,31 +257,41 @@ __global__ __launch_bounds__(kScanThreads) void k_bin_scan(BinArgs b)
 }
 
 // ---------------------------------------------------------------------------
-// K3: fill the strip-sorted entries; tall cells go to B; invalid cells get
-// zero force.
+// K3: fill the strip-sorted records; tall cells go to B; pos[i] for G2.
 // ---------------------------------------------------------------------------
-template <typename T, bool FIXED>
+template <typename T>
 __global__ __launch_bounds__(kBinThreads) void k_bin_fill(
     const T* __restrict__ px, const T* __restrict__ py,
     const T* __restrict__ sx, const T* __restrict__ sy, int nc, Grid g,
-    BinArgs b, T* __restrict__ gx, T* __restrict__ gy)
+    BinArgs b)
 {
-    using A = typename std::conditional<FIXED, unsigned long long, T>::type;
     extern __shared__ __align__(16) unsigned char smem[];
     unsigned* cur = reinterpret_cast<unsigned*>(smem);
     const int tid = threadIdx.x;
     const unsigned* row = b.cnt + (size_t)blockIdx.x * b.S;
-    for (int s = tid; s < b.S; s += kBinThreads) cur[s] = row[s];
+    const unsigned* xo = b.xoff + (size_t)(blockIdx.x % kCountSlots) * b.S;
+    for (int s = tid; s < b.S; s += kBinThreads) cur[s] = xo[s] + row[s];
     __syncthreads();
-    vec4_t<T>* ent = reinterpret_cast<vec4_t<T>*>(b.entries);
-    A* Bm = reinterpret_cast<A*>(b.B);
+    Rec<T>* rec = reinterpret_cast<Rec<T>*>(b.recs);
+    unsigned long long* Bm = reinterpret_cast<unsigned long long*>(b.B);
     const int c0 = blockIdx.x * kCellsPerGroup;
-    const int c1 = min(c0 + kCellsPerGroup, nc);
-    for (int i = c0 + tid; i < c1; i += kBinThreads) {
+    T cx[kCellsPerThread], cy[kCellsPerThread], cw[kCellsPerThread], chh[kCellsPerThread];
+#pragma unroll
+    for (int j = 0; j < kCellsPerThread; ++j) {
+        const int i = c0 + tid + j * kBinThreads;
+        const bool ok = i < nc;
+        cx[j] = ok ? px[i] : (T)0;
+        cy[j] = ok ? py[i] : (T)0;
+        cw[j] = ok ? sx[i] : (T)0;
+        chh[j] = ok ? sy[i] : (T)0;
+    }
+    for (int j = 0; j < kCellsPerThread; ++j) {
+        const int i = c0 + tid + j * kBinThreads;
+        if (i >= nc) break;
         CellSpan c;
-        const T x = px[i], y = py[i], w = sx[i], h = sy[i];
-        if (!cell_span((double)x, (double)y, (double)w, (double)h, g, c)) {
-            if (gx) { gx[i] = (T)0; gy[i] = (T)0; }
+        if (!cell_span((double)cx[j], (double)cy[j], (double)cw[j], (double)chh[j], g, c)) {
+            b.pos[i] = kPosNone;
+            b.pos2[i] = kPosNone;
             continue;
         }
         int s0, s1;
@@ -226,50 +307,50 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill(
                 for (int q = c.byl; q <= c.byh; ++q) {
                     const double ty = overlap_1d(c.y, c.h, g.yl, g.bsy, q);
                     if (ty <= 0.0) continue;
-                    const double v = stx * ty;
-                    if constexpr (FIXED)
-                        atomicAdd(&Bm[rowi + q], (unsigned long long)__double2ull_rn(v * g.fix_scale));
-                    else
-                        unsafeAtomicAdd(&Bm[rowi + q], (T)v);
+                    atomicAdd(&Bm[rowi + q], to_fixed(stx * ty, g.fix_scale));
                 }
             }
             for (int s = s0; s <= s1; ++s) b.bigflag[s] = 1u;
-            b.big_list[atomicAdd(b.big_count, 1u)] = (unsigned)i;
+            b.pos[i] = kPosTall;
+            b.pos2[i] = kPosNone;
             continue;
         }
-        const vec4_t<T> rec = {x, y, w, h};
+        // strip-relative record, evaluated in float64 and rounded once
+        const double ex = (c.x - (g.xl + c.bxl * g.bsx)) * g.inv_bsx;
+        const double ey = (c.y - (g.yl + c.byl * g.bsy)) * g.inv_bsy;
+        const vec4_t<T> geo = {(T)ex, (T)ey, (T)(c.w * g.inv_bsx), (T)(c.h * g.inv_bsy)};
+        const unsigned A = (unsigned)c.bxl | ((unsigned)(c.bxh - c.bxl) << 16);
+        const unsigned B = (unsigned)c.byl | ((unsigned)(c.byh - c.byl) << 16);
         const unsigned p0 = atomicAdd(&cur[s0], 1u);
-        ent[p0] = rec;
-        b.eidx[p0] = (unsigned)i;
+        rec[p0].set(geo, A, B, c.ratio, (unsigned)i);
+        b.pos[i] = p0;
+        unsigned p1 = kPosNone;
         if (s1 != s0) {
-            const unsigned p1 = atomicAdd(&cur[s1], 1u);
-            ent[p1] = rec;
-            b.eidx[p1] = (unsigned)i | kSecondStrip;
+            p1 = atomicAdd(&cur[s1], 1u);
+            rec[p1].set(geo, A, B, c.ratio, (unsigned)i | kSecondStrip);
         }
+        b.pos2[i] = p1;
     }
 }
 
-// Writes one accumulated strip value: rho = D0 + v (float modes) or the
-// fixed-point accumulator (deterministic mode, folded by the row DCT).
-template <typename T, bool FIXED>
-__device__ __forceinline__ void flush_value(
-    typename std::conditional<FIXED, unsigned long long, T>::type v,
-    size_t gi, const T* __restrict__ d0n, T* __restrict__ dens,
-    uint64_t* __restrict__ acc)
+// rho = D0 + fixed-point sum, rounded once to T.
+template <typename T>
+__device__ __forceinline__ void flush_value(unsigned long long v, size_t gi,
+                                            const T* __restrict__ d0n,
+                                            T* __restrict__ dens, double inv)
 {
-    if constexpr (FIXED) acc[gi] = (uint64_t)v;
-    else dens[gi] = d0n[gi] + v;
+    dens[gi] = (T)((double)d0n[gi] + (double)v * inv);
 }
 
 // ---------------------------------------------------------------------------
-// K4: accumulate one (strip, chunk) work item in LDS.
+// K4: accumulate one (strip, chunk) work item in an LDS tile of R x N
+// uint64 fixed-point words.
 // ---------------------------------------------------------------------------
-template <typename T, bool FIXED>
+template <typename T>
 __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
-    Grid g, BinArgs b, const T* __restrict__ d0n, T* __restrict__ dens,
-    uint64_t* __restrict__ acc)
+    Grid g, BinArgs b, const T* __restrict__ d0n, T* __restrict__ dens)
 {
-    using A = typename std::conditional<FIXED, unsigned long long, T>::type;
+    using A = unsigned long long;
     extern __shared__ __align__(16) unsigned char smem[];
     A* tile = reinterpret_cast<A*>(smem);
     const int w = blockIdx.x;
@@ -284,49 +365,77 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     // read before the barriers below: thread 0 clears it after the flush
     const bool single = b.nch[s] == 1u;
     const bool bf = b.bigflag[s] != 0u;
-    for (int e = tid; e < RN; e += kAccThreads) tile[e] = (A)0;
+    for (int e = tid; e < RN; e += kAccThreads) tile[e] = 0ull;
     __syncthreads();
 
     const unsigned e0 = b.strip_off[s] + (unsigned)chunk * (unsigned)b.CH;
     const unsigned eend = b.strip_off[s + 1];
     const unsigned e1 = min(e0 + (unsigned)b.CH, eend);
-    const vec4_t<T>* ent = reinterpret_cast<const vec4_t<T>*>(b.entries);
-    for (unsigned e = e0 + tid; e < e1; e += kAccThreads) {
-        const vec4_t<T> r = ent[e];
-        CellSpan c;
-        if (!cell_span((double)r.x, (double)r.y, (double)r.z, (double)r.w, g, c))
-            continue;
-        const double sc = c.ratio * g.inv_ba;
-        const int ka = max(c.bxl, k0), kb = min(c.bxh, k1);
-        for (int k = ka; k <= kb; ++k) {
-            const double tx = overlap_1d(c.x, c.w, g.xl, g.bsx, k);
-            if (tx <= 0.0) continue;
-            const double stx = sc * tx;
-            A* trow = tile + (k - k0) * N;
-            for (int q = c.byl; q <= c.byh; ++q) {
-                const double ty = overlap_1d(c.y, c.h, g.yl, g.bsy, q);
-                if (ty <= 0.0) continue;
-                const double v = stx * ty;
-                if constexpr (FIXED)
-                    atomicAdd(&trow[q], (unsigned long long)__double2ull_rn(v * g.fix_scale));
-                else
-                    atomicAdd(&trow[q], (T)v);
+    const Rec<T>* rec = reinterpret_cast<const Rec<T>*>(b.recs);
+    const double fs = g.fix_scale;
+    constexpr int kBatch = 4;       // record loads in flight per thread
+    for (unsigned eb = e0 + tid; eb < e1; eb += kBatch * kAccThreads) {
+        Rec<T> rb[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const unsigned e = eb + j * kAccThreads;
+            if (e < e1) rb[j] = rec[e];
+        }
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            if (eb + j * kAccThreads >= e1) continue;
+            const Rec<T>& r = rb[j];
+            const unsigned Aw = rec_A(r), Bw = rec_B(r);
+            const int bxl = (int)(Aw & 0xFFFFu), nx = (int)(Aw >> 16);
+            const int byl = (int)(Bw & 0xFFFFu), ny = (int)(Bw >> 16);
+            const int ka = max(bxl, k0), kb = min(bxl + nx, k1);
+            const T dx = r.g.x, dy = r.g.y, xr = r.g.x + r.g.z, yr = r.g.y + r.g.w;
+            const T rat = r.ratio();
+            for (int k = ka; k <= kb; ++k) {
+                const T jx = (T)(k - bxl);
+                const T tx = min(xr, jx + (T)1) - max(dx, jx);
+                if (!(tx > (T)0)) continue;
+                const T rtx = rat * tx;
+                A* trow = tile + (k - k0) * N + byl;
+                for (int q = 0; q <= ny; ++q) {
+                    const T ty = min(yr, (T)(q + 1)) - max(dy, (T)q);
+                    if (!(ty > (T)0)) continue;
+                    atomicAdd(&trow[q], to_fixed((double)(rtx * ty), fs));
+                }
             }
         }
     }
     __syncthreads();
 
     const size_t gbase = (size_t)k0 * N;
+    const double inv = 1.0 / fs;
     if (single) {
         A* Bm = reinterpret_cast<A*>(b.B);
-        for (int e = tid; e < RN; e += kAccThreads) {
-            A v = tile[e];
-            if (bf) {
-                v += Bm[gbase + e];
-                Bm[gbase + e] = (A)0;
+        if (!bf) {
+            // batches of U independent loads per thread; a tail loop takes
+            // what is left when R * N is not a multiple of U * kAccThreads
+            constexpr int U = 8;
+            int e = tid;
+            for (; e + (U - 1) * kAccThreads < RN; e += U * kAccThreads) {
+                A v[U];
+                T d[U];
+#pragma unroll
+                for (int j = 0; j < U; ++j) v[j] = tile[e + j * kAccThreads];
+#pragma unroll
+                for (int j = 0; j < U; ++j) d[j] = d0n[gbase + e + j * kAccThreads];
+#pragma unroll
+                for (int j = 0; j < U; ++j)
+                    dens[gbase + e + j * kAccThreads] = (T)((double)d[j] + (double)v[j] * inv);
             }
-            flush_value<T, FIXED>(v, gbase + e, d0n, dens, acc);
+            for (; e < RN; e += kAccThreads) flush_value<T>(tile[e], gbase + e, d0n, dens, inv);
+        } else {
+            for (int e = tid; e < RN; e += kAccThreads) {
+                const A v = tile[e] + Bm[gbase + e];
+                Bm[gbase + e] = 0ull;
+                flush_value<T>(v, gbase + e, d0n, dens, inv);
+            }
         }
+        __syncthreads();   // every thread has read bigflag[s]
         if (bf && tid == 0) b.bigflag[s] = 0u;
     } else {
         A* slot = reinterpret_cast<A*>(b.partial) + (size_t)w * RN;
@@ -337,12 +446,11 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
 // ---------------------------------------------------------------------------
 // K4r: strips split into several chunks: rho = D0 + sum of partials (+B).
 // ---------------------------------------------------------------------------
-template <typename T, bool FIXED>
+template <typename T>
 __global__ __launch_bounds__(kAccThreads) void k_strip_red(
-    Grid g, BinArgs b, const T* __restrict__ d0n, T* __restrict__ dens,
-    uint64_t* __restrict__ acc)
+    Grid g, BinArgs b, const T* __restrict__ d0n, T* __restrict__ dens)
 {
-    using A = typename std::conditional<FIXED, unsigned long long, T>::type;
+    using A = unsigned long long;
     const int s = blockIdx.x;
     const unsigned n = b.nch[s];
     if (n == 1u) return;
@@ -353,22 +461,103 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_red(
     const A* part = reinterpret_cast<const A*>(b.partial);
     A* Bm = reinterpret_cast<A*>(b.B);
     const bool bf = b.bigflag[s] != 0u;
+    const double inv = 1.0 / g.fix_scale;
     for (int e = tid; e < RN; e += kAccThreads) {
-        A v = (A)0;
+        A v = 0ull;
         for (unsigned c = 0; c < n; ++c) v += part[(size_t)(w0 + c) * RN + e];
         if (bf) {
             v += Bm[gbase + e];
-            Bm[gbase + e] = (A)0;
+            Bm[gbase + e] = 0ull;
         }
-        flush_value<T, FIXED>(v, gbase + e, d0n, dens, acc);
+        flush_value<T>(v, gbase + e, d0n, dens, inv);
     }
     __syncthreads();   // every thread has read bigflag[s]
     if (bf && tid == 0) b.bigflag[s] = 0u;
 }
 
 // ---------------------------------------------------------------------------
-// G: per-cell field gather over the strip-sorted entries (each non-tall cell
-// once, through its first strip) and the tall-cell list.
+// G1: one (strip, chunk) work item.  The strip's field rows are staged in
+// LDS, RG rows at a time (RG = R for float32; fewer for float64), and each
+// record's partial force over the rows of this strip is written (first row
+// group) or added (later groups) to gtmp in record order.
+// ---------------------------------------------------------------------------
+template <typename T>
+__host__ __device__ constexpr int gather_rows(int R, int N)
+{
+    int rg = R;
+    while (rg > 1 && (size_t)rg * N * 2 * sizeof(T) > kTileBytes) rg >>= 1;
+    return rg;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kAccThreads) void k_gather_bin(
+    Grid g, BinArgs b, const T* __restrict__ fx, const T* __restrict__ fy)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int w = blockIdx.x;
+    if (w >= (int)*b.nitems) return;            // uniform across the group
+    const unsigned item = b.items[w];
+    const int s = (int)(item & 0xFFFFu);
+    const int chunk = (int)(item >> 16);
+    const int tid = threadIdx.x;
+    const int R = b.R, N = g.N;
+    const int RG = gather_rows<T>(R, N);
+    T* lfx = reinterpret_cast<T*>(smem);
+    T* lfy = lfx + (size_t)RG * N;
+    const unsigned e0 = b.strip_off[s] + (unsigned)chunk * (unsigned)b.CH;
+    const unsigned e1 = min(e0 + (unsigned)b.CH, b.strip_off[s + 1]);
+    const Rec<T>* rec = reinterpret_cast<const Rec<T>*>(b.recs);
+    vec2_t<T>* out = reinterpret_cast<vec2_t<T>*>(b.gtmp);
+    const T ba = (T)(g.bsx * g.bsy);
+    for (int kg0 = s * R; kg0 < s * R + R; kg0 += RG) {
+        const int kg1 = kg0 + RG - 1;
+        __syncthreads();                    // previous group's readers done
+        const size_t gb = (size_t)kg0 * N;
+        for (int e = tid; e < RG * N; e += kAccThreads) {
+            lfx[e] = fx[gb + e];
+            lfy[e] = fy[gb + e];
+        }
+        __syncthreads();
+        const bool first = kg0 == s * R;
+        for (unsigned e = e0 + tid; e < e1; e += kAccThreads) {
+            const Rec<T> r = rec[e];
+            const unsigned Aw = rec_A(r), Bw = rec_B(r);
+            const int bxl = (int)(Aw & 0xFFFFu), nx = (int)(Aw >> 16);
+            const int byl = (int)(Bw & 0xFFFFu), ny = (int)(Bw >> 16);
+            const int ka = max(bxl, kg0), kb = min(bxl + nx, kg1);
+            const T dx = r.g.x, dy = r.g.y, xr = r.g.x + r.g.z, yr = r.g.y + r.g.w;
+            T ax = (T)0, ay = (T)0;
+            for (int k = ka; k <= kb; ++k) {
+                const T jx = (T)(k - bxl);
+                const T tx = min(xr, jx + (T)1) - max(dx, jx);
+                if (!(tx > (T)0)) continue;
+                const T* rx = lfx + (size_t)(k - kg0) * N + byl;
+                const T* ry = lfy + (size_t)(k - kg0) * N + byl;
+                T sx_ = (T)0, sy_ = (T)0;
+                for (int q = 0; q <= ny; ++q) {
+                    const T ty = min(yr, (T)(q + 1)) - max(dy, (T)q);
+                    if (!(ty > (T)0)) continue;
+                    sx_ += ty * rx[q];
+                    sy_ += ty * ry[q];
+                }
+                ax += tx * sx_;
+                ay += tx * sy_;
+            }
+            const T sc = r.ratio() * ba;
+            vec2_t<T> v = {sc * ax, sc * ay};
+            if (!first) {
+                const vec2_t<T> o = out[e];
+                v.x += o.x;
+                v.y += o.y;
+            }
+            out[e] = v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// G2: forces in cell order: gx[i], gy[i] from the record pos[i]; tall cells
+// are gathered here in float64; cells that contribute nothing get zero.
 // ---------------------------------------------------------------------------
 template <typename T>
 __device__ __forceinline__ void gather_one(const CellSpan& c, const Grid& g,
@@ -395,35 +584,35 @@ __device__ __forceinline__ void gather_one(const CellSpan& c, const Grid& g,
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void k_gather_bin(
+__global__ __launch_bounds__(256) void k_gather_out(
     const T* __restrict__ px, const T* __restrict__ py,
-    const T* __restrict__ sx, const T* __restrict__ sy, Grid g, BinArgs b,
-    const T* __restrict__ fx, const T* __restrict__ fy, T* __restrict__ gx,
-    T* __restrict__ gy)
+    const T* __restrict__ sx, const T* __restrict__ sy, int nc, Grid g,
+    BinArgs b, const T* __restrict__ fx, const T* __restrict__ fy,
+    T* __restrict__ gx, T* __restrict__ gy)
 {
-    const unsigned total = b.strip_off[b.S];
-    const unsigned nbig = *b.big_count;
-    const unsigned stride = gridDim.x * blockDim.x;
-    const vec4_t<T>* ent = reinterpret_cast<const vec4_t<T>*>(b.entries);
-    for (unsigned e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
-        const unsigned id = b.eidx[e];
-        if (id & kSecondStrip) continue;
-        const vec4_t<T> r = ent[e];
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nc) return;
+    const unsigned p = b.pos[i], p2 = b.pos2[i];
+    const vec2_t<T>* res = reinterpret_cast<const vec2_t<T>*>(b.gtmp);
+    T ox = (T)0, oy = (T)0;
+    if (p < kPosNone) {
+        const vec2_t<T> v = res[p];
+        ox = v.x;
+        oy = v.y;
+        if (p2 < kPosNone) {
+            const vec2_t<T> v2 = res[p2];
+            ox += v2.x;
+            oy += v2.y;
+        }
+    } else if (p == kPosTall) {
         CellSpan c;
         double ax = 0.0, ay = 0.0;
-        if (cell_span((double)r.x, (double)r.y, (double)r.z, (double)r.w, g, c))
-            gather_one(c, g, fx, fy, ax, ay);
-        gx[id] = (T)ax;
-        gy[id] = (T)ay;
+        if (load_span(px, py, sx, sy, i, g, c)) gather_one(c, g, fx, fy, ax, ay);
+        ox = (T)ax;
+        oy = (T)ay;
     }
-    for (unsigned t = blockIdx.x * blockDim.x + threadIdx.x; t < nbig; t += stride) {
-        const unsigned i = b.big_list[t];
-        CellSpan c;
-        double ax = 0.0, ay = 0.0;
-        if (load_span(px, py, sx, sy, (int)i, g, c)) gather_one(c, g, fx, fy, ax, ay);
-        gx[i] = (T)ax;
-        gy[i] = (T)ay;
-    }
+    gx[i] = ox;
+    gy[i] = oy;
 }
 
 }  // namespace dpep

@@ -13,38 +13,26 @@ static unsigned g1_of(int nc)
 template <typename T>
 hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
                               const T* sy, int nc, const Grid& g,
-                              BinArgs b, const T* d0n, T* dens,
-                              uint64_t* acc, T* gx, T* gy, hipStream_t s,
+                              BinArgs b, const T* d0n, T* dens, hipStream_t s,
                               hipEvent_t* ev)
 {
-    const bool fixed = acc != nullptr;
     b.G1 = (int)g1_of(nc);
-    const size_t acc_bytes = fixed ? 8 : sizeof(T);
-    const size_t tile = (size_t)b.R * g.N * acc_bytes;
+    const size_t tile = (size_t)b.R * g.N * sizeof(unsigned long long);
     const size_t hist = (size_t)b.S * sizeof(unsigned);
     hipError_t e;
     k_bin_count<T><<<b.G1, kBinThreads, hist, s>>>(px, py, sx, sy, nc, g, b);
     if ((e = hipGetLastError())) return e;
     if (ev && (e = hipEventRecord(ev[0], s))) return e;
-    k_bin_scan<<<1, kScanThreads, (size_t)(b.S + 2048) * sizeof(unsigned), s>>>(b);
+    k_bin_scan<<<1, kScanThreads, (size_t)(b.S + kScanThreads) * sizeof(unsigned), s>>>(b);
     if ((e = hipGetLastError())) return e;
     if (ev && (e = hipEventRecord(ev[1], s))) return e;
-    if (fixed)
-        k_bin_fill<T, true><<<b.G1, kBinThreads, hist, s>>>(px, py, sx, sy, nc, g, b, gx, gy);
-    else
-        k_bin_fill<T, false><<<b.G1, kBinThreads, hist, s>>>(px, py, sx, sy, nc, g, b, gx, gy);
+    k_bin_fill<T><<<b.G1, kBinThreads, hist, s>>>(px, py, sx, sy, nc, g, b);
     if ((e = hipGetLastError())) return e;
     if (ev && (e = hipEventRecord(ev[2], s))) return e;
-    if (fixed)
-        k_strip_acc<T, true><<<b.Wmax, kAccThreads, tile, s>>>(g, b, d0n, dens, acc);
-    else
-        k_strip_acc<T, false><<<b.Wmax, kAccThreads, tile, s>>>(g, b, d0n, dens, acc);
+    k_strip_acc<T><<<b.Wmax, kAccThreads, tile, s>>>(g, b, d0n, dens);
     if ((e = hipGetLastError())) return e;
     if (ev && (e = hipEventRecord(ev[3], s))) return e;
-    if (fixed)
-        k_strip_red<T, true><<<b.S, kAccThreads, 0, s>>>(g, b, d0n, dens, acc);
-    else
-        k_strip_red<T, false><<<b.S, kAccThreads, 0, s>>>(g, b, d0n, dens, acc);
+    k_strip_red<T><<<b.S, kAccThreads, 0, s>>>(g, b, d0n, dens);
     return hipGetLastError();
 }
 
@@ -55,22 +43,25 @@ hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
                              T* gx, T* gy, hipStream_t s)
 {
     if (nc <= 0) return hipSuccess;
-    long long blocks = ((long long)nc * 5 / 4 + 255) / 256;
-    if (blocks > 8192) blocks = 8192;
-    if (blocks < 1) blocks = 1;
-    k_gather_bin<T><<<(unsigned)blocks, 256, 0, s>>>(px, py, sx, sy, g, b, fx, fy, gx, gy);
+    const size_t lds = (size_t)gather_rows<T>(b.R, g.N) * g.N * 2 * sizeof(T);
+    k_gather_bin<T><<<b.Wmax, kAccThreads, lds, s>>>(g, b, fx, fy);
+    hipError_t e = hipGetLastError();
+    if (e) return e;
+    k_gather_out<T><<<(unsigned)((nc + 255) / 256), 256, 0, s>>>(px, py, sx, sy, nc, g, b,
+                                                                fx, fy, gx, gy);
     return hipGetLastError();
 }
 
 template <typename T>
 static hipError_t prepare_bin_type()
 {
-    hipError_t e;
-    if ((e = hipFuncSetAttribute((const void*)k_strip_acc<T, false>,
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, 65536)))
-        return e;
-    return hipFuncSetAttribute((const void*)k_strip_acc<T, true>,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, 65536);
+    hipError_t e = hipFuncSetAttribute((const void*)k_strip_acc<T>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)kTileBytes);
+    if (e) return e;
+    return hipFuncSetAttribute((const void*)k_gather_bin<T>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)kTileBytes);
 }
 
 hipError_t bin_prepare()
@@ -82,13 +73,11 @@ hipError_t bin_prepare()
 
 template hipError_t launch_bin_scatter<float>(const float*, const float*, const float*,
                                               const float*, int, const Grid&, BinArgs,
-                                              const float*, float*, uint64_t*, float*,
-                                              float*, hipStream_t, hipEvent_t*);
+                                              const float*, float*, hipStream_t, hipEvent_t*);
 template hipError_t launch_bin_scatter<double>(const double*, const double*,
                                                const double*, const double*, int,
                                                const Grid&, BinArgs, const double*,
-                                               double*, uint64_t*, double*, double*,
-                                               hipStream_t, hipEvent_t*);
+                                               double*, hipStream_t, hipEvent_t*);
 template hipError_t launch_bin_gather<float>(const float*, const float*, const float*,
                                              const float*, int, const Grid&,
                                              const BinArgs&, const float*, const float*,

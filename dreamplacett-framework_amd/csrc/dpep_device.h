@@ -16,12 +16,13 @@ struct Grid {
     double xl, yl, xh, yh;    // die
     double bsx, bsy;          // bin sizes
     double inv_ba;            // 1 / (bsx * bsy)
+    double inv_bsx, inv_bsy;  // 1 / bsx, 1 / bsy
     double minw, minh;        // sqrt2 * bsx, sqrt2 * bsy (stretch floor)
-    double fix_scale;         // 2^fix_exponent(nc_max) (deterministic mode)
+    double fix_scale;         // 2^fix_exponent(nc_max): fixed-point scale
     int stretch;              // 1: DREAMPlace small-cell stretch
 };
 
-// Fixed-point scale of the deterministic accumulator: each contribution
+// Fixed-point scale of the density accumulators: each contribution
 // ratio * tx * ty / bin_area is at most 1 (tx <= bsx, ty <= bsy, ratio <= 1),
 // so a bin's sum is below nc_max and round(v * 2^f) with
 // f = 62 - ceil(log2(nc_max)) (capped to [20, 52]) never overflows the
@@ -58,6 +59,22 @@ __device__ __forceinline__ C cmul_mi(C a)
 }
 
 // ---------------------------------------------------------------------------
+// XCD-aware block numbering.  MI355X dispatches workgroup b to XCD b % 8;
+// this returns a logical index such that logical blocks
+// [x * n/8, (x+1) * n/8) all run on XCD x, so consecutive logical blocks
+// share that XCD's L2.  Blocks beyond the largest multiple of 8 keep their
+// index.  A bijection on [0, n) whatever the hardware mapping is.
+// ---------------------------------------------------------------------------
+constexpr int kNumXcd = 8;
+
+__device__ __forceinline__ unsigned xcd_logical_block(unsigned b, unsigned n)
+{
+    const unsigned per = n / kNumXcd;
+    if (b >= per * kNumXcd) return b;
+    return (b % kNumXcd) * per + b / kNumXcd;
+}
+
+// ---------------------------------------------------------------------------
 // Cell geometry: stretch, bin span, 1-D overlap.  Evaluated in float64 with
 // contraction disabled so the GPU reproduces the float64 oracle's spans.
 // ---------------------------------------------------------------------------
@@ -65,6 +82,20 @@ struct CellSpan {
     double x, y, w, h, ratio;
     int bxl, bxh, byl, byh;
 };
+
+// Index of the bin containing v (origin + k*bs <= v < origin + (k+1)*bs for
+// the edges as computed in float64): reciprocal-multiply estimate corrected
+// against the exact edges (the reference's correct_bin_idx idea,
+// kernels/v4_compute.cpp:91-102); no float64 division.
+__device__ __forceinline__ double floor_bin(double v, double origin,
+                                            double bs, double inv)
+{
+#pragma clang fp contract(off)
+    double k = floor((v - origin) * inv);
+    if (origin + k * bs > v) k -= 1.0;
+    else if (origin + (k + 1.0) * bs <= v) k += 1.0;
+    return k;
+}
 
 __device__ __forceinline__ bool cell_span(double px, double py, double sx,
                                           double sy, const Grid& g,
@@ -82,10 +113,10 @@ __device__ __forceinline__ bool cell_span(double px, double py, double sx,
         y = py + 0.5 * (sy - h);
         ratio = (sx * sy) / (w * h);
     }
-    double fxl = floor((x - g.xl) / g.bsx);
-    double fxh = floor((x + w - g.xl) / g.bsx);
-    double fyl = floor((y - g.yl) / g.bsy);
-    double fyh = floor((y + h - g.yl) / g.bsy);
+    double fxl = floor_bin(x, g.xl, g.bsx, g.inv_bsx);
+    double fxh = floor_bin(x + w, g.xl, g.bsx, g.inv_bsx);
+    double fyl = floor_bin(y, g.yl, g.bsy, g.inv_bsy);
+    double fyh = floor_bin(y + h, g.yl, g.bsy, g.inv_bsy);
     fxl = fxl < 0.0 ? 0.0 : fxl;
     fyl = fyl < 0.0 ? 0.0 : fyl;
     fxh = fxh > (double)(g.M - 1) ? (double)(g.M - 1) : fxh;

@@ -26,7 +26,6 @@ struct SpectralArgs {
     double wu_step;     // 2 pi / M
     double wv_step;     // 2 pi / N * bsx / bsy
     int potential;      // compute the potential map
-    double fix_inv;     // 1 / Grid::fix_scale (deterministic mode)
     const void* twM;    // exp(-2 pi i m / M), m < M
     const void* postM;  // exp(-i pi k / 2M), k <= M/2
     const void* twN;
@@ -35,9 +34,8 @@ struct SpectralArgs {
 
 // Launchers (return hipError_t of the launch).  T = float or double.
 template <typename T>
-hipError_t launch_row_dct(const SpectralArgs& a, const T* density_in,
-                          const uint64_t* acc, const T* d0n, T* density_out,
-                          T* Tt, hipStream_t s);
+hipError_t launch_row_dct(const SpectralArgs& a, const T* density, T* Tt,
+                          hipStream_t s);
 template <typename T>
 hipError_t launch_col_pass(const SpectralArgs& a, T* Tt, T* Ux, T* Uy,
                            hipStream_t s);
@@ -47,10 +45,11 @@ hipError_t launch_row_inv(const SpectralArgs& a, const T* Ux, const T* Uy,
 // ---------------------------------------------------------------------------
 // Strip binning (kernels in dpep_bin.h)
 // ---------------------------------------------------------------------------
-constexpr int kBinThreads = 512;       // K1 / K3 workgroup size
-constexpr int kCellsPerThread = 16;    // K1 / K3 cells per thread
+constexpr int kBinThreads = 256;       // K1 / K3 workgroup size
+constexpr int kCellsPerThread = 8;     // K1 / K3 cells per thread
 constexpr int kCellsPerGroup = kBinThreads * kCellsPerThread;
-constexpr int kAccThreads = 512;       // K4 / K4r workgroup size
+constexpr int kAccThreads = 1024;      // K4 / K4r workgroup size
+constexpr int kCountSlots = 8;         // strip-total counters per strip
 constexpr int kScanThreads = 1024;     // K2 (one workgroup)
 constexpr unsigned kSecondStrip = 0x80000000u;
 
@@ -60,35 +59,39 @@ struct BinArgs {
     int G1;                 // K1/K3 workgroups of this step
     int CH;                 // entries per K4 work item (chunk)
     int Wmax;               // capacity of the work-item list
-    unsigned* cnt;          // [G1max][S] counts, then bases (in place)
+    unsigned* cnt;          // [G1max][S] base of workgroup g in its slot
+    unsigned* xtot;         // [kCountSlots][S] slot totals (zero between steps)
+    unsigned* xoff;         // [kCountSlots][S] first entry of each slot
     unsigned* strip_off;    // [S + 1] entry offset of each strip
     unsigned* nch;          // [S] chunks per strip
     unsigned* item_start;   // [S] first work item of each strip
     unsigned* items;        // [Wmax] strip | chunk << 16
     unsigned* nitems;       // [1]
-    unsigned* eidx;         // [2 nc_max] cell index | kSecondStrip
-    void* entries;          // [2 nc_max] vec4 (px, py, sx, sy)
-    unsigned* big_list;     // [nc_max] tall cells
-    unsigned* big_count;    // [1]
+    void* recs;             // [2 nc_max] strip records (Rec<T>)
+    unsigned* pos;          // [nc_max] record of cell i, or kPosTall / kPosNone
+    unsigned* pos2;         // [nc_max] second-strip record of cell i, or kPosNone
+    void* gtmp;             // [2 nc_max] vec2 forces in record order
     unsigned* bigflag;      // [S] strip has rows in B
-    void* B;                // [M*N] accumulator type, zero between steps
-    void* partial;          // [Wmax][R*N] accumulator type
+    void* B;                // [M*N] uint64, zero between steps
+    void* partial;          // [Wmax][R*N] uint64
 };
 
 // Host-side sizing of the binning buffers (shared with the CPU emulator).
+constexpr size_t kTileBytes = 131072;  // LDS tile of K4 (uint64 words) and G1
+
 struct BinPlan {
     int S, R, lgR, G1max, CH, Wmax;
-    size_t cap;             // entries (2 per cell)
-    size_t acc_bytes;       // accumulator element size
+    size_t cap;             // records (2 per cell)
+    size_t rec_bytes;       // sizeof(Rec<T>): 32 (float) or 64 (double)
     size_t partial_elems;   // Wmax * R * N
 };
 
-inline BinPlan make_bin_plan(int M, int N, int nc_max, size_t acc_bytes)
+inline BinPlan make_bin_plan(int M, int N, int nc_max, size_t elem_bytes)
 {
     BinPlan p{};
-    p.acc_bytes = acc_bytes;
+    p.rec_bytes = elem_bytes == 4 ? 32 : 64;
     int R = 8;
-    while (R > 1 && (size_t)R * N * acc_bytes > 65536) R >>= 1;
+    while (R > 1 && (size_t)R * N * 8 > kTileBytes) R >>= 1;
     if (R > M) R = M;
     p.R = R;
     p.lgR = 0;
@@ -106,13 +109,13 @@ inline BinPlan make_bin_plan(int M, int N, int nc_max, size_t acc_bytes)
     return p;
 }
 
-// Strip-binned scatter (K1..K4r) and gather; ev (nullable) receives 4
-// events recorded after K1, K2, K3 and K4.
+// Strip-binned scatter (K1..K4r) and gather (G1, G2); ev (nullable)
+// receives 4 events recorded after K1, K2, K3 and K4.
 template <typename T>
 hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
                               const T* sy, int nc, const Grid& g, BinArgs b,
-                              const T* d0n, T* dens, uint64_t* acc, T* gx,
-                              T* gy, hipStream_t s, hipEvent_t* ev);
+                              const T* d0n, T* dens, hipStream_t s,
+                              hipEvent_t* ev);
 template <typename T>
 hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
                              const T* sy, int nc, const Grid& g,

@@ -122,14 +122,10 @@ __device__ __forceinline__ vec2_t<T> pack2(vec2_t<T> v1, vec2_t<T> v2)
 
 // ---------------------------------------------------------------------------
 // P1: forward DCT-II along y of 2F rows of rho; writes T (tiled).
-// SRC 0: rho read from density_in.  SRC 1: rho = d0n + acc * 2^-f, also
-// written to density_out (deterministic accumulation).
 // ---------------------------------------------------------------------------
-template <typename T, int L, int F, int SRC>
+template <typename T, int L, int F>
 __global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_dct(
-    SpectralArgs a, const T* __restrict__ density_in,
-    const uint64_t* __restrict__ acc, const T* __restrict__ d0n,
-    T* __restrict__ density_out, T* __restrict__ Tt)
+    SpectralArgs a, const T* __restrict__ density_in, T* __restrict__ Tt)
 {
     using C = vec2_t<T>;
     constexpr int E = fft_e(L), TPF = L / E, NT = F * TPF, LP = lds_len(L);
@@ -144,13 +140,7 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_dct(
 #pragma unroll 4
     for (int e = tid; e < TX * L; e += NT) {
         const int r = e / L, m = e % L;
-        T val;
-        if constexpr (SRC == 0) {
-            val = density_in[base + e];
-        } else {
-            val = (T)((double)d0n[base + e] + (double)acc[base + e] * a.fix_inv);
-            density_out[base + e] = val;
-        }
+        const T val = density_in[base + e];
         comp<T>(sb[(r >> 1) * LP + lds_pad(makhoul_pos<L>(m))], r & 1) = val;
     }
     __syncthreads();

@@ -46,18 +46,14 @@ static hipError_t dispatch_len(int L, Fn&& fn)
 }
 
 template <typename T>
-hipError_t launch_row_dct(const SpectralArgs& a, const T* density_in,
-                          const uint64_t* acc, const T* d0n, T* density_out,
-                          T* Tt, hipStream_t s)
+hipError_t launch_row_dct(const SpectralArgs& a, const T* density, T* Tt,
+                          hipStream_t s)
 {
     return dispatch_len<T>(a.N, [&](auto lc) -> hipError_t {
         constexpr int L = decltype(lc)::value;
         constexpr int F = fpw<T>(L);
         const dim3 grid(a.M / (2 * F)), block(threads_of<T, L>());
-        if (acc)
-            k_row_dct<T, L, F, 1><<<grid, block, lds_bytes<T, L>(), s>>>(a, density_in, acc, d0n, density_out, Tt);
-        else
-            k_row_dct<T, L, F, 0><<<grid, block, lds_bytes<T, L>(), s>>>(a, density_in, acc, d0n, density_out, Tt);
+        k_row_dct<T, L, F><<<grid, block, lds_bytes<T, L>(), s>>>(a, density, Tt);
         return hipGetLastError();
     });
 }
@@ -96,10 +92,7 @@ static hipError_t prepare_len()
     constexpr int F = fpw<T>(L);
     const int bytes = (int)lds_bytes<T, L>();
     hipError_t e;
-    if ((e = hipFuncSetAttribute((const void*)k_row_dct<T, L, F, 0>,
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, bytes)))
-        return e;
-    if ((e = hipFuncSetAttribute((const void*)k_row_dct<T, L, F, 1>,
+    if ((e = hipFuncSetAttribute((const void*)k_row_dct<T, L, F>,
                                  hipFuncAttributeMaxDynamicSharedMemorySize, bytes)))
         return e;
     if ((e = hipFuncSetAttribute((const void*)k_col_pass<T, L, F>,
@@ -136,11 +129,9 @@ hipError_t spectral_prepare()
 }
 
 template hipError_t launch_row_dct<float>(const SpectralArgs&, const float*,
-                                          const uint64_t*, const float*,
-                                          float*, float*, hipStream_t);
+                                          float*, hipStream_t);
 template hipError_t launch_row_dct<double>(const SpectralArgs&, const double*,
-                                           const uint64_t*, const double*,
-                                           double*, double*, hipStream_t);
+                                           double*, hipStream_t);
 template hipError_t launch_col_pass<float>(const SpectralArgs&, float*, float*,
                                            float*, hipStream_t);
 template hipError_t launch_col_pass<double>(const SpectralArgs&, double*,

@@ -49,8 +49,10 @@ extern "C" {
 #define DPEP_DTYPE_F64 1
 
 /* flags for dpep_create */
-#define DPEP_FLAG_DETERMINISTIC 0x1u /* int64 fixed-point bin accumulation:
-                                        run-to-run bitwise reproducible    */
+#define DPEP_FLAG_DETERMINISTIC 0x1u /* accepted for compatibility: every
+                                        mode accumulates the density in
+                                        uint64 fixed point and is bitwise
+                                        reproducible run to run           */
 #define DPEP_FLAG_NO_POTENTIAL 0x2u  /* skip the potential map             */
 #define DPEP_FLAG_NO_STRETCH 0x4u    /* no sqrt2*bin stretch, ratio = 1
                                         (the TT path's semantics,

@@ -68,6 +68,18 @@ typedef struct {
     int byl, byh;      /* inclusive bin span along y (clipped to [0,N))  */
 } cell_geom;
 
+/* Index of the bin containing v: the k with origin + k*bs <= v <
+ * origin + (k+1)*bs for the bin edges as computed in floating point.  The
+ * reciprocal-multiply estimate is corrected against those exact edges, the
+ * approach of the reference's correct_bin_idx (kernels/v4_compute.cpp:91-102). */
+double oracle_floor_bin(double v, double origin, double bs, double inv)
+{
+    double k = floor((v - origin) * inv);
+    if (origin + k * bs > v) k -= 1.0;
+    else if (origin + (k + 1.0) * bs <= v) k += 1.0;
+    return k;
+}
+
 /* Returns 1 when the cell contributes, 0 for padding / degenerate cells.   */
 int oracle_cell_geom(double px, double py, double sx, double sy,
                      int M, int N, double xl, double yl, double xh, double yh,
@@ -89,10 +101,11 @@ int oracle_cell_geom(double px, double py, double sx, double sy,
         y = py + 0.5 * (sy - h);
         ratio = (sx * sy) / (w * h);
     }
-    double fxl = floor((x - xl) / bsx);
-    double fxh = floor((x + w - xl) / bsx);
-    double fyl = floor((y - yl) / bsy);
-    double fyh = floor((y + h - yl) / bsy);
+    const double ibx = 1.0 / bsx, iby = 1.0 / bsy;
+    double fxl = oracle_floor_bin(x, xl, bsx, ibx);
+    double fxh = oracle_floor_bin(x + w, xl, bsx, ibx);
+    double fyl = oracle_floor_bin(y, yl, bsy, iby);
+    double fyh = oracle_floor_bin(y + h, yl, bsy, iby);
     if (fxl < 0.0) fxl = 0.0;
     if (fyl < 0.0) fyl = 0.0;
     if (fxh > M - 1) fxh = M - 1;

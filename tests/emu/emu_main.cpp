@@ -79,8 +79,10 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     Grid g{};
     g.M = M; g.N = N; g.xl = xl; g.yl = yl; g.xh = xh; g.yh = yh;
     g.bsx = (xh - xl) / M; g.bsy = (yh - yl) / N; g.inv_ba = 1.0 / (g.bsx * g.bsy);
+    g.inv_bsx = 1.0 / g.bsx; g.inv_bsy = 1.0 / g.bsy;
     g.minw = M_SQRT2 * g.bsx; g.minh = M_SQRT2 * g.bsy; g.stretch = 1;
     g.fix_scale = ldexp(1.0, fix_exponent(nc));
+    (void)det;
     std::mt19937_64 rng(1234);
     std::uniform_real_distribution<double> U(0, 1);
     T* px = exact<T>(nc); T* py = exact<T>(nc); T* sx = exact<T>(nc); T* sy = exact<T>(nc);
@@ -96,7 +98,6 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     T* d0n = exact<T>(mn); T* dens = exact<T>(mn); T* phi = pot ? exact<T>(mn) : nullptr;
     T* fx = exact<T>(mn); T* fy = exact<T>(mn); T* Tt = exact<T>(mn); T* Ux = exact<T>(mn);
     T* Uy = exact<T>(mn); T* gx = exact<T>(nc); T* gy = exact<T>(nc);
-    uint64_t* acc = det ? exact<uint64_t>(mn) : nullptr;
     for (size_t i = 0; i < mn; ++i) d0n[i] = (T)(0.5 * U(rng));
     auto twM = table<T>(M, false), twN = table<T>(N, false);
     auto poM = table<T>(M, true), poN = table<T>(N, true);
@@ -108,11 +109,10 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     a.M = M; a.N = N;
     a.tiles.TX = 2 * fpw<T>(N); a.tiles.TV = 2 * fpw<T>(M);
     a.wu_step = 2 * M_PI / M; a.wv_step = 2 * M_PI / N * (g.bsx / g.bsy);
-    a.potential = pot; a.fix_inv = 1.0 / g.fix_scale; a.twM = d_twM; a.postM = d_poM; a.twN = d_twN; a.postN = d_poN;
+    a.potential = pot; a.twM = d_twM; a.postM = d_poM; a.twN = d_twN; a.postN = d_poN;
 
     // strip binning buffers, exact sizes
-    const size_t accb = det ? 8 : sizeof(T);
-    BinPlan p = make_bin_plan(M, N, nc, accb);
+    BinPlan p = make_bin_plan(M, N, nc, sizeof(T));
     if (ch > 0) {
         p.CH = ch;
         p.Wmax = p.S + (int)((p.cap + ch - 1) / ch) + 1;
@@ -123,41 +123,42 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     b.G1 = (nc + kCellsPerGroup - 1) / kCellsPerGroup;
     if (b.G1 < 1) b.G1 = 1;
     b.cnt = exact<unsigned>((size_t)b.G1 * p.S);
+    b.xtot = exact<unsigned>((size_t)kCountSlots * p.S);
+    b.xoff = exact<unsigned>((size_t)kCountSlots * p.S);
+    memset(b.xtot, 0, (size_t)kCountSlots * p.S * sizeof(unsigned));
     b.strip_off = exact<unsigned>(p.S + 1);
     b.nch = exact<unsigned>(p.S);
     b.item_start = exact<unsigned>(p.S);
     b.items = exact<unsigned>(p.Wmax);
     b.nitems = exact<unsigned>(1);
-    b.eidx = exact<unsigned>(p.cap);
-    b.entries = exact<vec4_t<T>>(p.cap);
-    b.big_list = exact<unsigned>(nc > 0 ? nc : 1);
-    b.big_count = exact<unsigned>(1);
+    b.recs = malloc(p.cap * p.rec_bytes);
+    if (sizeof(Rec<T>) != p.rec_bytes) { fprintf(stderr, "record size mismatch\n"); return 4; }
+    b.pos = exact<unsigned>(nc > 0 ? nc : 1);
+    b.pos2 = exact<unsigned>(nc > 0 ? nc : 1);
+    b.gtmp = exact<vec2_t<T>>(p.cap);
     b.bigflag = exact<unsigned>(p.S);
-    b.B = malloc(mn * accb);
-    b.partial = malloc(p.partial_elems * accb);
-    memset(b.B, 0, mn * accb);
+    b.B = malloc(mn * 8);
+    b.partial = malloc(p.partial_elems * 8);
+    memset(b.B, 0, mn * 8);
     memset(b.bigflag, 0, p.S * sizeof(unsigned));
-    *b.big_count = 0;
     const size_t hist = (size_t)p.S * sizeof(unsigned);
-    const size_t tile = (size_t)p.R * N * accb;
+    const size_t tile = (size_t)p.R * N * 8;
     for (int rep = 0; rep < 2; ++rep) {   // two steps: B / flags must be clean again
         launch(b.G1, kBinThreads, hist, [&] { k_bin_count<T>(px, py, sx, sy, nc, g, b); });
-        launch(1, kScanThreads, (size_t)(p.S + 2048) * sizeof(unsigned), [&] { k_bin_scan(b); });
-        if (det) launch(b.G1, kBinThreads, hist, [&] { k_bin_fill<T, true>(px, py, sx, sy, nc, g, b, gx, gy); });
-        else launch(b.G1, kBinThreads, hist, [&] { k_bin_fill<T, false>(px, py, sx, sy, nc, g, b, gx, gy); });
-        if (det) launch(p.Wmax, kAccThreads, tile, [&] { k_strip_acc<T, true>(g, b, d0n, dens, acc); });
-        else launch(p.Wmax, kAccThreads, tile, [&] { k_strip_acc<T, false>(g, b, d0n, dens, acc); });
-        if (det) launch(p.S, kAccThreads, 0, [&] { k_strip_red<T, true>(g, b, d0n, dens, acc); });
-        else launch(p.S, kAccThreads, 0, [&] { k_strip_red<T, false>(g, b, d0n, dens, acc); });
+        launch(1, kScanThreads, (size_t)(p.S + kScanThreads) * sizeof(unsigned), [&] { k_bin_scan(b); });
+        launch(b.G1, kBinThreads, hist, [&] { k_bin_fill<T>(px, py, sx, sy, nc, g, b); });
+        launch(p.Wmax, kAccThreads, tile, [&] { k_strip_acc<T>(g, b, d0n, dens); });
+        launch(p.S, kAccThreads, 0, [&] { k_strip_red<T>(g, b, d0n, dens); });
         for (int s2 = 0; s2 < p.S; ++s2)
             if (b.bigflag[s2]) { fprintf(stderr, "bigflag left set\n"); return 4; }
+        for (int s2 = 0; s2 < kCountSlots * p.S; ++s2)
+            if (b.xtot[s2]) { fprintf(stderr, "slot totals left set\n"); return 4; }
     }
     {
         constexpr int F = fpw<T>(LN);
         const size_t shm = (size_t)F * lds_len(LN) * sizeof(vec2_t<T>);
         const unsigned nt = F * (LN / fft_e(LN));
-        if (det) launch(M / (2 * F), nt, shm, [&] { k_row_dct<T, LN, F, 1>(a, dens, acc, d0n, dens, Tt); });
-        else launch(M / (2 * F), nt, shm, [&] { k_row_dct<T, LN, F, 0>(a, dens, acc, d0n, dens, Tt); });
+        launch(M / (2 * F), nt, shm, [&] { k_row_dct<T, LN, F>(a, dens, Tt); });
     }
     {
         constexpr int F = fpw<T>(LM);
@@ -171,17 +172,17 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
         launch(grid, F * (LN / fft_e(LN)), shm, [&] { k_row_inv<T, LN, F>(a, Ux, Uy, Tt, fx, fy, phi); });
     }
     if (nc > 0) {
-        unsigned gb = (unsigned)((nc * 5 / 4 + 255) / 256);
-        if (gb > 64) gb = 64;
-        launch(gb, 256, 0, [&] { k_gather_bin<T>(px, py, sx, sy, g, b, fx, fy, gx, gy); });
+        const size_t glds = (size_t)gather_rows<T>(p.R, N) * N * 2 * sizeof(T);
+        launch(p.Wmax, kAccThreads, glds, [&] { k_gather_bin<T>(g, b, fx, fy); });
+        launch((nc + 255) / 256, 256, 0, [&] { k_gather_out<T>(px, py, sx, sy, nc, g, b, fx, fy, gx, gy); });
     }
     {
         const unsigned char* Bb = (const unsigned char*)b.B;
-        for (size_t i = 0; i < mn * accb; ++i)
-            if (Bb[i]) { fprintf(stderr, "side map B not re-zeroed at byte %zu (row %zu)\n", i, i / accb / N); return 4; }
+        for (size_t i = 0; i < mn * 8; ++i)
+            if (Bb[i]) { fprintf(stderr, "side map B not re-zeroed at byte %zu (row %zu)\n", i, i / 8 / N); return 4; }
     }
-    printf("emu plan S=%d R=%d CH=%d Wmax=%d items=%u big=%u entries=%u\n", p.S, p.R, p.CH,
-           p.Wmax, *b.nitems, *b.big_count, b.strip_off[p.S]);
+    printf("emu plan S=%d R=%d CH=%d Wmax=%d items=%u records=%u\n", p.S, p.R, p.CH,
+           p.Wmax, *b.nitems, b.strip_off[p.S]);
 
     // oracle
     std::vector<double> dpx(nc), dpy(nc), dsx(nc), dsy(nc), dd0(mn), rho(mn), rphi(mn), rfx(mn), rfy(mn), rgx(nc), rgy(nc);

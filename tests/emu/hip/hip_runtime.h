@@ -31,6 +31,10 @@ struct dim3 {
 struct float2 { float x, y; };
 struct double2 { double x, y; };
 struct float4 { float x, y, z, w; };
+struct uint2 { unsigned x, y; };
+struct uint4 { unsigned x, y, z, w; };
+inline float __uint_as_float(unsigned u) { float f; memcpy(&f, &u, 4); return f; }
+inline unsigned __float_as_uint(float f) { unsigned u; memcpy(&u, &f, 4); return u; }
 struct double4 { double x, y, z, w; };
 using std::max;
 using std::min;
