@@ -1,0 +1,419 @@
+"""Drop-in replacement of the reference's integration/scatter_ttnn_client.py
+for the MI355X electric-potential step.
+
+Same public API:
+    ScatterTTNNClient(container, ipc_dir, num_bins_x, num_bins_y, nc_max,
+                      xl, yl, xh, yh, direct)               (:185-220)
+        .start(M, N, nc_actual, xl, yl, xh, yh)              (:293-390)
+        .call(px, py, sx, sy) -> (field_x, field_y, timing)  (:411-509)
+        .stop()                                              (:392-409)
+        .timing_summary(n_warmup)                            (:511-531)
+    patch_dreamplace(container, ipc_dir, num_cells, direct)  (:534-870)
+    get_timing_summary(), teardown()                         (:873-881)
+
+Two transports, both numpy-only in the hot loop:
+  * server (default): launches density_scatter_hip_server and talks the
+    reference's shared-memory protocol (dpep/shm.py; version 2 also carries
+    density, potential and per-cell forces);
+  * in-process (inprocess=True): calls libdpep.so through ctypes, no second
+    process.  Do not combine it with a ROCm build of PyTorch in the same
+    process (two HIP runtimes); the server mode has no such restriction.
+
+Semantics the server applies (and the reference's TT path did not): px, py
+are lower-left corners and sx, sy the cells' original sizes; DREAMPlace's
+sqrt2*bin stretch and area ratio are applied on the GPU.  Cells need no
+sorting and no sub-cell split.  call() returns torch tensors (made with
+torch.from_numpy, as the reference does) when the calling process has already
+imported torch, numpy arrays otherwise; as_torch= forces either.  The client
+never imports torch itself except in the DREAMPlace adapter.
+
+Errors: TimeoutError (server start / step), FileNotFoundError (missing
+server binary or library), ValueError (bad sizes), RuntimeError (server
+exited).
+"""
+from __future__ import annotations
+
+import atexit
+import mmap
+import os
+import struct
+import subprocess
+import sys
+import threading
+import time
+from typing import Dict, Optional, Tuple
+
+import numpy as np
+
+from . import shm as S
+
+_THIS_DIR = os.path.dirname(os.path.realpath(__file__))
+# DREAMPLACE_TT_SERVER_BINARY overrides the default, as in the reference.
+_SERVER_BINARY = os.environ.get(
+    "DREAMPLACE_TT_SERVER_BINARY",
+    os.path.join(_THIS_DIR, "density_scatter_hip_server"))
+
+_client: Optional["ScatterTTNNClient"] = None
+
+
+class ScatterTTNNClient:
+    def __init__(self, container: str = "", ipc_dir: str = "/dev/shm/dpep_ipc",
+                 num_bins_x: int = 0, num_bins_y: int = 0, nc_max: int = 0,
+                 xl: float = 0.0, yl: float = 0.0,
+                 xh: float = 1e6, yh: float = 1e6,
+                 direct: bool = True, inprocess: bool = False,
+                 server_binary=None, as_torch: Optional[bool] = None,
+                 ready_timeout: float = 600.0, step_timeout: float = 120.0):
+        # `container` and `direct` are accepted for API compatibility: the
+        # server is always launched directly (no container runtime).
+        self.container = container
+        self.direct = direct
+        self.ipc_dir = ipc_dir
+        self.inprocess = inprocess
+        self.M, self.N = int(num_bins_x), int(num_bins_y)
+        self.nc_max = int(nc_max)
+        self.xl, self.yl, self.xh, self.yh = xl, yl, xh, yh
+        # a path, or a command prefix (list) that the server arguments follow
+        self.server_binary = server_binary or _SERVER_BINARY
+        self.as_torch = as_torch
+        self.ready_timeout = ready_timeout
+        self.step_timeout = step_timeout
+
+        self.ready_flag = os.path.join(ipc_dir, "ready.flag")
+        self.shm_path = os.path.join(ipc_dir, "scatter.shm")
+        self._proc: Optional[subprocess.Popen] = None
+        self._ready = False
+        self._timings: list = []
+        self._fd = -1
+        self._mm: Optional[mmap.mmap] = None
+        self._layout: Optional[S.Layout] = None
+        self._views: Dict[str, np.ndarray] = {}
+        self._ctx = None                     # in-process dpep.Context
+        self._d0_pending: Optional[np.ndarray] = None
+        self.last_outputs: Dict[str, np.ndarray] = {}
+
+    # -- shared memory -------------------------------------------------------
+    def _create_shm(self) -> None:
+        lay = S.Layout(self.M, self.N, self.nc_max, version=2)
+        self._fd = os.open(self.shm_path, os.O_RDWR | os.O_CREAT | os.O_TRUNC, 0o666)
+        os.ftruncate(self._fd, lay.total_size)
+        self._mm = mmap.mmap(self._fd, lay.total_size, access=mmap.ACCESS_WRITE)
+        self._layout = lay
+        soa, mn = lay.soa, (self.M, self.N)
+        for name in ("px", "py", "sx", "sy", "grad_x", "grad_y"):
+            self._views[name] = np.ndarray((soa,), np.float32, self._mm, lay.offset(name))
+        for name in ("field_x", "field_y", "init_density", "density", "potential"):
+            self._views[name] = np.ndarray(mn, np.float32, self._mm, lay.offset(name))
+        struct.pack_into("<I", self._mm, S.OFF_STATE, S.STATE_IDLE)
+        S.write_v2_header(self._mm)
+
+    def _close_shm(self) -> None:
+        self._views = {}
+        if self._mm is not None:
+            try:
+                self._mm.close()
+            except (BufferError, ValueError):
+                pass
+            self._mm = None
+        if self._fd >= 0:
+            os.close(self._fd)
+            self._fd = -1
+        try:
+            os.unlink(self.shm_path)
+        except FileNotFoundError:
+            pass
+
+    # -- life cycle ------------------------------------------------------------
+    def start(self, M: int = 0, N: int = 0, nc_actual: int = 0,
+              xl: float = 0.0, yl: float = 0.0,
+              xh: float = 1e6, yh: float = 1e6) -> None:
+        if self._ready:
+            return
+        if M:
+            self.M = int(M)
+        if N:
+            self.N = int(N)
+        if xl or yl or xh != 1e6 or yh != 1e6:
+            self.xl, self.yl, self.xh, self.yh = xl, yl, xh, yh
+        if self.nc_max == 0:
+            if nc_actual == 0:
+                raise ValueError("nc_max=0 and no nc_actual supplied")
+            self.nc_max = int(nc_actual)
+        if self.M <= 0 or self.N <= 0:
+            raise ValueError(f"bin grid {self.M}x{self.N} is empty")
+
+        if self.inprocess:
+            from ._lib import Context
+            self._ctx = Context(self.M, self.N, self.nc_max, self.xl, self.yl,
+                                self.xh, self.yh)
+            if self._d0_pending is not None:
+                self._ctx.set_initial_density(self._d0_pending)
+            self._ready = True
+            atexit.register(self.stop)
+            return
+
+        prefix = ([self.server_binary] if isinstance(self.server_binary, str)
+                  else list(self.server_binary))
+        if not os.path.exists(prefix[0]):
+            raise FileNotFoundError(
+                f"server binary not found: {prefix[0]} (build it with "
+                "`make -C dreamplacett-framework_amd/csrc`)")
+        os.makedirs(self.ipc_dir, exist_ok=True)
+        try:
+            os.remove(self.ready_flag)       # a stale flag would race (:312-315)
+        except FileNotFoundError:
+            pass
+        self._create_shm()
+        if self._d0_pending is not None:
+            self._views["init_density"][...] = self._d0_pending
+        cmd = prefix + [str(self.M), str(self.N), str(self.nc_max),
+               self.ipc_dir, repr(float(self.xl)), repr(float(self.yl)),
+               repr(float(self.xh)), repr(float(self.yh))]
+        self._proc = subprocess.Popen(cmd, stdout=subprocess.PIPE,
+                                      stderr=subprocess.STDOUT, text=True)
+
+        def _log():
+            for line in self._proc.stdout:
+                print(f"[dpep_srv] {line}", end="", flush=True)
+        threading.Thread(target=_log, daemon=True).start()
+
+        deadline = time.monotonic() + self.ready_timeout
+        while not os.path.exists(self.ready_flag):
+            if self._proc.poll() is not None:
+                self._close_shm()
+                raise RuntimeError(f"server exited with code {self._proc.returncode} "
+                                   "before ready.flag")
+            if time.monotonic() > deadline:
+                self._kill()
+                self._close_shm()
+                raise TimeoutError("timeout waiting for the server's ready.flag")
+            time.sleep(0.01)
+        self._ready = True
+        atexit.register(self.stop)
+
+    def _kill(self) -> None:
+        if self._proc is not None and self._proc.poll() is None:
+            self._proc.kill()
+            self._proc.wait(timeout=20)
+
+    def stop(self) -> None:
+        if not self._ready:
+            return
+        if self._ctx is not None:
+            self._ctx.close()
+            self._ctx = None
+        if self._mm is not None:
+            struct.pack_into("<I", self._mm, S.OFF_STATE, S.STATE_QUIT)
+        if self._proc is not None:
+            try:
+                self._proc.wait(timeout=20)
+            except subprocess.TimeoutExpired:
+                self._kill()
+        self._close_shm()
+        self._ready = False
+
+    # -- per-step call -----------------------------------------------------------
+    def set_initial_density(self, init_density_normalized) -> None:
+        """initial_density_map / bin_area (M x N); sent once before the first
+        call, as the reference's shm slot 3 (:786-795)."""
+        d = np.ascontiguousarray(init_density_normalized, np.float32)
+        if self.M and self.N and d.size != self.M * self.N:
+            raise ValueError(f"initial density has {d.size} elements, expected "
+                             f"{self.M * self.N}")
+        if self._ctx is not None:
+            self._ctx.set_initial_density(d)
+        elif self._mm is not None:
+            self._views["init_density"][...] = d.reshape(self.M, self.N)
+        else:
+            self._d0_pending = d.reshape(self.M, self.N) if self.M else d
+
+    def call(self, px, py, sx, sy) -> Tuple[object, object, dict]:
+        out, timing = self._step(px, py, sx, sy)
+        fx, fy = out["field_x"], out["field_y"]
+        as_torch = self.as_torch if self.as_torch is not None else "torch" in sys.modules
+        if as_torch:
+            import torch
+            fx, fy = torch.from_numpy(fx), torch.from_numpy(fy)
+        return fx, fy, timing
+
+    def call_full(self, px, py, sx, sy) -> Dict[str, object]:
+        """One step; returns density, potential, field_x, field_y, grad_x,
+        grad_y (numpy) and timing."""
+        out, timing = self._step(px, py, sx, sy)
+        out = dict(out)
+        out["timing"] = timing
+        return out
+
+    def _step(self, px, py, sx, sy):
+        if not self._ready:
+            raise RuntimeError("client not started")
+        nc = int(np.asarray(px).size)
+        if nc > self.nc_max:
+            raise ValueError(f"nc={nc} exceeds nc_max={self.nc_max}")
+        if self._ctx is not None:
+            t0 = time.perf_counter()
+            out = self._ctx.step(px, py, sx, sy)
+            wall = (time.perf_counter() - t0) * 1e3
+            tm = self._ctx.timings()
+            timing = {"pos_write_ms": 0.0, "kernel_wait_ms": wall, "field_read_ms": 0.0,
+                      "h2d_ms": tm["h2d"], "scatter_ms": tm["scatter"],
+                      "gather_ms": tm["gather"], "d2h_density_ms": tm["d2h_den"],
+                      "ttnn_upload_ms": 0.0, "ttnn_compute_ms": tm["compute"],
+                      "ttnn_download_ms": tm["download"], "fw_ms": 0.0,
+                      "total_server_ms": tm["total"], "total_client_ms": wall,
+                      "gather_mode": "hip"}
+            self._timings.append(timing)
+            self.last_outputs = out
+            return out, timing
+
+        v = self._views
+        t0 = time.perf_counter()
+        for name, a in (("px", px), ("py", py), ("sx", sx), ("sy", sy)):
+            v[name][:nc] = np.asarray(a, dtype=np.float32)
+            v[name][nc:] = 0.0
+        pos_write_ms = (time.perf_counter() - t0) * 1e3
+        # nc before state (ordering on non-TSO hosts, :462-464)
+        struct.pack_into("<i", self._mm, S.OFF_NC, nc)
+        struct.pack_into("<I", self._mm, S.OFF_STATE, S.STATE_GO)
+        t0 = time.perf_counter()
+        deadline = time.monotonic() + self.step_timeout
+        while True:
+            st = struct.unpack_from("<I", self._mm, S.OFF_STATE)[0]
+            if st == S.STATE_DONE:
+                break
+            if self._proc is not None and self._proc.poll() is not None:
+                raise RuntimeError(f"server exited with code {self._proc.returncode}")
+            if time.monotonic() > deadline:
+                raise TimeoutError("timeout waiting for shm DONE")
+            time.sleep(0.0002)
+        kernel_wait_ms = (time.perf_counter() - t0) * 1e3
+        _, _, tm, gm = S.read_timings(self._mm)
+        struct.pack_into("<I", self._mm, S.OFF_STATE, S.STATE_IDLE)
+        t0 = time.perf_counter()
+        out = {
+            "field_x": v["field_x"].copy(), "field_y": v["field_y"].copy(),
+            "density": v["density"].copy(), "potential": v["potential"].copy(),
+            "grad_x": v["grad_x"][:nc].copy(), "grad_y": v["grad_y"][:nc].copy(),
+        }
+        field_read_ms = (time.perf_counter() - t0) * 1e3
+        timing = {"pos_write_ms": pos_write_ms, "kernel_wait_ms": kernel_wait_ms,
+                  "field_read_ms": field_read_ms}
+        timing.update(tm)
+        timing["total_client_ms"] = pos_write_ms + kernel_wait_ms + field_read_ms
+        timing["gather_mode"] = S.GATHER_MODE_NAMES.get(gm, "v6")
+        self._timings.append(timing)
+        self.last_outputs = out
+        return out, timing
+
+    def timing_summary(self, n_warmup: int = 4) -> dict:
+        timings = self._timings[n_warmup:] if len(self._timings) > n_warmup else self._timings
+        if not timings:
+            return {}
+        result = {}
+        for k in timings[0]:
+            vals = [t[k] for t in timings if k in t]
+            if isinstance(vals[0], (int, float)):
+                result[f"{k}_mean"] = float(np.mean(vals))
+                result[f"{k}_median"] = float(np.median(vals))
+            else:
+                result[k] = max(set(vals), key=vals.count)
+        result["n_iters"] = len(self._timings)
+        result["n_timed"] = len(timings)
+        return result
+
+
+# ---------------------------------------------------------------------------
+# DREAMPlace adapter (reference :534-870)
+# ---------------------------------------------------------------------------
+def _to_numpy(t):
+    return t.detach().cpu().numpy() if hasattr(t, "detach") else np.asarray(t)
+
+
+def make_forward(client: ScatterTTNNClient):
+    """Builds the replacement of ElectricPotentialFunction.forward (same 30+
+    argument signature as the reference's patched forward, :553-574)."""
+
+    def _forward(ctx, pos, node_size_x_clamped, node_size_y_clamped,
+                 offset_x, offset_y, ratio, bin_center_x, bin_center_y,
+                 initial_density_map, target_density, xl, yl, xh, yh,
+                 bin_size_x, bin_size_y, num_movable_nodes, num_filler_nodes,
+                 padding, padding_mask, num_bins_x, num_bins_y,
+                 num_movable_impacted_bins_x, num_movable_impacted_bins_y,
+                 num_filler_impacted_bins_x, num_filler_impacted_bins_y,
+                 deterministic_flag, sorted_node_map, exact_expkM=None,
+                 exact_expkN=None, inv_wu2_plus_wv2=None,
+                 wu_by_wu2_plus_wv2_half=None, wv_by_wu2_plus_wv2_half=None,
+                 dct2=None, idct2=None, idct_idxst=None, idxst_idct=None,
+                 fast_mode=True):
+        import torch   # DREAMPlace edge only
+
+        num_nodes = pos.shape[0] // 2
+        n_mov, n_fil = int(num_movable_nodes), int(num_filler_nodes)
+        posn = _to_numpy(pos)
+        # layout [movable | fixed terminals | filler] (:611-617); original
+        # sizes = clamped + 2 * offset (:632-633): the GPU stretches itself
+        osx = _to_numpy(node_size_x_clamped + 2.0 * offset_x)
+        osy = _to_numpy(node_size_y_clamped + 2.0 * offset_y)
+        px = np.concatenate([posn[:n_mov], posn[num_nodes - n_fil:num_nodes]])
+        py = np.concatenate([posn[num_nodes:num_nodes + n_mov],
+                             posn[2 * num_nodes - n_fil:2 * num_nodes]])
+        sx = np.concatenate([osx[:n_mov], osx[num_nodes - n_fil:num_nodes]])
+        sy = np.concatenate([osy[:n_mov], osy[num_nodes - n_fil:num_nodes]])
+        if not client._ready:
+            client.xl, client.yl = float(xl), float(yl)
+            client.xh, client.yh = float(xh), float(yh)
+            client.M, client.N = int(num_bins_x), int(num_bins_y)
+            bin_area = float(bin_size_x) * float(bin_size_y)
+            client.set_initial_density(_to_numpy(initial_density_map) / bin_area)
+            client.start(nc_actual=px.size)
+        out = client.call_full(px, py, sx, sy)
+        ctx.field_map_x = torch.from_numpy(out["field_x"]).to(pos.dtype)
+        ctx.field_map_y = torch.from_numpy(out["field_y"]).to(pos.dtype)
+        ctx.pos = pos
+        ctx.node_size_x_clamped = node_size_x_clamped
+        ctx.node_size_y_clamped = node_size_y_clamped
+        ctx.offset_x = offset_x
+        ctx.offset_y = offset_y
+        ctx.ratio = ratio
+        ctx.bin_center_x = bin_center_x
+        ctx.bin_center_y = bin_center_y
+        ctx.target_density = target_density
+        ctx.xl, ctx.yl, ctx.xh, ctx.yh = xl, yl, xh, yh
+        ctx.bin_size_x, ctx.bin_size_y = bin_size_x, bin_size_y
+        ctx.num_movable_nodes = num_movable_nodes
+        ctx.num_filler_nodes = num_filler_nodes
+        ctx.padding = padding
+        ctx.num_bins_x, ctx.num_bins_y = num_bins_x, num_bins_y
+        ctx.num_movable_impacted_bins_x = num_movable_impacted_bins_x
+        ctx.num_movable_impacted_bins_y = num_movable_impacted_bins_y
+        ctx.num_filler_impacted_bins_x = num_filler_impacted_bins_x
+        ctx.num_filler_impacted_bins_y = num_filler_impacted_bins_y
+        ctx.deterministic_flag = deterministic_flag
+        ctx.sorted_node_map = sorted_node_map
+        # the reference returns a zero energy (:860)
+        return torch.zeros(1, dtype=pos.dtype, device=pos.device)
+
+    return staticmethod(_forward)
+
+
+def patch_dreamplace(container: str = "", ipc_dir: str = "/dev/shm/dpep_ipc",
+                     num_cells: int = 0, direct: bool = True,
+                     inprocess: bool = False) -> None:
+    global _client
+    _client = ScatterTTNNClient(container=container, ipc_dir=ipc_dir,
+                                nc_max=num_cells, direct=direct, inprocess=inprocess)
+    os.makedirs(ipc_dir, exist_ok=True)
+    try:
+        import dreamplace.ops.electric_potential.electric_potential as ep_mod
+    except ImportError as e:
+        raise ImportError(f"could not import DREAMPlace electric_potential: {e}") from e
+    ep_mod.ElectricPotentialFunction.forward = make_forward(_client)
+
+
+def get_timing_summary() -> dict:
+    return {} if _client is None else _client.timing_summary()
+
+
+def teardown() -> None:
+    if _client is not None:
+        _client.stop()

@@ -1,0 +1,62 @@
+"""GPU: the drop-in boundary end to end -- density_scatter_hip_server driven
+by ScatterTTNNClient over the shared-memory protocol, and the client's
+in-process mode over the C ABI -- against the float64 oracle on the same
+seeded cells (float32 tolerances: density/potential rel L-inf <= 1e-5,
+fields/forces rel L2 <= 1e-4)."""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import PKG, rel_l2, rel_linf
+
+from dpep import workloads
+from dpep.scatter_ttnn_client import ScatterTTNNClient
+
+pytestmark = pytest.mark.gpu
+
+SERVER_BIN = os.path.join(PKG, "dpep", "density_scatter_hip_server")
+
+
+def _check(out, ref):
+    for k in ("density", "potential"):
+        e = rel_linf(out[k], ref[k])
+        assert e <= 1e-5, f"{k} rel Linf {e:.3e}"
+    for k in ("field_x", "field_y", "grad_x", "grad_y"):
+        e = rel_l2(out[k], ref[k])
+        assert e <= 1e-4, f"{k} rel L2 {e:.3e}"
+
+
+@pytest.mark.parametrize("inprocess", [False, True])
+def test_client_against_oracle(tmp_path, oracle, inprocess):
+    if not inprocess and not os.path.exists(SERVER_BIN):
+        pytest.fail(f"server binary missing: {SERVER_BIN}")
+    w = workloads.small(3, seed=21, cells=30000, grid=256)
+    print(f"client inprocess={inprocess} cells={w.nc} grid={w.M}", flush=True)
+    c = ScatterTTNNClient(ipc_dir=str(tmp_path / "ipc"), num_bins_x=w.M,
+                          num_bins_y=w.N, nc_max=w.nc + 5000, xl=w.xl, yl=w.yl,
+                          xh=w.xh, yh=w.yh, inprocess=inprocess,
+                          server_binary=SERVER_BIN, as_torch=False,
+                          ready_timeout=120, step_timeout=60)
+    c.set_initial_density(w.d0n)
+    c.start()
+    try:
+        px, py, sx, sy = w.cells(np.float32)
+        rng = np.random.default_rng(5)
+        for k in range(3):
+            # cells move between steps, as in a placement run
+            pxk = (px + rng.normal(0, 2, px.size)).astype(np.float32)
+            out = c.call_full(pxk, py, sx, sy)
+            ref = oracle.step(pxk, py, sx, sy, w.M, w.N, w.xl, w.yl, w.xh, w.yh,
+                              d0n=w.d0n.astype(np.float32))
+            _check(out, ref)
+        # fewer cells than before: the tail of the previous step is gone
+        n2 = w.nc // 3
+        out = c.call_full(px[:n2], py[:n2], sx[:n2], sy[:n2])
+        ref = oracle.step(px[:n2], py[:n2], sx[:n2], sy[:n2], w.M, w.N, w.xl, w.yl,
+                          w.xh, w.yh, d0n=w.d0n.astype(np.float32))
+        _check(out, ref)
+        t = c.timing_summary(n_warmup=1)
+        assert t["gather_mode"] == "hip" and t["n_iters"] == 4
+    finally:
+        c.stop()
