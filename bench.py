@@ -29,6 +29,12 @@ for _p in (PKG, ORACLE):
 import numpy as np  # noqa: E402
 
 HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "kernels_c3_1.1M_2048.md")
+# kernel name prefix in the rocprofv3 summary for each bench kernel key
+PMC_NAMES = {"bin_count": "k_bin_count", "bin_fill": "k_bin_fill",
+             "strip_acc": "k_strip_acc", "row_dct": "k_row_dct",
+             "col_pass": "k_col_pass", "row_inv": "k_row_inv",
+             "gather": ("k_gather_bin", "k_gather_out")}
 METRIC = ("ms per potential step (scatter+DCT+field), 1.1M cells @2048^2; "
           "% HBM peak")
 
@@ -49,6 +55,25 @@ def kernel_bytes(nc, M, N, esz, potential=True):
         "row_inv": 2 * nmaps * esz * mn,               # read U*, write maps
         "gather": 6 * esz * nc + 2 * esz * mn,         # cells, fields, forces
     }
+
+
+def pmc_traffic(key):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 PMC
+    summary of the 1.1M-cell 2048^2 float32 workload (FETCH_SIZE x 2 +
+    WRITE_SIZE x 1 KiB, calibrated on a plain copy); None if absent."""
+    names = PMC_NAMES.get(key)
+    if names is None or not os.path.exists(PMC_SUMMARY):
+        return None
+    names = (names,) if isinstance(names, str) else names
+    total = 0.0
+    found = 0
+    with open(PMC_SUMMARY) as f:
+        for line in f:
+            cols = [c.strip() for c in line.strip().strip("|").split("|")]
+            if len(cols) >= 9 and any(cols[0].startswith(n + "<") for n in names):
+                total += float(cols[8]) * 1e6
+                found += 1
+    return round(total) if found == len(names) else None
 
 
 def step_bytes(nc, M, N, esz, potential=True):
@@ -135,6 +160,17 @@ def main():
     ctx.sync()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
 
+    # PCIe-inclusive rate (host buffers in and out, pageable memory): not `value`
+    host_ms = None
+    if not args.no_profile:
+        n_host = 5
+        ctx.step(px, py, sx, sy)
+        t0 = time.perf_counter()
+        for _ in range(n_host):
+            ctx.step(px, py, sx, sy)
+        host_ms = (time.perf_counter() - t0) * 1e3 / n_host
+        ctx.set_cells(px, py, sx, sy)
+
     kt = None
     if not args.no_profile:
         # same K steps again with HIP events between launches on the
@@ -153,9 +189,13 @@ def main():
     if kt:
         dom = max((k for k in kb), key=lambda k: kt[k])
         ach = kb[dom] / (kt[dom] * 1e-6)
+        headline = (args.config == 3 and dtype == np.float32 and potential)
         roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach / 1e9, 1),
                 "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                "frac": round(ach / HBM_PEAK, 4), "traffic": None,
+                "frac": round(ach / HBM_PEAK, 4),
+                "traffic": pmc_traffic(dom) if headline else None,
+                "traffic_source": (os.path.relpath(PMC_SUMMARY, ROOT)
+                                   if headline else None),
                 "algorithmic_bytes": kb[dom], "avg_us": round(kt[dom], 2)}
 
     cpu = None
@@ -186,6 +226,7 @@ def main():
         "step_bytes": bstep,
         "roofline": roof,
         "kernel_us": {k: round(v, 2) for k, v in kt.items()} if kt else None,
+        "host_step_ms": round(host_ms, 3) if host_ms else None,
         "cpu_baseline": cpu,
         "workload_gen_s": round(gen_s, 2),
     }

@@ -61,7 +61,7 @@ class ScatterTTNNClient:
                  num_bins_x: int = 0, num_bins_y: int = 0, nc_max: int = 0,
                  xl: float = 0.0, yl: float = 0.0,
                  xh: float = 1e6, yh: float = 1e6,
-                 direct: bool = True, inprocess: bool = False,
+                 direct: bool = False, inprocess: bool = False,
                  server_binary=None, as_torch: Optional[bool] = None,
                  ready_timeout: float = 600.0, step_timeout: float = 120.0):
         # `container` and `direct` are accepted for API compatibility: the
@@ -397,7 +397,7 @@ def make_forward(client: ScatterTTNNClient):
 
 
 def patch_dreamplace(container: str = "", ipc_dir: str = "/dev/shm/dpep_ipc",
-                     num_cells: int = 0, direct: bool = True,
+                     num_cells: int = 0, direct: bool = False,
                      inprocess: bool = False) -> None:
     global _client
     _client = ScatterTTNNClient(container=container, ipc_dir=ipc_dir,

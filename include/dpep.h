@@ -5,8 +5,9 @@
  *
  * The ABI replaces the device side of the reference's shared-memory server
  * (host/density_scatter_ttnn_server_host.cpp) with plain functions over plain
- * pointers; the reference-side bindings a maintainer adds (ctypes for the
- * Python client, the C++ server loop) are listed in INTEGRATION.md.
+ * pointers.  Its callers here are the ctypes binding of the Python client
+ * (dreamplacett-framework_amd/dpep/_lib.py) and the shm server loop
+ * (dreamplacett-framework_amd/csrc/dpep_server.cpp).
  *
  * Conventions
  *   - Maps are x-major: map[bx * N + by], M = num_bins_x rows of N = num_bins_y

@@ -40,8 +40,9 @@ def emu(tmp_path_factory):
 # reduce); tall gives a tenth of the cells a span of 3..40 rows (side map B).
 CASES = [
     "f32 8 8 50", "f32 16 16 200 tall", "f32 8 32 60 nopot", "f32 16 128 3000 ch=128",
-    "f32 128 16 300 det", "f64 8 8 40", "f64 64 64 1000 det ch=100 tall",
-    "f32 64 64 2000 ch=64 tall", "f32 64 64 2000 ch=64 tall det", "f32 256 256 2000",
+    "f32 128 16 300", "f64 8 8 40", "f64 64 64 1000 ch=100 tall",
+    "f32 64 64 2000 ch=64 tall", "f32 256 32 600", "f32 32 256 400 tall",
+    "f32 32 2048 500",
     "f32 16 4096 2000 tall", "f64 16 4096 100",
 ]
 

@@ -240,11 +240,13 @@ def test_gather_matches_bruteforce(oracle):
 
 def test_planted_mistakes_are_caught(oracle, spectral_golden):
     """The golden checks above would fail for typical slips: a missing factor
-    2 in S_M, transposed axes, a dropped stretch ratio."""
+    2 in S_M, a flipped sign, swapped fields, transposed axes, a dropped
+    stretch ratio."""
     rho = spectral_golden["rho_16x8"]
     bsx, bsy = spectral_golden["geom_16x8"]
     phi, fx, fy = oracle.solve(rho, bsx, bsy)
     assert rel_linf(fx / 2.0, spectral_golden["fx_16x8"]) > 0.1
+    assert rel_linf(-fx, spectral_golden["fx_16x8"]) > 0.1
     assert rel_linf(fy, spectral_golden["fx_16x8"]) > 0.1
     phi_t, _, _ = oracle.solve(rho.T.copy(), bsy, bsx)
     assert rel_linf(phi_t.T, spectral_golden["phi_16x8"]) > 1e-3
