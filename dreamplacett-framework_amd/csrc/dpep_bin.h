@@ -120,6 +120,13 @@ __device__ __forceinline__ unsigned long long to_fixed(double v, double scale)
     return (unsigned long long)__double2ull_rn(v * scale);
 }
 
+// The scale is a power of two, so v * scale is exact in float as in double
+// and both round to the same integer: float32 contributions need no float64.
+__device__ __forceinline__ unsigned long long to_fixed(float v, float scale)
+{
+    return (unsigned long long)__float2ull_rn(v * scale);
+}
+
 // ---------------------------------------------------------------------------
 // K1: per-workgroup strip histogram.
 // ---------------------------------------------------------------------------
@@ -372,7 +379,7 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     const unsigned eend = b.strip_off[s + 1];
     const unsigned e1 = min(e0 + (unsigned)b.CH, eend);
     const Rec<T>* rec = reinterpret_cast<const Rec<T>*>(b.recs);
-    const double fs = g.fix_scale;
+    const T fs = (T)g.fix_scale;
     constexpr int kBatch = 4;       // record loads in flight per thread
     for (unsigned eb = e0 + tid; eb < e1; eb += kBatch * kAccThreads) {
         Rec<T> rb[kBatch];
@@ -400,7 +407,7 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
                 for (int q = 0; q <= ny; ++q) {
                     const T ty = min(yr, (T)(q + 1)) - max(dy, (T)q);
                     if (!(ty > (T)0)) continue;
-                    atomicAdd(&trow[q], to_fixed((double)(rtx * ty), fs));
+                    atomicAdd(&trow[q], to_fixed(rtx * ty, fs));
                 }
             }
         }
@@ -408,7 +415,7 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     __syncthreads();
 
     const size_t gbase = (size_t)k0 * N;
-    const double inv = 1.0 / fs;
+    const double inv = 1.0 / g.fix_scale;
     if (single) {
         A* Bm = reinterpret_cast<A*>(b.B);
         if (!bf) {
@@ -583,36 +590,46 @@ __device__ __forceinline__ void gather_one(const CellSpan& c, const Grid& g,
     ay *= c.ratio;
 }
 
+// One workgroup per K3 block of kCellsPerGroup cells (same cell-to-thread
+// map): the records of a block sit in one short run per strip, so the
+// block's partials are read by one CU while they are still in its caches.
 template <typename T>
-__global__ __launch_bounds__(256) void k_gather_out(
+__global__ __launch_bounds__(kBinThreads) void k_gather_out(
     const T* __restrict__ px, const T* __restrict__ py,
     const T* __restrict__ sx, const T* __restrict__ sy, int nc, Grid g,
     BinArgs b, const T* __restrict__ fx, const T* __restrict__ fy,
     T* __restrict__ gx, T* __restrict__ gy)
 {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= nc) return;
-    const unsigned p = b.pos[i], p2 = b.pos2[i];
+    const int c0 = blockIdx.x * kCellsPerGroup + threadIdx.x;
     const vec2_t<T>* res = reinterpret_cast<const vec2_t<T>*>(b.gtmp);
-    T ox = (T)0, oy = (T)0;
-    if (p < kPosNone) {
-        const vec2_t<T> v = res[p];
-        ox = v.x;
-        oy = v.y;
-        if (p2 < kPosNone) {
-            const vec2_t<T> v2 = res[p2];
-            ox += v2.x;
-            oy += v2.y;
-        }
-    } else if (p == kPosTall) {
-        CellSpan c;
-        double ax = 0.0, ay = 0.0;
-        if (load_span(px, py, sx, sy, i, g, c)) gather_one(c, g, fx, fy, ax, ay);
-        ox = (T)ax;
-        oy = (T)ay;
+    unsigned p[kCellsPerThread], p2[kCellsPerThread];
+#pragma unroll
+    for (int j = 0; j < kCellsPerThread; ++j) {
+        const int i = c0 + j * kBinThreads;
+        p[j] = i < nc ? b.pos[i] : kPosNone;
+        p2[j] = i < nc ? b.pos2[i] : kPosNone;
     }
-    gx[i] = ox;
-    gy[i] = oy;
+    vec2_t<T> v[kCellsPerThread], v2[kCellsPerThread];
+#pragma unroll
+    for (int j = 0; j < kCellsPerThread; ++j) {
+        v[j] = p[j] < kPosNone ? res[p[j]] : vec2_t<T>{(T)0, (T)0};
+        v2[j] = p2[j] < kPosNone ? res[p2[j]] : vec2_t<T>{(T)0, (T)0};
+    }
+#pragma unroll
+    for (int j = 0; j < kCellsPerThread; ++j) {
+        const int i = c0 + j * kBinThreads;
+        if (i >= nc) break;
+        T ox = v[j].x + v2[j].x, oy = v[j].y + v2[j].y;
+        if (p[j] == kPosTall) {
+            CellSpan c;
+            double ax = 0.0, ay = 0.0;
+            if (load_span(px, py, sx, sy, i, g, c)) gather_one(c, g, fx, fy, ax, ay);
+            ox = (T)ax;
+            oy = (T)ay;
+        }
+        gx[i] = ox;
+        gy[i] = oy;
+    }
 }
 
 }  // namespace dpep

@@ -47,8 +47,8 @@ hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
     k_gather_bin<T><<<b.Wmax, kAccThreads, lds, s>>>(g, b, fx, fy);
     hipError_t e = hipGetLastError();
     if (e) return e;
-    k_gather_out<T><<<(unsigned)((nc + 255) / 256), 256, 0, s>>>(px, py, sx, sy, nc, g, b,
-                                                                fx, fy, gx, gy);
+    k_gather_out<T><<<g1_of(nc), kBinThreads, 0, s>>>(px, py, sx, sy, nc, g, b, fx, fy, gx,
+                                                      gy);
     return hipGetLastError();
 }
 

@@ -149,7 +149,16 @@ __device__ __forceinline__ double overlap_1d(double lo, double ext,
 // ---------------------------------------------------------------------------
 __host__ __device__ constexpr int fft_e(int L) { return L < 16 ? L : 16; }
 __host__ __device__ constexpr int lds_pad(int e) { return e + (e >> 5); }
-__host__ __device__ constexpr int lds_len(int L) { return L + (L >> 5); }
+// Row stride of one FFT's buffer: the padded length plus a skew of 8
+// elements, so rows of consecutive FFTs start 8 banks-pairs apart and the
+// tile loads/stores that touch one element of several rows do not collide.
+__host__ __device__ constexpr int lds_len(int L) { return L + (L >> 5) + 8; }
+
+// 16-byte vector of T (global loads and stores of the spectral passes).
+template <typename T, int V = 16 / (int)sizeof(T)>
+struct alignas(16) pack {
+    T v[V];
+};
 
 // Makhoul's even/odd-reversed ordering: x[m] sits at position perm(m).
 template <int L>
@@ -277,12 +286,22 @@ __device__ __forceinline__ void fft_stage(vec2_t<T>* buf, int t,
         const int j = t + TPF * b;
         const int k = j % NS;
         if constexpr (NS > 1) {
+            // W^(r k S) for r < R: the power-of-two exponents come from the
+            // table, the others are products of at most three of them
+            constexpr int S = L / (NS * R);
+            C w[R];
 #pragma unroll
             for (int r = 1; r < R; ++r) {
-                C w = tw[r * k * (L / (NS * R))];
-                if (INV) w.y = -w.y;
-                v[b][r] = cmul(v[b][r], w);
+                const int hi = 1 << (31 - __builtin_clz(r));
+                if (hi == r) {
+                    w[r] = tw[r * k * S];
+                    if (INV) w[r].y = -w[r].y;
+                } else {
+                    w[r] = cmul(w[hi], w[r - hi]);
+                }
             }
+#pragma unroll
+            for (int r = 1; r < R; ++r) v[b][r] = cmul(v[b][r], w[r]);
         }
         dft_r<T, R, INV>(v[b]);
     }

@@ -48,6 +48,17 @@ __device__ __forceinline__ T& comp(vec2_t<T>& c, int which)
 }
 
 template <typename T>
+__device__ __forceinline__ T comp_of(const vec2_t<T>& c, int which)
+{
+    return which ? c.y : c.x;
+}
+
+// Global accesses of the passes move 16-byte vectors: V elements each, NV
+// vectors per thread for a block of `elems` elements.
+template <typename T>
+constexpr int kVec = 16 / (int)sizeof(T);
+
+template <typename T>
 __device__ __forceinline__ T spectral_weight(int round, int u, int v,
                                              const SpectralArgs& a)
 {
@@ -137,11 +148,22 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_dct(
     const int x0 = blockIdx.x * TX;
     const size_t base = (size_t)x0 * L;
 
-#pragma unroll 4
-    for (int e = tid; e < TX * L; e += NT) {
-        const int r = e / L, m = e % L;
-        const T val = density_in[base + e];
-        comp<T>(sb[(r >> 1) * LP + lds_pad(makhoul_pos<L>(m))], r & 1) = val;
+    constexpr int V = kVec<T>, NV = TX * L / (NT * V);
+    static_assert(NV * NT * V == TX * L, "P1 block is not a whole number of vectors");
+    {
+        const pack<T>* src = reinterpret_cast<const pack<T>*>(density_in + base);
+        pack<T> r[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) r[i] = src[tid + i * NT];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int e0 = (tid + i * NT) * V;
+            const int row = e0 / L, m0 = e0 % L;
+            C* rowp = sb + (row >> 1) * LP;
+#pragma unroll
+            for (int q = 0; q < V; ++q)
+                comp<T>(rowp[lds_pad(makhoul_pos<L>(m0 + q))], row & 1) = r[i].v[q];
+        }
     }
     __syncthreads();
     fft_lds<T, L, false>(buf, t, reinterpret_cast<const C*>(a.twN));
@@ -164,14 +186,19 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_dct(
     const int TV = a.tiles.TV;
     const int lgTV = __builtin_ctz(TV);
     const int lgTE = __builtin_ctz(TX) + lgTV;
-    T* out = Tt + base;
-#pragma unroll 4
-    for (int e = tid; e < TX * L; e += NT) {
-        const int bv = e >> lgTE;
-        const int w = e & ((1 << lgTE) - 1);
+    pack<T>* out = reinterpret_cast<pack<T>*>(Tt + base);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int e0 = (tid + i * NT) * V;        // V consecutive v of one x
+        const int bv = e0 >> lgTE;
+        const int w = e0 & ((1 << lgTE) - 1);
         const int x_in = w >> lgTV;
         const int v = (bv << lgTV) + (w & (TV - 1));
-        out[e] = comp<T>(sb[(x_in >> 1) * LP + lds_pad(v)], x_in & 1);
+        const C* rowp = sb + (x_in >> 1) * LP;
+        pack<T> o;
+#pragma unroll
+        for (int q = 0; q < V; ++q) o.v[q] = comp_of<T>(rowp[lds_pad(v + q)], x_in & 1);
+        out[tid + i * NT] = o;
     }
 }
 
@@ -200,15 +227,32 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
     const int tile_elems = TX * TV;
     const int lgTE = lgTX + lgTV;
 
-    // load the tiles (bx, b2) for every bx
-#pragma unroll 4
-    for (int e = tid; e < L * TV; e += NT) {
-        const int bx = e >> lgTE;
-        const int w = e & (tile_elems - 1);
-        const int x = (bx << lgTX) + (w >> lgTV);
-        const int v_in = w & (TV - 1);
-        const T val = Tt[((size_t)bx * NBV + b2) * tile_elems + w];
-        comp<T>(sb[(v_in >> 1) * LP + lds_pad(makhoul_pos<L>(x))], v_in & 1) = val;
+    // load the tiles (bx, b2) for every bx: each vector holds V consecutive
+    // columns v (pairs of them form the complex input of one FFT) of one x
+    constexpr int V = kVec<T>, NV = L * TV / (NT * V);
+    static_assert(NV * NT * V == L * TV && V % 2 == 0 && TV % V == 0, "P2 vector split");
+    {
+        pack<T> r[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int e0 = (tid + i * NT) * V;
+            const int bx = e0 >> lgTE;
+            const int w = e0 & (tile_elems - 1);
+            r[i] = *reinterpret_cast<const pack<T>*>(
+                Tt + ((size_t)bx * NBV + b2) * tile_elems + w);
+        }
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int e0 = (tid + i * NT) * V;
+            const int bx = e0 >> lgTE;
+            const int w = e0 & (tile_elems - 1);
+            const int x = (bx << lgTX) + (w >> lgTV);
+            const int v_in = w & (TV - 1);
+            const int px = lds_pad(makhoul_pos<L>(x));
+#pragma unroll
+            for (int q = 0; q < V; q += 2)
+                sb[((v_in + q) >> 1) * LP + px] = C{r[i].v[q], r[i].v[q + 1]};
+        }
     }
     __syncthreads();
     fft_lds<T, L, false>(buf, t, reinterpret_cast<const C*>(a.twM));
@@ -220,7 +264,21 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
     for (int i = 0; i < E / 2; ++i)
         dct_post<T, L>(buf, t + TPF * i, post, scale, Ak[i], Am[i]);
 
+    // A / D once (zero at (0,0)); the rounds then only scale by w_u / 2
+    // (a function of the row k), w_v / 2 (of the column) or 1, so nothing
+    // per-element has to stay live across the rounds.
     const int v1 = v0 + 2 * f, v2 = v1 + 1;
+#pragma unroll
+    for (int i = 0; i < E / 2; ++i) {
+        const int s = t + TPF * i;
+        const int k = s, m = (s == 0) ? L / 2 : L - s;
+        Ak[i].x *= spectral_weight<T>(2, k, v1, a);
+        Ak[i].y *= spectral_weight<T>(2, k, v2, a);
+        Am[i].x *= spectral_weight<T>(2, m, v1, a);
+        Am[i].y *= spectral_weight<T>(2, m, v2, a);
+    }
+    const T hu = (T)0.5 * (T)a.wu_step;
+    const T hv1 = (T)0.5 * (T)v1 * (T)a.wv_step, hv2 = (T)0.5 * (T)v2 * (T)a.wv_step;
     const int nrounds = a.potential ? 3 : 2;
     for (int round = 0; round < nrounds; ++round) {
         const bool rev = (round == 0);
@@ -229,10 +287,20 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
         for (int i = 0; i < E / 2; ++i) {
             const int s = t + TPF * i;
             const int k = s, m = (s == 0) ? L / 2 : L - s;
-            const T b1k = Ak[i].x * spectral_weight<T>(round, k, v1, a);
-            const T b1m = Am[i].x * spectral_weight<T>(round, m, v1, a);
-            const T b2k = Ak[i].y * spectral_weight<T>(round, k, v2, a);
-            const T b2m = Am[i].y * spectral_weight<T>(round, m, v2, a);
+            T w1k, w1m, w2k, w2m;
+            if (round == 0) {
+                w1k = w2k = (T)k * hu;
+                w1m = w2m = (T)m * hu;
+            } else if (round == 1) {
+                w1k = w1m = hv1;
+                w2k = w2m = hv2;
+            } else {
+                w1k = w1m = w2k = w2m = (T)1;
+            }
+            const T b1k = Ak[i].x * w1k;
+            const T b1m = Am[i].x * w1m;
+            const T b2k = Ak[i].y * w2k;
+            const T b2m = Am[i].y * w2m;
             C p1k, p1m, p2k, p2m;
             inv_pre<T, L>(s, b1k, b1m, rev, post, p1k, p1m);
             inv_pre<T, L>(s, b2k, b2m, rev, post, p2k, p2m);
@@ -251,16 +319,23 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
 
         T* dst = round == 0 ? Ux : (round == 1 ? Uy : Tt);
         const T rscale = round == 1 ? (T)2 : (T)1;
-#pragma unroll 4
-        for (int e = tid; e < L * TV; e += NT) {
-            const int bx = e >> lgTE;
-            const int w = e & (tile_elems - 1);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int e0 = (tid + i * NT) * V;
+            const int bx = e0 >> lgTE;
+            const int w = e0 & (tile_elems - 1);
             const int x = (bx << lgTX) + (w >> lgTV);
             const int v_in = w & (TV - 1);
-            T val = comp<T>(sb[(v_in >> 1) * LP + lds_pad(makhoul_pos<L>(x))], v_in & 1);
-            val *= rscale;
-            if (round == 0 && (x & 1)) val = -val;
-            dst[((size_t)bx * NBV + b2) * tile_elems + w] = val;
+            const int px = lds_pad(makhoul_pos<L>(x));
+            const T sc = (round == 0 && (x & 1)) ? -rscale : rscale;
+            pack<T> o;
+#pragma unroll
+            for (int q = 0; q < V; q += 2) {
+                const C z = sb[((v_in + q) >> 1) * LP + px];
+                o.v[q] = z.x * sc;
+                o.v[q + 1] = z.y * sc;
+            }
+            *reinterpret_cast<pack<T>*>(dst + ((size_t)bx * NBV + b2) * tile_elems + w) = o;
         }
     }
 }
@@ -296,14 +371,30 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_inv(
         const int bx = ab >> 1, half = ab & 1;
         const int chunk = F * TV;
         const int lgCH = __builtin_ctz(F) + lgTV;
-#pragma unroll 4
-        for (int e = tid; e < F * L; e += NT) {
-            const int bv = e >> lgCH;
-            const int w = e & (chunk - 1);
-            const int xr = w >> lgTV;
-            const int v = (bv << lgTV) + (w & (TV - 1));
-            const size_t g = ((size_t)bx * NBV + bv) * (TX * TV) + half * chunk + w;
-            sb[xr * LP + lds_pad(v)] = C{Ux[g], Uy[g]};
+        constexpr int V = kVec<T>, NVA = F * L / (NT * V);
+        static_assert(NVA * NT * V == F * L, "P3 vector split");
+        {
+            pack<T> rx[NVA], ry[NVA];
+#pragma unroll
+            for (int i = 0; i < NVA; ++i) {
+                const int e0 = (tid + i * NT) * V;
+                const int bv = e0 >> lgCH;
+                const int w = e0 & (chunk - 1);
+                const size_t g = ((size_t)bx * NBV + bv) * (TX * TV) + half * chunk + w;
+                rx[i] = *reinterpret_cast<const pack<T>*>(Ux + g);
+                ry[i] = *reinterpret_cast<const pack<T>*>(Uy + g);
+            }
+#pragma unroll
+            for (int i = 0; i < NVA; ++i) {
+                const int e0 = (tid + i * NT) * V;
+                const int bv = e0 >> lgCH;
+                const int w = e0 & (chunk - 1);
+                const int xr = w >> lgTV;
+                const int v = (bv << lgTV) + (w & (TV - 1));
+#pragma unroll
+                for (int q = 0; q < V; ++q)
+                    sb[xr * LP + lds_pad(v + q)] = C{rx[i].v[q], ry[i].v[q]};
+            }
         }
         __syncthreads();
         C Vk[E / 2], Vm[E / 2];
@@ -328,25 +419,43 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_inv(
         __syncthreads();
         fft_lds<T, L, true>(buf, t, tw);
         const size_t base = (size_t)x0 * L;
-#pragma unroll 4
-        for (int e = tid; e < F * L; e += NT) {
-            const int xr = e / L, y = e % L;
-            const C z = sb[xr * LP + lds_pad(makhoul_pos<L>(y))];
-            fx[base + e] = z.x;
-            fy[base + e] = (y & 1) ? (T)-0.5 * z.y : (T)0.5 * z.y;
+#pragma unroll
+        for (int i = 0; i < NVA; ++i) {
+            const int e0 = (tid + i * NT) * V;
+            const int xr = e0 / L, y0 = e0 % L;
+            pack<T> ox, oy;
+#pragma unroll
+            for (int q = 0; q < V; ++q) {
+                const C z = sb[xr * LP + lds_pad(makhoul_pos<L>(y0 + q))];
+                ox.v[q] = z.x;
+                oy.v[q] = (q & 1) ? (T)-0.5 * z.y : (T)0.5 * z.y;   // y0 is even
+            }
+            *reinterpret_cast<pack<T>*>(fx + base + e0) = ox;
+            *reinterpret_cast<pack<T>*>(fy + base + e0) = oy;
         }
     } else {
         const int bb = blockIdx.x - nA;
         const int x0 = bb * TX;
         const size_t base = (size_t)x0 * L;
         const int lgTE = __builtin_ctz(TX) + lgTV;
-#pragma unroll 4
-        for (int e = tid; e < TX * L; e += NT) {
-            const int bv = e >> lgTE;
-            const int w = e & ((1 << lgTE) - 1);
-            const int x_in = w >> lgTV;
-            const int v = (bv << lgTV) + (w & (TV - 1));
-            comp<T>(sb[(x_in >> 1) * LP + lds_pad(v)], x_in & 1) = Up[base + e];
+        constexpr int V = kVec<T>, NVB = TX * L / (NT * V);
+        static_assert(NVB * NT * V == TX * L, "P3 vector split");
+        {
+            const pack<T>* src = reinterpret_cast<const pack<T>*>(Up + base);
+            pack<T> r[NVB];
+#pragma unroll
+            for (int i = 0; i < NVB; ++i) r[i] = src[tid + i * NT];
+#pragma unroll
+            for (int i = 0; i < NVB; ++i) {
+                const int e0 = (tid + i * NT) * V;
+                const int bv = e0 >> lgTE;
+                const int w = e0 & ((1 << lgTE) - 1);
+                const int x_in = w >> lgTV;
+                const int v = (bv << lgTV) + (w & (TV - 1));
+                C* rowp = sb + (x_in >> 1) * LP;
+#pragma unroll
+                for (int q = 0; q < V; ++q) comp<T>(rowp[lds_pad(v + q)], x_in & 1) = r[i].v[q];
+            }
         }
         __syncthreads();
         C Vk[E / 2], Vm[E / 2];
@@ -370,11 +479,17 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_inv(
         }
         __syncthreads();
         fft_lds<T, L, true>(buf, t, tw);
-#pragma unroll 4
-        for (int e = tid; e < TX * L; e += NT) {
-            const int r = e / L, y = e % L;
-            const C z = sb[(r >> 1) * LP + lds_pad(makhoul_pos<L>(y))];
-            phi[base + e] = (r & 1) ? z.y : z.x;
+        pack<T>* dst = reinterpret_cast<pack<T>*>(phi + base);
+#pragma unroll
+        for (int i = 0; i < NVB; ++i) {
+            const int e0 = (tid + i * NT) * V;
+            const int r = e0 / L, y0 = e0 % L;
+            const C* rowp = sb + (r >> 1) * LP;
+            pack<T> o;
+#pragma unroll
+            for (int q = 0; q < V; ++q)
+                o.v[q] = comp_of<T>(rowp[lds_pad(makhoul_pos<L>(y0 + q))], r & 1);
+            dst[tid + i * NT] = o;
         }
     }
 }

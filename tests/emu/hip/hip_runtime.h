@@ -51,6 +51,10 @@ inline unsigned long long __double2ull_rn(double x)
 {
     return (unsigned long long)std::nearbyint(x);
 }
+inline unsigned long long __float2ull_rn(float x)
+{
+    return (unsigned long long)std::nearbyint(x);
+}
 template <class T>
 inline T unsafeAtomicAdd(T* p, T v)
 {
