@@ -51,8 +51,8 @@ def kernel_bytes(nc, M, N, esz, potential=True):
         "strip_acc": 2 * esz * mn,                     # read D0, write rho (+ entries: scratch)
         "strip_red": 0,                                # split strips only
         "row_dct": 2 * esz * mn,                       # read rho, write T
-        "col_pass": (1 + nmaps) * esz * mn,            # read T, write U*
-        "row_inv": 2 * nmaps * esz * mn,               # read U*, write maps
+        "col_pass": 3 * esz * mn,                      # read T, write Ux, Uy
+        "row_inv": (2 + nmaps) * esz * mn,             # read Ux, Uy, write maps
         "gather": 6 * esz * nc + 2 * esz * mn,         # cells, fields, forces
     }
 
@@ -77,9 +77,13 @@ def pmc_traffic(key):
 
 
 def step_bytes(nc, M, N, esz, potential=True):
-    """The step's byte model: 10 e Nc + 16 e MN (e = element size), i.e.
-    40 Nc + 64 MN at float32; 12 e MN less without the potential."""
-    return 10 * esz * nc + (16 if potential else 13) * esz * M * N
+    """The step's byte model: 10 e Nc + 14 e MN (e = element size), i.e.
+    40 Nc + 56 MN at float32; e MN less without the potential.  Cells are
+    read twice (scatter, gather) and the forces written; the maps: D0 and rho
+    (2), P1 (2), P2 (3), P3 (2 in, 3 out), the gather's two field maps (2).
+    The potential's own column transforms are not needed (Up = Uy / w_v),
+    so the 3-pass model's 64 MN round trip of Up is not moved."""
+    return 10 * esz * nc + (14 if potential else 13) * esz * M * N
 
 
 def cpu_baseline(w, seconds, max_steps=20):

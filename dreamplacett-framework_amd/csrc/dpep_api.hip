@@ -196,8 +196,8 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
     if (prof) HIP_TRY(hipEventRecord(pe[6], s));
     HIP_TRY(launch_col_pass<T>(c->sargs, (T*)c->d_T, (T*)c->d_Ux, (T*)c->d_Uy, s));
     if (prof) HIP_TRY(hipEventRecord(pe[7], s));
-    HIP_TRY(launch_row_inv<T>(c->sargs, (const T*)c->d_Ux, (const T*)c->d_Uy,
-                              (const T*)c->d_T, fx, fy, phi, s));
+    HIP_TRY(launch_row_inv<T>(c->sargs, (const T*)c->d_Ux, (const T*)c->d_Uy, fx, fy,
+                              phi, s));
     if (prof) HIP_TRY(hipEventRecord(pe[8], s));
     if (gather)
         HIP_TRY(launch_bin_gather<T>(px, py, sx, sy, nc, c->grid, c->bins, fx, fy,

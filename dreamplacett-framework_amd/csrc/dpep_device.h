@@ -323,7 +323,7 @@ __device__ __forceinline__ void fft_stages(vec2_t<T>* buf, int t,
 {
     if constexpr (NS < L) {
         constexpr int REM = L / NS;
-        constexpr int R = REM >= 16 ? 16 : REM;
+        constexpr int R = REM >= fft_e(L) ? fft_e(L) : REM;
         fft_stage<T, L, R, NS, INV>(buf, t, tw);
         fft_stages<T, L, NS * R, INV>(buf, t, tw);
     }

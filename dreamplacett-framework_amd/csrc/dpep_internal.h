@@ -37,11 +37,11 @@ template <typename T>
 hipError_t launch_row_dct(const SpectralArgs& a, const T* density, T* Tt,
                           hipStream_t s);
 template <typename T>
-hipError_t launch_col_pass(const SpectralArgs& a, T* Tt, T* Ux, T* Uy,
+hipError_t launch_col_pass(const SpectralArgs& a, const T* Tt, T* Ux, T* Uy,
                            hipStream_t s);
 template <typename T>
 hipError_t launch_row_inv(const SpectralArgs& a, const T* Ux, const T* Uy,
-                          const T* Up, T* fx, T* fy, T* phi, hipStream_t s);
+                          T* fx, T* fy, T* phi, hipStream_t s);
 // ---------------------------------------------------------------------------
 // Strip binning (kernels in dpep_bin.h)
 // ---------------------------------------------------------------------------

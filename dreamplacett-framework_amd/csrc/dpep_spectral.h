@@ -21,11 +21,20 @@
 // A thread owns the index pair {s, L-s} (s = 0 owns {0, L/2}) so the pre- and
 // post-processing never crosses threads.
 //
+// The potential needs no transform of its own along x: w_v depends only on
+// the column v, so for v >= 1
+//   Up[:, v] = I_M (A[:, v] / D[:, v]) = Uy[:, v] / w_v(v)
+// with Uy = 2 I_M (A . Wy) as stored.  Column 0 of Uy would be zero
+// (w_v(0) = 0) and the S-type transform that turns Uy into fy never reads
+// it, so P2 stores w_v(1) Up[:, 0] there instead: the weight of column 1,
+// so the two columns that share one complex FFT keep similar magnitudes
+// (the FFT's rounding is relative to the pair, not to each column).
+//
 // Passes and HBM traffic (MN = M*N elements):
 //   P1  k_row_dct : rho rows (along y)  -> T        tiled      read MN, write MN
-//   P2  k_col_pass: T rows (along x)    -> Ux,Uy,Up tiled      read MN, write 3MN
-//                   (DCT-II, weights, three inverse transforms; Up overwrites T)
-//   P3  k_row_inv : Ux,Uy,Up rows (y)   -> fx, fy, phi         read 3MN, write 3MN
+//   P2  k_col_pass: T rows (along x)    -> Ux, Uy   tiled      read MN, write 2MN
+//                   (DCT-II, weights, two inverse transforms)
+//   P3  k_row_inv : Ux, Uy rows (y)     -> fx, fy, phi         read 2MN, write 3MN
 // Tiles of TX x TV elements (TX = rows of a P1 workgroup, TV = rows of a P2
 // workgroup) make every global access a run of >= 128 contiguous bytes while
 // P1 and P2 write "transposed" relative to the rows they process.
@@ -208,7 +217,7 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_dct(
 // ---------------------------------------------------------------------------
 template <typename T, int L, int F>
 __global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
-    SpectralArgs a, T* __restrict__ Tt, T* __restrict__ Ux,
+    SpectralArgs a, const T* __restrict__ Tt, T* __restrict__ Ux,
     T* __restrict__ Uy)
 {
     using C = vec2_t<T>;
@@ -279,8 +288,9 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
     }
     const T hu = (T)0.5 * (T)a.wu_step;
     const T hv1 = (T)0.5 * (T)v1 * (T)a.wv_step, hv2 = (T)0.5 * (T)v2 * (T)a.wv_step;
-    const int nrounds = a.potential ? 3 : 2;
-    for (int round = 0; round < nrounds; ++round) {
+    // column 0: w_v(1) I_M (A / D) in the otherwise-zero column of Uy
+    const T hv1z = v1 == 0 ? (T)0.5 * (T)a.wv_step : hv1;
+    for (int round = 0; round < 2; ++round) {
         const bool rev = (round == 0);
         C Vk[E / 2], Vm[E / 2];
 #pragma unroll
@@ -291,11 +301,9 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
             if (round == 0) {
                 w1k = w2k = (T)k * hu;
                 w1m = w2m = (T)m * hu;
-            } else if (round == 1) {
-                w1k = w1m = hv1;
-                w2k = w2m = hv2;
             } else {
-                w1k = w1m = w2k = w2m = (T)1;
+                w1k = w1m = hv1z;
+                w2k = w2m = hv2;
             }
             const T b1k = Ak[i].x * w1k;
             const T b1m = Am[i].x * w1m;
@@ -317,7 +325,7 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
         __syncthreads();
         fft_lds<T, L, true>(buf, t, reinterpret_cast<const C*>(a.twM));
 
-        T* dst = round == 0 ? Ux : (round == 1 ? Uy : Tt);
+        T* dst = round == 0 ? Ux : Uy;
         const T rscale = round == 1 ? (T)2 : (T)1;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
@@ -341,15 +349,17 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
 }
 
 // ---------------------------------------------------------------------------
-// P3: inverse transforms along y.  Blocks [0, M/F): one row per FFT, packs
-// (Ux row, reversed Uy row) -> fx and fy.  Blocks [M/F, M/F + M/2F): two rows
-// of Up per FFT -> phi.
+// P3: inverse transforms along y.  Rows come in groups of TX = 2F; a group
+// has two type-A blocks (F rows each, one row per FFT packing (Ux row,
+// reversed Uy row) -> fx and fy) and, with the potential, one type-B block
+// (two rows per FFT of Up = Uy / w_v, column 0 = Uy / w_v(1) -> phi).  The blocks
+// of a group are consecutive in XCD-logical order, so the Uy rows the
+// type-B block re-reads are still in that XCD's L2.
 // ---------------------------------------------------------------------------
 template <typename T, int L, int F>
 __global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_inv(
     SpectralArgs a, const T* __restrict__ Ux, const T* __restrict__ Uy,
-    const T* __restrict__ Up, T* __restrict__ fx, T* __restrict__ fy,
-    T* __restrict__ phi)
+    T* __restrict__ fx, T* __restrict__ fy, T* __restrict__ phi)
 {
     using C = vec2_t<T>;
     constexpr int E = fft_e(L), TPF = L / E, NT = F * TPF, LP = lds_len(L);
@@ -361,12 +371,14 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_inv(
     const int TV = a.tiles.TV;
     const int lgTV = __builtin_ctz(TV);
     const int NBV = L / TV;
-    const int nA = a.M / F;
     const C* post = reinterpret_cast<const C*>(a.postN);
     const C* tw = reinterpret_cast<const C*>(a.twN);
+    const int per_group = a.potential ? 3 : 2;
+    const int lb = (int)xcd_logical_block(blockIdx.x, gridDim.x);
+    const int grp = lb / per_group, role = lb % per_group;
 
-    if ((int)blockIdx.x < nA) {
-        const int ab = blockIdx.x;
+    if (role < 2) {
+        const int ab = 2 * grp + role;
         const int x0 = ab * F;
         const int bx = ab >> 1, half = ab & 1;
         const int chunk = F * TV;
@@ -434,14 +446,15 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_inv(
             *reinterpret_cast<pack<T>*>(fy + base + e0) = oy;
         }
     } else {
-        const int bb = blockIdx.x - nA;
+        const int bb = grp;
         const int x0 = bb * TX;
         const size_t base = (size_t)x0 * L;
         const int lgTE = __builtin_ctz(TX) + lgTV;
         constexpr int V = kVec<T>, NVB = TX * L / (NT * V);
         static_assert(NVB * NT * V == TX * L, "P3 vector split");
         {
-            const pack<T>* src = reinterpret_cast<const pack<T>*>(Up + base);
+            const pack<T>* src = reinterpret_cast<const pack<T>*>(Uy + base);
+            const T wv = (T)a.wv_step;
             pack<T> r[NVB];
 #pragma unroll
             for (int i = 0; i < NVB; ++i) r[i] = src[tid + i * NT];
@@ -454,7 +467,11 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_inv(
                 const int v = (bv << lgTV) + (w & (TV - 1));
                 C* rowp = sb + (x_in >> 1) * LP;
 #pragma unroll
-                for (int q = 0; q < V; ++q) comp<T>(rowp[lds_pad(v + q)], x_in & 1) = r[i].v[q];
+                for (int q = 0; q < V; ++q) {
+                    const int vq = v + q;
+                    const T up = r[i].v[q] / ((T)(vq > 0 ? vq : 1) * wv);
+                    comp<T>(rowp[lds_pad(vq)], x_in & 1) = up;
+                }
             }
         }
         __syncthreads();

@@ -59,7 +59,7 @@ hipError_t launch_row_dct(const SpectralArgs& a, const T* density, T* Tt,
 }
 
 template <typename T>
-hipError_t launch_col_pass(const SpectralArgs& a, T* Tt, T* Ux, T* Uy,
+hipError_t launch_col_pass(const SpectralArgs& a, const T* Tt, T* Ux, T* Uy,
                            hipStream_t s)
 {
     return dispatch_len<T>(a.M, [&](auto lc) -> hipError_t {
@@ -73,15 +73,14 @@ hipError_t launch_col_pass(const SpectralArgs& a, T* Tt, T* Ux, T* Uy,
 
 template <typename T>
 hipError_t launch_row_inv(const SpectralArgs& a, const T* Ux, const T* Uy,
-                          const T* Up, T* fx, T* fy, T* phi, hipStream_t s)
+                          T* fx, T* fy, T* phi, hipStream_t s)
 {
     return dispatch_len<T>(a.N, [&](auto lc) -> hipError_t {
         constexpr int L = decltype(lc)::value;
         constexpr int F = fpw<T>(L);
-        const int nA = a.M / F;
-        const int nB = a.potential ? a.M / (2 * F) : 0;
-        const dim3 grid(nA + nB), block(threads_of<T, L>());
-        k_row_inv<T, L, F><<<grid, block, lds_bytes<T, L>(), s>>>(a, Ux, Uy, Up, fx, fy, phi);
+        const int groups = a.M / (2 * F);
+        const dim3 grid(groups * (a.potential ? 3 : 2)), block(threads_of<T, L>());
+        k_row_inv<T, L, F><<<grid, block, lds_bytes<T, L>(), s>>>(a, Ux, Uy, fx, fy, phi);
         return hipGetLastError();
     });
 }
@@ -132,16 +131,15 @@ template hipError_t launch_row_dct<float>(const SpectralArgs&, const float*,
                                           float*, hipStream_t);
 template hipError_t launch_row_dct<double>(const SpectralArgs&, const double*,
                                            double*, hipStream_t);
-template hipError_t launch_col_pass<float>(const SpectralArgs&, float*, float*,
-                                           float*, hipStream_t);
-template hipError_t launch_col_pass<double>(const SpectralArgs&, double*,
+template hipError_t launch_col_pass<float>(const SpectralArgs&, const float*,
+                                           float*, float*, hipStream_t);
+template hipError_t launch_col_pass<double>(const SpectralArgs&, const double*,
                                             double*, double*, hipStream_t);
 template hipError_t launch_row_inv<float>(const SpectralArgs&, const float*,
-                                          const float*, const float*, float*,
-                                          float*, float*, hipStream_t);
+                                          const float*, float*, float*, float*,
+                                          hipStream_t);
 template hipError_t launch_row_inv<double>(const SpectralArgs&, const double*,
-                                           const double*, const double*,
-                                           double*, double*, double*,
-                                           hipStream_t);
+                                           const double*, double*, double*,
+                                           double*, hipStream_t);
 
 }  // namespace dpep

@@ -179,8 +179,8 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     {
         constexpr int F = fpw<T>(LN);
         const size_t shm = (size_t)F * lds_len(LN) * sizeof(vec2_t<T>);
-        const unsigned grid = M / F + (pot ? M / (2 * F) : 0);
-        launch(grid, F * (LN / fft_e(LN)), shm, [&] { k_row_inv<T, LN, F>(a, Ux, Uy, Tt, fx, fy, phi); });
+        const unsigned grid = (M / (2 * F)) * (pot ? 3 : 2);
+        launch(grid, F * (LN / fft_e(LN)), shm, [&] { k_row_inv<T, LN, F>(a, Ux, Uy, fx, fy, phi); });
     }
     if (nc > 0) {
         const size_t glds = (size_t)gather_rows<T>(p.R, N) * N * 2 * sizeof(T);
