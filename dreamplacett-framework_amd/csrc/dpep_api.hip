@@ -3,12 +3,12 @@
 // A context owns every device buffer of one (M, N, nc_max, dtype) problem,
 // allocated once at creation; a step allocates nothing.  Launch sequence of
 // one step on the context's stream:
-//   k_bin_count, k_bin_scan, k_bin_fill   counting sort of cells into strips
-//   k_strip_acc, k_strip_red              LDS strip accumulation, D0 fold
-//   k_row_dct   P1  (converts the fixed-point map when deterministic)
+//   k_bin_count, k_bin_fill               counting sort of cells into strips
+//   k_strip_acc                           LDS strip accumulation, D0 fold
+//   k_row_dct   P1
 //   k_col_pass  P2
 //   k_row_inv   P3  -> field_x, field_y, potential
-//   k_gather_bin     cells <- fields
+//   k_gather_bin, k_gather_out   per-cell forces <- fields
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -145,7 +145,8 @@ static void release(dpep_ctx* c)
                     c->d_density, c->d_potential, c->d_fx, c->d_fy, c->d_gx,
                     c->d_gy, c->d_T, c->d_Ux, c->d_Uy, c->d_twM,
                     c->d_postM, c->d_twN, c->d_postN, b.cnt, b.xtot, b.xoff, b.strip_off,
-                    b.nch, b.item_start, b.items, b.nitems, b.recs, b.pos, b.pos2, b.gtmp,
+                    b.nch, b.item_start, b.items, b.nitems, b.ticket, b.done, b.recg,
+                    b.recm, b.pos, b.pos2, b.gtmp,
                     b.bigflag, b.B, b.partial};
     for (void* p : bufs)
         if (p) (void)hipFree(p);
@@ -177,7 +178,8 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
         !b.xtot || !b.xoff ||
         (nc > 0 && (!px || !py || !sx || !sy)) ||
         (gather && (!gx || !gy)) || !b.cnt || !b.strip_off || !b.nch ||
-        !b.item_start || !b.items || !b.nitems || !b.recs || !b.pos || !b.pos2 ||
+        !b.item_start || !b.items || !b.nitems || !b.ticket || !b.done || !b.recg ||
+        !b.recm || !b.pos || !b.pos2 ||
         !b.gtmp || !b.bigflag || !b.B || !b.partial)
         return fail(DPEP_ERR_STATE, "internal: a kernel argument is NULL");
     if (nc > c->nc_max)
@@ -339,7 +341,12 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
         HIP_TRY(hipMalloc((void**)&b.item_start, (size_t)p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.items, (size_t)p.Wmax * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.nitems, sizeof(unsigned)));
-        HIP_TRY(hipMalloc(&b.recs, p.cap * p.rec_bytes));
+        HIP_TRY(hipMalloc((void**)&b.ticket, sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.done, (size_t)p.S * sizeof(unsigned)));
+        HIP_TRY(hipMemset(b.ticket, 0, sizeof(unsigned)));
+        HIP_TRY(hipMemset(b.done, 0, (size_t)p.S * sizeof(unsigned)));
+        HIP_TRY(hipMalloc(&b.recg, p.cap * p.geo_bytes));
+        HIP_TRY(hipMalloc((void**)&b.recm, p.cap * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.pos, (size_t)(nc_max > 0 ? nc_max : 1) * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.pos2, (size_t)(nc_max > 0 ? nc_max : 1) * sizeof(unsigned)));
         HIP_TRY(hipMalloc(&b.gtmp, p.cap * 2 * c->esz));

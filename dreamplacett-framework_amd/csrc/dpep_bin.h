@@ -8,12 +8,13 @@
 //
 //   k_bin_count   per-workgroup strip histograms; each nonzero count  K1
 //                 is added to one of kCountSlots totals per strip and
-//                 the returned old total is the workgroup's base
-//   k_bin_scan    strip offsets, slot offsets, chunk list (1 group)   K2
+//                 the returned old total is the workgroup's base; the
+//                 last workgroup to finish builds the strip table
+//                 (strip and slot offsets, chunk list)
 //   k_bin_fill    cells -> strip-sorted records; tall cells -> B      K3
 //   k_strip_acc   one work item = (strip, chunk): LDS accumulate,     K4
-//                 flush rho = D0 + tile (+B) or a partial slot
-//   k_strip_red   strips split into several chunks: sum partials      K4r
+//                 flush rho = D0 + tile (+B); a strip split into
+//                 several chunks is summed by its last chunk to finish
 //   k_gather_bin  one work item = (strip, chunk): the strip's field   G1
 //                 rows staged in LDS, each record's partial force over
 //                 the rows of this strip, in record order
@@ -28,18 +29,20 @@
 // runs about seven times faster than ds_add_f32.)
 //
 // K3 evaluates each cell's stretch and span once, in float64, and stores a
-// record in bin units relative to its first bin's edges (offsets dx, dy in
-// [0, 1), stretched extents w, h) with the packed span, the area ratio and
-// the cell index: K4 and G1 then need only short arithmetic on small
-// numbers, which float32 carries to ~1e-7 of a bin (absolute die coordinates
-// would not).  K3 also writes pos[i] and pos2[i], the records of cell i (in
-// cell order, coalesced), so G2 can write the forces in cell order instead
-// of G1 scattering them.
+// 20-byte record (structure of arrays): geometry in bin units relative to
+// the edges of its first bin (offsets dx, dy of the stretched corner, in
+// [0, 1), and the cell's original extents w, h, from which K4 and G1 re-derive
+// the stretched extents and the area ratio), and one span word.  Short
+// arithmetic on small numbers, which float32 carries to ~1e-7 of a bin
+// (absolute die coordinates would not).  K3 also writes pos[i] and pos2[i],
+// the records of cell i (in cell order, coalesced), so G2 can write the
+// forces in cell order instead of G1 scattering them.
 //
-// A cell whose span covers more than R rows ("tall") skips the sort: K3 adds
-// it with global atomics into the side map B (zero between steps), marks the
-// strips it touches, and K4/K4r fold and re-zero those rows of B.  Every
-// other cell touches at most two strips, so the record array holds 2*nc_max.
+// A cell whose span covers more than R rows or more than kMaxSpanY + 1
+// columns ("tall") skips the sort: K3 adds it with global atomics into the
+// side map B (zero between steps), marks the strips it touches, and K4 folds
+// and re-zeroes those rows of B.  Every other cell touches at most two
+// strips, so the record arrays hold 2*nc_max.
 #pragma once
 
 #include <type_traits>
@@ -53,55 +56,57 @@ template <> struct vec4<float> { using type = float4; };
 template <> struct vec4<double> { using type = double4; };
 template <typename T> using vec4_t = typename vec4<T>::type;
 
-// Strip record: geometry in bin units relative to the edges of bin
-// (bxl, byl); bxl | nx << 16, byl | ny << 16 (nx = bxh - bxl, ny = byh - byl);
-// the stretch's area ratio; the cell index (| kSecondStrip for the copy in
-// the second strip of a cell that crosses a strip boundary).
-template <typename T> struct Rec;
-template <> struct alignas(32) Rec<float> {
-    float4 g;           // dx, dy, w, h
-    uint4 m;            // A, B, ratio bits, index
-    __device__ __forceinline__ float ratio() const { return __uint_as_float(m.z); }
-    __device__ __forceinline__ unsigned index() const { return m.w; }
-    __device__ __forceinline__ void set(float4 geo, unsigned A, unsigned B, double r, unsigned idx)
-    {
-        g = geo;
-        m = uint4{A, B, __float_as_uint((float)r), idx};
-    }
+// Span word of a record in strip s (first row k0 = s * R):
+//   bits 0-3   bxl - k0, two's complement in [-7, 7] (negative for the copy
+//              of a cell that starts in the strip before)
+//   bits 4-6   nx = bxh - bxl (< R <= 8)
+//   bits 7-18  ny = byh - byl (<= kMaxSpanY)
+//   bits 19-31 byl (< 8192)
+__device__ __forceinline__ unsigned span_word(int rel, int nx, int ny, int byl)
+{
+    return ((unsigned)rel & 0xFu) | ((unsigned)nx << 4) | ((unsigned)ny << 7) |
+           ((unsigned)byl << 19);
+}
+
+struct SpanBox {
+    int bxl, nx, byl, ny;
 };
-template <> struct alignas(64) Rec<double> {
-    double4 g;
-    double r;
-    unsigned A, B, idx, pad;
-    __device__ __forceinline__ double ratio() const { return r; }
-    __device__ __forceinline__ unsigned index() const { return idx; }
-    __device__ __forceinline__ void set(double4 geo, unsigned a, unsigned b_, double rr, unsigned i)
-    {
-        g = geo;
-        r = rr;
-        A = a;
-        B = b_;
-        idx = i;
-        pad = 0u;
+
+__device__ __forceinline__ SpanBox span_of(unsigned m, int k0)
+{
+    SpanBox b;
+    b.bxl = k0 + (((int)(m << 28)) >> 28);
+    b.nx = (int)((m >> 4) & 7u);
+    b.ny = (int)((m >> 7) & 0xFFFu);
+    b.byl = (int)(m >> 19);
+    return b;
+}
+
+// Stretched extents and area ratio from a record's original extents.
+template <typename T>
+__device__ __forceinline__ void stretch_of(const vec4_t<T>& r, int stretch, T& xr,
+                                           T& yr, T& ratio)
+{
+    T wc = r.z, hc = r.w;
+    ratio = (T)1;
+    if (stretch) {
+        const T m = (T)1.41421356237309504880;
+        wc = r.z > m ? r.z : m;
+        hc = r.w > m ? r.w : m;
+        ratio = (r.z * r.w) / (wc * hc);
     }
-};
-static_assert(sizeof(Rec<float>) == 32 && sizeof(Rec<double>) == 64,
-              "record sizes are part of the buffer plan (make_bin_plan)");
-template <typename T> __device__ __forceinline__ unsigned rec_A(const Rec<T>& r);
-template <> __device__ __forceinline__ unsigned rec_A(const Rec<float>& r) { return r.m.x; }
-template <> __device__ __forceinline__ unsigned rec_A(const Rec<double>& r) { return r.A; }
-template <typename T> __device__ __forceinline__ unsigned rec_B(const Rec<T>& r);
-template <> __device__ __forceinline__ unsigned rec_B(const Rec<float>& r) { return r.m.y; }
-template <> __device__ __forceinline__ unsigned rec_B(const Rec<double>& r) { return r.B; }
+    xr = r.x + wc;
+    yr = r.y + hc;
+}
 
 constexpr unsigned kPosTall = 0xFFFFFFFFu;     // pos[i]: tall cell (side map)
 constexpr unsigned kPosNone = 0xFFFFFFFEu;     // pos[i]: contributes nothing
 
-// Strips [s0, s1] a cell occupies and whether it is tall.
+// Strips [s0, s1] a cell occupies and whether it takes the tall path.
 __device__ __forceinline__ void cell_strips(const CellSpan& c, int R, int lgR,
                                             int& s0, int& s1, bool& tall)
 {
-    tall = (c.bxh - c.bxl + 1) > R;
+    tall = (c.bxh - c.bxl + 1) > R || (c.byh - c.byl) > kMaxSpanY;
     s0 = c.bxl >> lgR;
     s1 = c.bxh >> lgR;
 }
@@ -128,7 +133,97 @@ __device__ __forceinline__ unsigned long long to_fixed(float v, float scale)
 }
 
 // ---------------------------------------------------------------------------
-// K1: per-workgroup strip histogram.
+// Strip table, built by the last K1 workgroup: strip_off = exclusive scan of
+// the strip totals, xoff = first entry of each (slot, strip), the chunk list.
+// LDS: tot[S] | tmp[kBinThreads].  Leaves the slot totals at zero.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ unsigned block_exclusive_scan(unsigned v,
+                                                         unsigned* tmp,
+                                                         unsigned& total)
+{
+    // Hillis-Steele over kBinThreads values in LDS.
+    const int tid = threadIdx.x;
+    tmp[tid] = v;
+    __syncthreads();
+    for (int off = 1; off < kBinThreads; off <<= 1) {
+        const unsigned a = tid >= off ? tmp[tid - off] : 0u;
+        __syncthreads();
+        tmp[tid] += a;
+        __syncthreads();
+    }
+    const unsigned incl = tmp[tid];
+    total = tmp[kBinThreads - 1];
+    __syncthreads();
+    return incl - v;
+}
+
+// The slot totals are only ever touched by device-scope atomics (K1's adds,
+// the reads and the reset here), which are performed coherently across the
+// XCDs' separate L2 caches: no fence is needed, and none is taken (a
+// device-scope fence writes back the whole L2 of the XCD).
+__device__ __forceinline__ unsigned coherent_load(unsigned* p) { return atomicAdd(p, 0u); }
+
+__device__ __forceinline__ void build_strip_table(const BinArgs& b, unsigned* tot,
+                                                  unsigned* tmp)
+{
+    const int tid = threadIdx.x;
+    const int S = b.S;
+    // strip totals = sum of the slot totals
+    for (int s = tid; s < S; s += kBinThreads) {
+        unsigned t = 0u;
+#pragma unroll
+        for (int x = 0; x < kCountSlots; ++x) t += coherent_load(&b.xtot[(size_t)x * S + s]);
+        tot[s] = t;
+    }
+    __syncthreads();
+    // exclusive scan of the totals (each thread a run of strips)
+    const int per = (S + kBinThreads - 1) / kBinThreads;
+    const int r0 = min(tid * per, S), r1 = min(r0 + per, S);
+    unsigned run = 0u;
+    for (int s = r0; s < r1; ++s) run += tot[s];
+    unsigned total;
+    unsigned base = block_exclusive_scan(run, tmp, total);
+    for (int s = r0; s < r1; ++s) {
+        const unsigned t = tot[s];
+        b.strip_off[s] = base;
+        tot[s] = base;          // tot now holds the strip offsets
+        base += t;
+        const unsigned n = (t + (unsigned)b.CH - 1u) / (unsigned)b.CH;
+        b.nch[s] = n > 1u ? n : 1u;
+    }
+    if (tid == 0) b.strip_off[S] = total;
+    __syncthreads();
+    // slot offsets; the slot totals are consumed here and left at zero
+    for (int s = tid; s < S; s += kBinThreads) {
+        unsigned off = tot[s];
+#pragma unroll
+        for (int x = 0; x < kCountSlots; ++x) {
+            const unsigned v = atomicExch(&b.xtot[(size_t)x * S + s], 0u);
+            b.xoff[(size_t)x * S + s] = off;
+            off += v;
+        }
+    }
+    // work items (strip, chunk)
+    unsigned nrun = 0u;
+    for (int s = r0; s < r1; ++s) nrun += b.nch[s];
+    unsigned ntotal;
+    unsigned ibase = block_exclusive_scan(nrun, tmp, ntotal);
+    for (int s = r0; s < r1; ++s) {
+        const unsigned n = b.nch[s];
+        b.item_start[s] = ibase;
+        for (unsigned c = 0; c < n; ++c)
+            if (ibase + c < (unsigned)b.Wmax) b.items[ibase + c] = (unsigned)s | (c << 16);
+        ibase += n;
+    }
+    if (tid == 0) {
+        *b.nitems = ntotal < (unsigned)b.Wmax ? ntotal : (unsigned)b.Wmax;
+        atomicExch(b.ticket, 0u);      // every K1 workgroup has taken its ticket
+    }
+}
+
+// ---------------------------------------------------------------------------
+// K1: per-workgroup strip histogram; the last workgroup builds the table.
+// LDS: hist[S] | tmp[kBinThreads] | flag.
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(kBinThreads) void k_bin_count(
@@ -138,6 +233,7 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_count(
 {
     extern __shared__ __align__(16) unsigned char smem[];
     unsigned* hist = reinterpret_cast<unsigned*>(smem);
+    unsigned* flag = hist + b.S + kBinThreads;
     const int tid = threadIdx.x;
     for (int s = tid; s < b.S; s += kBinThreads) hist[s] = 0u;
     __syncthreads();
@@ -174,93 +270,14 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_count(
         const unsigned h = hist[s];
         row[s] = h ? atomicAdd(&slot[s], h) : 0u;
     }
-}
-
-// ---------------------------------------------------------------------------
-// K2: one workgroup.  strip_off = exclusive scan of strip totals; cnt[g][s]
-// becomes the first entry slot of workgroup g in strip s; work items.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ unsigned block_exclusive_scan(unsigned v,
-                                                         unsigned* tmp,
-                                                         unsigned& total)
-{
-    // Hillis-Steele over kScanThreads values in LDS.
-    const int tid = threadIdx.x;
-    tmp[tid] = v;
+    // Every slot add of this workgroup has returned (its result was stored
+    // above) before the barrier, hence before the ticket: the last workgroup
+    // to take one sees all totals.
     __syncthreads();
-    for (int off = 1; off < kScanThreads; off <<= 1) {
-        const unsigned a = tid >= off ? tmp[tid - off] : 0u;
-        __syncthreads();
-        tmp[tid] += a;
-        __syncthreads();
-    }
-    const unsigned incl = tmp[tid];
-    total = tmp[kScanThreads - 1];
+    if (tid == 0) *flag = atomicAdd(b.ticket, 1u) == gridDim.x - 1 ? 1u : 0u;
     __syncthreads();
-    return incl - v;
-}
-
-__global__ __launch_bounds__(kScanThreads) void k_bin_scan(BinArgs b)
-{
-    // LDS: tot[S] | tmp[1024]
-    extern __shared__ __align__(16) unsigned char smem[];
-    unsigned* tot = reinterpret_cast<unsigned*>(smem);
-    unsigned* tmp = tot + b.S;
-    const int tid = threadIdx.x;
-    const int S = b.S;
-
-    // strip totals = sum of the slot totals
-    for (int s = tid; s < S; s += kScanThreads) {
-        unsigned v[kCountSlots];
-#pragma unroll
-        for (int x = 0; x < kCountSlots; ++x) v[x] = b.xtot[(size_t)x * S + s];
-        unsigned t = 0u;
-#pragma unroll
-        for (int x = 0; x < kCountSlots; ++x) t += v[x];
-        tot[s] = t;
-    }
-    __syncthreads();
-    // exclusive scan of the totals (each thread a run of strips)
-    const int per = (S + kScanThreads - 1) / kScanThreads;
-    const int r0 = min(tid * per, S), r1 = min(r0 + per, S);
-    unsigned run = 0u;
-    for (int s = r0; s < r1; ++s) run += tot[s];
-    unsigned total;
-    unsigned base = block_exclusive_scan(run, tmp, total);
-    for (int s = r0; s < r1; ++s) {
-        const unsigned t = tot[s];
-        b.strip_off[s] = base;
-        tot[s] = base;          // tot now holds the strip offsets
-        base += t;
-        const unsigned n = (t + (unsigned)b.CH - 1u) / (unsigned)b.CH;
-        b.nch[s] = n > 1u ? n : 1u;
-    }
-    if (tid == 0) b.strip_off[S] = total;
-    __syncthreads();
-    // slot offsets; the slot totals are consumed here and left at zero
-    for (int s = tid; s < S; s += kScanThreads) {
-        unsigned off = tot[s];
-#pragma unroll
-        for (int x = 0; x < kCountSlots; ++x) {
-            const unsigned v = b.xtot[(size_t)x * S + s];
-            b.xoff[(size_t)x * S + s] = off;
-            b.xtot[(size_t)x * S + s] = 0u;
-            off += v;
-        }
-    }
-    // work items (strip, chunk)
-    unsigned nrun = 0u;
-    for (int s = r0; s < r1; ++s) nrun += b.nch[s];
-    unsigned ntotal;
-    unsigned ibase = block_exclusive_scan(nrun, tmp, ntotal);
-    for (int s = r0; s < r1; ++s) {
-        const unsigned n = b.nch[s];
-        b.item_start[s] = ibase;
-        for (unsigned c = 0; c < n; ++c)
-            if (ibase + c < (unsigned)b.Wmax) b.items[ibase + c] = (unsigned)s | (c << 16);
-        ibase += n;
-    }
-    if (tid == 0) *b.nitems = ntotal < (unsigned)b.Wmax ? ntotal : (unsigned)b.Wmax;
+    if (*flag == 0u) return;                 // uniform across the group
+    build_strip_table(b, hist, hist + b.S);
 }
 
 // ---------------------------------------------------------------------------
@@ -279,7 +296,7 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill(
     const unsigned* xo = b.xoff + (size_t)(blockIdx.x % kCountSlots) * b.S;
     for (int s = tid; s < b.S; s += kBinThreads) cur[s] = xo[s] + row[s];
     __syncthreads();
-    Rec<T>* rec = reinterpret_cast<Rec<T>*>(b.recs);
+    vec4_t<T>* recg = reinterpret_cast<vec4_t<T>*>(b.recg);
     unsigned long long* Bm = reinterpret_cast<unsigned long long*>(b.B);
     const int c0 = blockIdx.x * kCellsPerGroup;
     T cx[kCellsPerThread], cy[kCellsPerThread], cw[kCellsPerThread], chh[kCellsPerThread];
@@ -325,16 +342,18 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill(
         // strip-relative record, evaluated in float64 and rounded once
         const double ex = (c.x - (g.xl + c.bxl * g.bsx)) * g.inv_bsx;
         const double ey = (c.y - (g.yl + c.byl * g.bsy)) * g.inv_bsy;
-        const vec4_t<T> geo = {(T)ex, (T)ey, (T)(c.w * g.inv_bsx), (T)(c.h * g.inv_bsy)};
-        const unsigned A = (unsigned)c.bxl | ((unsigned)(c.bxh - c.bxl) << 16);
-        const unsigned B = (unsigned)c.byl | ((unsigned)(c.byh - c.byl) << 16);
+        const vec4_t<T> geo = {(T)ex, (T)ey, (T)((double)cw[j] * g.inv_bsx),
+                               (T)((double)chh[j] * g.inv_bsy)};
+        const int nx = c.bxh - c.bxl, ny = c.byh - c.byl;
         const unsigned p0 = atomicAdd(&cur[s0], 1u);
-        rec[p0].set(geo, A, B, c.ratio, (unsigned)i);
+        recg[p0] = geo;
+        b.recm[p0] = span_word(c.bxl - (s0 << b.lgR), nx, ny, c.byl);
         b.pos[i] = p0;
         unsigned p1 = kPosNone;
         if (s1 != s0) {
             p1 = atomicAdd(&cur[s1], 1u);
-            rec[p1].set(geo, A, B, c.ratio, (unsigned)i | kSecondStrip);
+            recg[p1] = geo;
+            b.recm[p1] = span_word(c.bxl - (s1 << b.lgR), nx, ny, c.byl);
         }
         b.pos2[i] = p1;
     }
@@ -351,7 +370,9 @@ __device__ __forceinline__ void flush_value(unsigned long long v, size_t gi,
 
 // ---------------------------------------------------------------------------
 // K4: accumulate one (strip, chunk) work item in an LDS tile of R x N
-// uint64 fixed-point words.
+// uint64 fixed-point words and flush it.  A strip split into n > 1 chunks:
+// each chunk writes its tile to its partial slot; the last chunk to finish
+// adds the other n - 1 slots to its own tile and flushes the strip.
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
@@ -369,42 +390,43 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     const int R = b.R, N = g.N;
     const int RN = R * N;
     const int k0 = s * R, k1 = k0 + R - 1;
-    // read before the barriers below: thread 0 clears it after the flush
-    const bool single = b.nch[s] == 1u;
-    const bool bf = b.bigflag[s] != 0u;
+    const unsigned n = b.nch[s];
+    unsigned* last_flag = reinterpret_cast<unsigned*>(tile + RN);   // LDS word
     for (int e = tid; e < RN; e += kAccThreads) tile[e] = 0ull;
     __syncthreads();
 
     const unsigned e0 = b.strip_off[s] + (unsigned)chunk * (unsigned)b.CH;
     const unsigned eend = b.strip_off[s + 1];
     const unsigned e1 = min(e0 + (unsigned)b.CH, eend);
-    const Rec<T>* rec = reinterpret_cast<const Rec<T>*>(b.recs);
+    const vec4_t<T>* recg = reinterpret_cast<const vec4_t<T>*>(b.recg);
     const T fs = (T)g.fix_scale;
     constexpr int kBatch = 4;       // record loads in flight per thread
     for (unsigned eb = e0 + tid; eb < e1; eb += kBatch * kAccThreads) {
-        Rec<T> rb[kBatch];
+        vec4_t<T> rg[kBatch];
+        unsigned rm[kBatch];
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
             const unsigned e = eb + j * kAccThreads;
-            if (e < e1) rb[j] = rec[e];
+            if (e < e1) {
+                rg[j] = recg[e];
+                rm[j] = b.recm[e];
+            }
         }
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
             if (eb + j * kAccThreads >= e1) continue;
-            const Rec<T>& r = rb[j];
-            const unsigned Aw = rec_A(r), Bw = rec_B(r);
-            const int bxl = (int)(Aw & 0xFFFFu), nx = (int)(Aw >> 16);
-            const int byl = (int)(Bw & 0xFFFFu), ny = (int)(Bw >> 16);
-            const int ka = max(bxl, k0), kb = min(bxl + nx, k1);
-            const T dx = r.g.x, dy = r.g.y, xr = r.g.x + r.g.z, yr = r.g.y + r.g.w;
-            const T rat = r.ratio();
+            const SpanBox sb = span_of(rm[j], k0);
+            T xr, yr, rat;
+            stretch_of<T>(rg[j], g.stretch, xr, yr, rat);
+            const T dx = rg[j].x, dy = rg[j].y;
+            const int ka = max(sb.bxl, k0), kb = min(sb.bxl + sb.nx, k1);
             for (int k = ka; k <= kb; ++k) {
-                const T jx = (T)(k - bxl);
+                const T jx = (T)(k - sb.bxl);
                 const T tx = min(xr, jx + (T)1) - max(dx, jx);
                 if (!(tx > (T)0)) continue;
                 const T rtx = rat * tx;
-                A* trow = tile + (k - k0) * N + byl;
-                for (int q = 0; q <= ny; ++q) {
+                A* trow = tile + (k - k0) * N + sb.byl;
+                for (int q = 0; q <= sb.ny; ++q) {
                     const T ty = min(yr, (T)(q + 1)) - max(dy, (T)q);
                     if (!(ty > (T)0)) continue;
                     atomicAdd(&trow[q], to_fixed(rtx * ty, fs));
@@ -416,67 +438,53 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
 
     const size_t gbase = (size_t)k0 * N;
     const double inv = 1.0 / g.fix_scale;
-    if (single) {
-        A* Bm = reinterpret_cast<A*>(b.B);
-        if (!bf) {
-            // batches of U independent loads per thread; a tail loop takes
-            // what is left when R * N is not a multiple of U * kAccThreads
-            constexpr int U = 8;
-            int e = tid;
-            for (; e + (U - 1) * kAccThreads < RN; e += U * kAccThreads) {
-                A v[U];
-                T d[U];
-#pragma unroll
-                for (int j = 0; j < U; ++j) v[j] = tile[e + j * kAccThreads];
-#pragma unroll
-                for (int j = 0; j < U; ++j) d[j] = d0n[gbase + e + j * kAccThreads];
-#pragma unroll
-                for (int j = 0; j < U; ++j)
-                    dens[gbase + e + j * kAccThreads] = (T)((double)d[j] + (double)v[j] * inv);
-            }
-            for (; e < RN; e += kAccThreads) flush_value<T>(tile[e], gbase + e, d0n, dens, inv);
-        } else {
-            for (int e = tid; e < RN; e += kAccThreads) {
-                const A v = tile[e] + Bm[gbase + e];
-                Bm[gbase + e] = 0ull;
-                flush_value<T>(v, gbase + e, d0n, dens, inv);
-            }
-        }
-        __syncthreads();   // every thread has read bigflag[s]
-        if (bf && tid == 0) b.bigflag[s] = 0u;
-    } else {
-        A* slot = reinterpret_cast<A*>(b.partial) + (size_t)w * RN;
-        for (int e = tid; e < RN; e += kAccThreads) slot[e] = tile[e];
-    }
-}
-
-// ---------------------------------------------------------------------------
-// K4r: strips split into several chunks: rho = D0 + sum of partials (+B).
-// ---------------------------------------------------------------------------
-template <typename T>
-__global__ __launch_bounds__(kAccThreads) void k_strip_red(
-    Grid g, BinArgs b, const T* __restrict__ d0n, T* __restrict__ dens)
-{
-    using A = unsigned long long;
-    const int s = blockIdx.x;
-    const unsigned n = b.nch[s];
-    if (n == 1u) return;
-    const int tid = threadIdx.x;
-    const int RN = b.R * g.N;
-    const size_t gbase = (size_t)s * b.R * g.N;
-    const unsigned w0 = b.item_start[s];
-    const A* part = reinterpret_cast<const A*>(b.partial);
     A* Bm = reinterpret_cast<A*>(b.B);
-    const bool bf = b.bigflag[s] != 0u;
-    const double inv = 1.0 / g.fix_scale;
-    for (int e = tid; e < RN; e += kAccThreads) {
-        A v = 0ull;
-        for (unsigned c = 0; c < n; ++c) v += part[(size_t)(w0 + c) * RN + e];
-        if (bf) {
-            v += Bm[gbase + e];
-            Bm[gbase + e] = 0ull;
+    A* part = reinterpret_cast<A*>(b.partial);
+    if (n > 1u) {
+        // publish this chunk's tile; the last chunk of the strip continues
+        A* slot = part + (size_t)w * RN;
+        for (int e = tid; e < RN; e += kAccThreads) slot[e] = tile[e];
+        __threadfence();
+        __syncthreads();
+        if (tid == 0) *last_flag = atomicAdd(&b.done[s], 1u) == n - 1u ? 1u : 0u;
+        __syncthreads();
+        if (*last_flag == 0u) return;           // uniform across the group
+        __threadfence();
+        const unsigned w0 = b.item_start[s];
+        for (int e = tid; e < RN; e += kAccThreads) {
+            A v = tile[e];
+            for (unsigned c = 0; c < n; ++c)
+                if (w0 + c != (unsigned)w) v += part[(size_t)(w0 + c) * RN + e];
+            tile[e] = v;
         }
-        flush_value<T>(v, gbase + e, d0n, dens, inv);
+        if (tid == 0) b.done[s] = 0u;
+        __syncthreads();
+    }
+    // read before the barrier below: thread 0 clears it after the flush
+    const bool bf = b.bigflag[s] != 0u;
+    if (!bf) {
+        // batches of U independent loads per thread; a tail loop takes
+        // what is left when R * N is not a multiple of U * kAccThreads
+        constexpr int U = 8;
+        int e = tid;
+        for (; e + (U - 1) * kAccThreads < RN; e += U * kAccThreads) {
+            A v[U];
+            T d[U];
+#pragma unroll
+            for (int j = 0; j < U; ++j) v[j] = tile[e + j * kAccThreads];
+#pragma unroll
+            for (int j = 0; j < U; ++j) d[j] = d0n[gbase + e + j * kAccThreads];
+#pragma unroll
+            for (int j = 0; j < U; ++j)
+                dens[gbase + e + j * kAccThreads] = (T)((double)d[j] + (double)v[j] * inv);
+        }
+        for (; e < RN; e += kAccThreads) flush_value<T>(tile[e], gbase + e, d0n, dens, inv);
+    } else {
+        for (int e = tid; e < RN; e += kAccThreads) {
+            const A v = tile[e] + Bm[gbase + e];
+            Bm[gbase + e] = 0ull;
+            flush_value<T>(v, gbase + e, d0n, dens, inv);
+        }
     }
     __syncthreads();   // every thread has read bigflag[s]
     if (bf && tid == 0) b.bigflag[s] = 0u;
@@ -509,14 +517,15 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
     const int tid = threadIdx.x;
     const int R = b.R, N = g.N;
     const int RG = gather_rows<T>(R, N);
+    const int k0 = s * R;
     T* lfx = reinterpret_cast<T*>(smem);
     T* lfy = lfx + (size_t)RG * N;
     const unsigned e0 = b.strip_off[s] + (unsigned)chunk * (unsigned)b.CH;
     const unsigned e1 = min(e0 + (unsigned)b.CH, b.strip_off[s + 1]);
-    const Rec<T>* rec = reinterpret_cast<const Rec<T>*>(b.recs);
+    const vec4_t<T>* recg = reinterpret_cast<const vec4_t<T>*>(b.recg);
     vec2_t<T>* out = reinterpret_cast<vec2_t<T>*>(b.gtmp);
     const T ba = (T)(g.bsx * g.bsy);
-    for (int kg0 = s * R; kg0 < s * R + R; kg0 += RG) {
+    for (int kg0 = k0; kg0 < k0 + R; kg0 += RG) {
         const int kg1 = kg0 + RG - 1;
         __syncthreads();                    // previous group's readers done
         const size_t gb = (size_t)kg0 * N;
@@ -525,23 +534,23 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
             lfy[e] = fy[gb + e];
         }
         __syncthreads();
-        const bool first = kg0 == s * R;
+        const bool first = kg0 == k0;
         for (unsigned e = e0 + tid; e < e1; e += kAccThreads) {
-            const Rec<T> r = rec[e];
-            const unsigned Aw = rec_A(r), Bw = rec_B(r);
-            const int bxl = (int)(Aw & 0xFFFFu), nx = (int)(Aw >> 16);
-            const int byl = (int)(Bw & 0xFFFFu), ny = (int)(Bw >> 16);
-            const int ka = max(bxl, kg0), kb = min(bxl + nx, kg1);
-            const T dx = r.g.x, dy = r.g.y, xr = r.g.x + r.g.z, yr = r.g.y + r.g.w;
+            const vec4_t<T> rg = recg[e];
+            const SpanBox sb = span_of(b.recm[e], k0);
+            T xr, yr, rat;
+            stretch_of<T>(rg, g.stretch, xr, yr, rat);
+            const T dx = rg.x, dy = rg.y;
+            const int ka = max(sb.bxl, kg0), kb = min(sb.bxl + sb.nx, kg1);
             T ax = (T)0, ay = (T)0;
             for (int k = ka; k <= kb; ++k) {
-                const T jx = (T)(k - bxl);
+                const T jx = (T)(k - sb.bxl);
                 const T tx = min(xr, jx + (T)1) - max(dx, jx);
                 if (!(tx > (T)0)) continue;
-                const T* rx = lfx + (size_t)(k - kg0) * N + byl;
-                const T* ry = lfy + (size_t)(k - kg0) * N + byl;
+                const T* rx = lfx + (size_t)(k - kg0) * N + sb.byl;
+                const T* ry = lfy + (size_t)(k - kg0) * N + sb.byl;
                 T sx_ = (T)0, sy_ = (T)0;
-                for (int q = 0; q <= ny; ++q) {
+                for (int q = 0; q <= sb.ny; ++q) {
                     const T ty = min(yr, (T)(q + 1)) - max(dy, (T)q);
                     if (!(ty > (T)0)) continue;
                     sx_ += ty * rx[q];
@@ -550,7 +559,7 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
                 ax += tx * sx_;
                 ay += tx * sy_;
             }
-            const T sc = r.ratio() * ba;
+            const T sc = rat * ba;
             vec2_t<T> v = {sc * ax, sc * ay};
             if (!first) {
                 const vec2_t<T> o = out[e];

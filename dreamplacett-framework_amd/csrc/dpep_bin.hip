@@ -17,14 +17,13 @@ hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
                               hipEvent_t* ev)
 {
     b.G1 = (int)g1_of(nc);
-    const size_t tile = (size_t)b.R * g.N * sizeof(unsigned long long);
+    const size_t tile = (size_t)b.R * g.N * sizeof(unsigned long long) + 16;
+    const size_t count_lds = (size_t)(b.S + kBinThreads + 1) * sizeof(unsigned);
     const size_t hist = (size_t)b.S * sizeof(unsigned);
     hipError_t e;
-    k_bin_count<T><<<b.G1, kBinThreads, hist, s>>>(px, py, sx, sy, nc, g, b);
+    k_bin_count<T><<<b.G1, kBinThreads, count_lds, s>>>(px, py, sx, sy, nc, g, b);
     if ((e = hipGetLastError())) return e;
     if (ev && (e = hipEventRecord(ev[0], s))) return e;
-    k_bin_scan<<<1, kScanThreads, (size_t)(b.S + kScanThreads) * sizeof(unsigned), s>>>(b);
-    if ((e = hipGetLastError())) return e;
     if (ev && (e = hipEventRecord(ev[1], s))) return e;
     k_bin_fill<T><<<b.G1, kBinThreads, hist, s>>>(px, py, sx, sy, nc, g, b);
     if ((e = hipGetLastError())) return e;
@@ -32,8 +31,7 @@ hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
     k_strip_acc<T><<<b.Wmax, kAccThreads, tile, s>>>(g, b, d0n, dens);
     if ((e = hipGetLastError())) return e;
     if (ev && (e = hipEventRecord(ev[3], s))) return e;
-    k_strip_red<T><<<b.S, kAccThreads, 0, s>>>(g, b, d0n, dens);
-    return hipGetLastError();
+    return hipSuccess;
 }
 
 template <typename T>
@@ -57,7 +55,7 @@ static hipError_t prepare_bin_type()
 {
     hipError_t e = hipFuncSetAttribute((const void*)k_strip_acc<T>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)kTileBytes);
+                                       (int)kAccLds);
     if (e) return e;
     return hipFuncSetAttribute((const void*)k_gather_bin<T>,
                                hipFuncAttributeMaxDynamicSharedMemorySize,

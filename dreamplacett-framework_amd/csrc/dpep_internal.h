@@ -48,10 +48,9 @@ hipError_t launch_row_inv(const SpectralArgs& a, const T* Ux, const T* Uy,
 constexpr int kBinThreads = 256;       // K1 / K3 workgroup size
 constexpr int kCellsPerThread = 8;     // K1 / K3 cells per thread
 constexpr int kCellsPerGroup = kBinThreads * kCellsPerThread;
-constexpr int kAccThreads = 1024;      // K4 / K4r workgroup size
+constexpr int kAccThreads = 1024;      // K4 workgroup size
 constexpr int kCountSlots = 8;         // strip-total counters per strip
-constexpr int kScanThreads = 1024;     // K2 (one workgroup)
-constexpr unsigned kSecondStrip = 0x80000000u;
+constexpr int kMaxSpanY = 4095;        // larger y spans take the tall path
 
 // Shared between host (sizing) and device.
 struct BinArgs {
@@ -67,7 +66,10 @@ struct BinArgs {
     unsigned* item_start;   // [S] first work item of each strip
     unsigned* items;        // [Wmax] strip | chunk << 16
     unsigned* nitems;       // [1]
-    void* recs;             // [2 nc_max] strip records (Rec<T>)
+    unsigned* ticket;       // [1] K1 workgroups done (zero between steps)
+    unsigned* done;         // [S] K4 chunks done per strip (zero between steps)
+    void* recg;             // [2 nc_max] record geometry, vec4 of T
+    unsigned* recm;         // [2 nc_max] record span word
     unsigned* pos;          // [nc_max] record of cell i, or kPosTall / kPosNone
     unsigned* pos2;         // [nc_max] second-strip record of cell i, or kPosNone
     void* gtmp;             // [2 nc_max] vec2 forces in record order
@@ -78,18 +80,19 @@ struct BinArgs {
 
 // Host-side sizing of the binning buffers (shared with the CPU emulator).
 constexpr size_t kTileBytes = 131072;  // LDS tile of K4 (uint64 words) and G1
+constexpr size_t kAccLds = kTileBytes + 16;   // K4: tile + the last-chunk flag
 
 struct BinPlan {
     int S, R, lgR, G1max, CH, Wmax;
     size_t cap;             // records (2 per cell)
-    size_t rec_bytes;       // sizeof(Rec<T>): 32 (float) or 64 (double)
+    size_t geo_bytes;       // bytes of one record's geometry (4 elements)
     size_t partial_elems;   // Wmax * R * N
 };
 
 inline BinPlan make_bin_plan(int M, int N, int nc_max, size_t elem_bytes)
 {
     BinPlan p{};
-    p.rec_bytes = elem_bytes == 4 ? 32 : 64;
+    p.geo_bytes = 4 * elem_bytes;
     int R = 8;
     while (R > 1 && (size_t)R * N * 8 > kTileBytes) R >>= 1;
     if (R > M) R = M;
@@ -109,8 +112,9 @@ inline BinPlan make_bin_plan(int M, int N, int nc_max, size_t elem_bytes)
     return p;
 }
 
-// Strip-binned scatter (K1..K4r) and gather (G1, G2); ev (nullable)
-// receives 4 events recorded after K1, K2, K3 and K4.
+// Strip-binned scatter (K1, K3, K4) and gather (G1, G2); ev (nullable)
+// receives 4 events: after K1, again after K1 (the strip scan runs inside
+// it), after K3 and after K4.
 template <typename T>
 hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
                               const T* sy, int nc, const Grid& g, BinArgs b,

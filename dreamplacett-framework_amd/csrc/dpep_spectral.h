@@ -67,17 +67,14 @@ __device__ __forceinline__ T comp_of(const vec2_t<T>& c, int which)
 template <typename T>
 constexpr int kVec = 16 / (int)sizeof(T);
 
+// 1 / D(u, v) = 1 / (w_u^2 + w_v^2), zero at (0, 0).
 template <typename T>
-__device__ __forceinline__ T spectral_weight(int round, int u, int v,
-                                             const SpectralArgs& a)
+__device__ __forceinline__ T inv_d(int u, int v, const SpectralArgs& a)
 {
     if (u == 0 && v == 0) return (T)0;
     const T wu = (T)u * (T)a.wu_step;
     const T wv = (T)v * (T)a.wv_step;
-    const T inv = (T)1 / (wu * wu + wv * wv);
-    if (round == 0) return wu * inv * (T)0.5;
-    if (round == 1) return wv * inv * (T)0.5;
-    return inv;
+    return fast_rcp(wu * wu + wv * wv);
 }
 
 // Forward post-processing of slot s for two packed rows: returns X at k and m
@@ -281,10 +278,10 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
     for (int i = 0; i < E / 2; ++i) {
         const int s = t + TPF * i;
         const int k = s, m = (s == 0) ? L / 2 : L - s;
-        Ak[i].x *= spectral_weight<T>(2, k, v1, a);
-        Ak[i].y *= spectral_weight<T>(2, k, v2, a);
-        Am[i].x *= spectral_weight<T>(2, m, v1, a);
-        Am[i].y *= spectral_weight<T>(2, m, v2, a);
+        Ak[i].x *= inv_d<T>(k, v1, a);
+        Ak[i].y *= inv_d<T>(k, v2, a);
+        Am[i].x *= inv_d<T>(m, v1, a);
+        Am[i].y *= inv_d<T>(m, v2, a);
     }
     const T hu = (T)0.5 * (T)a.wu_step;
     const T hv1 = (T)0.5 * (T)v1 * (T)a.wv_step, hv2 = (T)0.5 * (T)v2 * (T)a.wv_step;
@@ -469,7 +466,7 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_inv(
 #pragma unroll
                 for (int q = 0; q < V; ++q) {
                     const int vq = v + q;
-                    const T up = r[i].v[q] / ((T)(vq > 0 ? vq : 1) * wv);
+                    const T up = r[i].v[q] * fast_rcp((T)(vq > 0 ? vq : 1) * wv);
                     comp<T>(rowp[lds_pad(vq)], x_in & 1) = up;
                 }
             }

@@ -142,8 +142,13 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     b.item_start = exact<unsigned>(p.S);
     b.items = exact<unsigned>(p.Wmax);
     b.nitems = exact<unsigned>(1);
-    b.recs = malloc(p.cap * p.rec_bytes);
-    if (sizeof(Rec<T>) != p.rec_bytes) { fprintf(stderr, "record size mismatch\n"); return 4; }
+    if (sizeof(vec4_t<T>) != p.geo_bytes) { fprintf(stderr, "record size mismatch\n"); return 4; }
+    b.recg = malloc(p.cap * p.geo_bytes);
+    b.recm = exact<unsigned>(p.cap);
+    b.ticket = exact<unsigned>(1);
+    b.done = exact<unsigned>(p.S);
+    *b.ticket = 0u;
+    memset(b.done, 0, p.S * sizeof(unsigned));
     b.pos = exact<unsigned>(nc > 0 ? nc : 1);
     b.pos2 = exact<unsigned>(nc > 0 ? nc : 1);
     b.gtmp = exact<vec2_t<T>>(p.cap);
@@ -155,11 +160,13 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     const size_t hist = (size_t)p.S * sizeof(unsigned);
     const size_t tile = (size_t)p.R * N * 8;
     for (int rep = 0; rep < 2; ++rep) {   // two steps: B / flags must be clean again
-        launch(b.G1, kBinThreads, hist, [&] { k_bin_count<T>(px, py, sx, sy, nc, g, b); });
-        launch(1, kScanThreads, (size_t)(p.S + kScanThreads) * sizeof(unsigned), [&] { k_bin_scan(b); });
+        launch(b.G1, kBinThreads, (size_t)(p.S + kBinThreads + 1) * sizeof(unsigned),
+               [&] { k_bin_count<T>(px, py, sx, sy, nc, g, b); });
         launch(b.G1, kBinThreads, hist, [&] { k_bin_fill<T>(px, py, sx, sy, nc, g, b); });
-        launch(p.Wmax, kAccThreads, tile, [&] { k_strip_acc<T>(g, b, d0n, dens); });
-        launch(p.S, kAccThreads, 0, [&] { k_strip_red<T>(g, b, d0n, dens); });
+        launch(p.Wmax, kAccThreads, tile + 16, [&] { k_strip_acc<T>(g, b, d0n, dens); });
+        if (*b.ticket) { fprintf(stderr, "K1 ticket left set\n"); return 4; }
+        for (int s2 = 0; s2 < p.S; ++s2)
+            if (b.done[s2]) { fprintf(stderr, "strip chunk counter left set\n"); return 4; }
         for (int s2 = 0; s2 < p.S; ++s2)
             if (b.bigflag[s2]) { fprintf(stderr, "bigflag left set\n"); return 4; }
         for (int s2 = 0; s2 < kCountSlots * p.S; ++s2)

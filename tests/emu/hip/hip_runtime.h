@@ -43,6 +43,7 @@ extern thread_local dim3 threadIdx, blockIdx;
 extern dim3 blockDim, gridDim;
 extern std::barrier<>* emu_barrier;
 inline void __syncthreads() { emu_barrier->arrive_and_wait(); }
+inline void __threadfence() { std::atomic_thread_fence(std::memory_order_seq_cst); }
 
 using std::floor;
 using std::isfinite;
@@ -51,6 +52,7 @@ inline unsigned long long __double2ull_rn(double x)
 {
     return (unsigned long long)std::nearbyint(x);
 }
+#define __builtin_amdgcn_rcpf(x) (1.0f / (x))
 inline unsigned long long __float2ull_rn(float x)
 {
     return (unsigned long long)std::nearbyint(x);
@@ -64,6 +66,11 @@ inline T unsafeAtomicAdd(T* p, T v)
 inline unsigned long long atomicAdd(unsigned long long* p, unsigned long long v)
 {
     return __atomic_fetch_add(p, v, __ATOMIC_RELAXED);
+}
+inline unsigned atomicExch(unsigned* p, unsigned v)
+{
+    std::atomic_ref<unsigned> r(*p);
+    return r.exchange(v);
 }
 inline unsigned atomicAdd(unsigned* p, unsigned v)
 {
