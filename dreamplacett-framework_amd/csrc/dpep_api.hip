@@ -4,8 +4,8 @@
 // allocated once at creation; a step allocates nothing.  Launch sequence of
 // one step on the context's stream:
 //   k_bin_count, k_bin_fill               counting sort of cells into strips
-//   k_strip_acc                           LDS strip accumulation, D0 fold
-//   k_row_dct   P1
+//   k_strip_acc                           LDS strip accumulation, D0 fold,
+//                                         and P1 (row DCT) of each strip
 //   k_col_pass  P2
 //   k_row_inv   P3  -> field_x, field_y, potential
 //   k_gather_bin, k_gather_out   per-cell forces <- fields
@@ -191,10 +191,9 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
                           : nullptr;
     HIP_TRY(hipEventRecord(c->ev[0], s));
     if (prof) HIP_TRY(hipEventRecord(pe[0], s));
-    HIP_TRY(launch_bin_scatter<T>(px, py, sx, sy, nc, c->grid, c->bins, d0n,
-                                  dens, s, prof ? pe + 1 : nullptr));
+    HIP_TRY(launch_bin_scatter<T>(px, py, sx, sy, nc, c->grid, c->bins, c->sargs, d0n,
+                                  dens, (T*)c->d_T, s, prof ? pe + 1 : nullptr));
     if (prof) HIP_TRY(hipEventRecord(pe[5], s));
-    HIP_TRY(launch_row_dct<T>(c->sargs, dens, (T*)c->d_T, s));
     if (prof) HIP_TRY(hipEventRecord(pe[6], s));
     HIP_TRY(launch_col_pass<T>(c->sargs, (T*)c->d_T, (T*)c->d_Ux, (T*)c->d_Uy, s));
     if (prof) HIP_TRY(hipEventRecord(pe[7], s));

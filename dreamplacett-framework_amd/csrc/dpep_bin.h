@@ -48,6 +48,7 @@
 #include <type_traits>
 
 #include "dpep_internal.h"
+#include "dpep_spectral.h"
 
 namespace dpep {
 
@@ -370,15 +371,39 @@ __device__ __forceinline__ void flush_value(unsigned long long v, size_t gi,
 
 // ---------------------------------------------------------------------------
 // K4: accumulate one (strip, chunk) work item in an LDS tile of R x N
-// uint64 fixed-point words and flush it.  A strip split into n > 1 chunks:
-// each chunk writes its tile to its partial slot; the last chunk to finish
-// adds the other n - 1 slots to its own tile and flushes the strip.
+// uint64 fixed-point words; the workgroup that completes a strip flushes it
+// (rho = D0 + tile (+B)) and runs the strip's row DCT-II (the first spectral
+// pass) on the rows it already holds, writing T in the tile layout: the
+// density is never read back.  A strip split into n > 1 chunks: each chunk
+// writes its tile to its partial slot; the last chunk to finish adds the
+// other n - 1 slots to its own tile and completes the strip.
 // ---------------------------------------------------------------------------
-template <typename T>
+__host__ __device__ constexpr int strip_rows(int N)
+{
+    int R = 8;
+    while (R > 1 && (size_t)R * N * 8 > kTileBytes) R >>= 1;
+    return R;
+}
+
+template <typename T, int L>
+__host__ __device__ constexpr size_t acc_lds_bytes()
+{
+    constexpr int R = strip_rows(L);
+    const size_t tile = (size_t)R * L * sizeof(unsigned long long) + 16;
+    const size_t fft = (size_t)(R / 2) * lds_len(L) * sizeof(vec2_t<T>);
+    return tile > fft ? tile : fft;
+}
+
+template <typename T, int L>
 __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
-    Grid g, BinArgs b, const T* __restrict__ d0n, T* __restrict__ dens)
+    Grid g, BinArgs b, SpectralArgs a, const T* __restrict__ d0n,
+    T* __restrict__ dens, T* __restrict__ Tt)
 {
     using A = unsigned long long;
+    using C = vec2_t<T>;
+    constexpr int R = strip_rows(L);
+    constexpr int RN = R * L;
+    constexpr int N = L;
     extern __shared__ __align__(16) unsigned char smem[];
     A* tile = reinterpret_cast<A*>(smem);
     const int w = blockIdx.x;
@@ -387,8 +412,6 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     const int s = (int)(item & 0xFFFFu);
     const int chunk = (int)(item >> 16);
     const int tid = threadIdx.x;
-    const int R = b.R, N = g.N;
-    const int RN = R * N;
     const int k0 = s * R, k1 = k0 + R - 1;
     const unsigned n = b.nch[s];
     unsigned* last_flag = reinterpret_cast<unsigned*>(tile + RN);   // LDS word
@@ -460,34 +483,107 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
         if (tid == 0) b.done[s] = 0u;
         __syncthreads();
     }
-    // read before the barrier below: thread 0 clears it after the flush
+
+    // ---- flush: rho = D0 + tile (+B), kept in registers ------------------
+    constexpr int PER = (RN + kAccThreads - 1) / kAccThreads;
     const bool bf = b.bigflag[s] != 0u;
-    if (!bf) {
-        // batches of U independent loads per thread; a tail loop takes
-        // what is left when R * N is not a multiple of U * kAccThreads
-        constexpr int U = 8;
-        int e = tid;
-        for (; e + (U - 1) * kAccThreads < RN; e += U * kAccThreads) {
-            A v[U];
-            T d[U];
+    T rv[PER];
+    {
+        A v[PER];
+        T d[PER];
 #pragma unroll
-            for (int j = 0; j < U; ++j) v[j] = tile[e + j * kAccThreads];
-#pragma unroll
-            for (int j = 0; j < U; ++j) d[j] = d0n[gbase + e + j * kAccThreads];
-#pragma unroll
-            for (int j = 0; j < U; ++j)
-                dens[gbase + e + j * kAccThreads] = (T)((double)d[j] + (double)v[j] * inv);
+        for (int j = 0; j < PER; ++j) {
+            const int e = tid + j * kAccThreads;
+            if (e < RN) {
+                v[j] = tile[e];
+                d[j] = d0n[gbase + e];
+            }
         }
-        for (; e < RN; e += kAccThreads) flush_value<T>(tile[e], gbase + e, d0n, dens, inv);
-    } else {
-        for (int e = tid; e < RN; e += kAccThreads) {
-            const A v = tile[e] + Bm[gbase + e];
-            Bm[gbase + e] = 0ull;
-            flush_value<T>(v, gbase + e, d0n, dens, inv);
+        if (bf) {
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const int e = tid + j * kAccThreads;
+                if (e < RN) {
+                    v[j] += Bm[gbase + e];
+                    Bm[gbase + e] = 0ull;
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int e = tid + j * kAccThreads;
+            if (e < RN) {
+                rv[j] = (T)((double)d[j] + (double)v[j] * inv);
+                dens[gbase + e] = rv[j];
+            }
         }
     }
-    __syncthreads();   // every thread has read bigflag[s]
+    __syncthreads();   // the tile is dead (the FFT buffers alias it); bigflag read
     if (bf && tid == 0) b.bigflag[s] = 0u;
+
+    // ---- row DCT-II of the strip's R rows: rows (2p, 2p+1) -> FFT slot p --
+    constexpr int LP = lds_len(L), E = fft_e(L), TPF = L / E;
+    C* sbuf = reinterpret_cast<C*>(smem);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int e = tid + j * kAccThreads;
+        if (e < RN) {
+            const int r = e / L, m = e % L;
+            comp<T>(sbuf[(r >> 1) * LP + lds_pad(makhoul_pos<L>(m))], r & 1) = rv[j];
+        }
+    }
+    __syncthreads();
+    const bool act = tid < (R / 2) * TPF;
+    const int f = act ? tid / TPF : 0, t = tid % TPF;
+    C* buf = sbuf + f * LP;
+    fft_lds<T, L, false>(buf, t, reinterpret_cast<const C*>(a.twN), act);
+    {
+        const C* post = reinterpret_cast<const C*>(a.postN);
+        const T scale = (T)2 / (T)L;
+        C Xk[E / 2], Xm[E / 2];
+        if (act) {
+#pragma unroll
+            for (int i = 0; i < E / 2; ++i)
+                dct_post<T, L>(buf, t + TPF * i, post, scale, Xk[i], Xm[i]);
+        }
+        __syncthreads();
+        if (act) {
+#pragma unroll
+            for (int i = 0; i < E / 2; ++i) {
+                const int sl = t + TPF * i;
+                buf[lds_pad(sl)] = Xk[i];
+                buf[lds_pad(sl == 0 ? L / 2 : L - sl)] = Xm[i];
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- T in the tile layout: bands of min(R, TX) rows ------------------
+    {
+        constexpr int V = kVec<T>;
+        const int TX = a.tiles.TX, TV = a.tiles.TV;
+        const int lgTV = __builtin_ctz(TV);
+        const int TE = TX * TV, NBV = L / TV;
+        const int TXe = R < TX ? R : TX;
+        const int lgTXe = __builtin_ctz(TXe);
+        constexpr int lgL = __builtin_ctz(L);
+        for (int n0 = tid * V; n0 < RN; n0 += kAccThreads * V) {
+            const int band = n0 >> (lgTXe + lgL);
+            const int nb = n0 & ((TXe << lgL) - 1);
+            const int bv = nb >> (lgTXe + lgTV);
+            const int wv = nb & ((TXe << lgTV) - 1);
+            const int r = band * TXe + (wv >> lgTV);        // row within the strip
+            const int x = k0 + r;
+            const int v = (bv << lgTV) + (wv & (TV - 1));
+            const C* rowp = sbuf + (r >> 1) * LP;
+            pack<T> o;
+#pragma unroll
+            for (int q = 0; q < V; ++q) o.v[q] = comp_of<T>(rowp[lds_pad(v + q)], r & 1);
+            const size_t gi = ((size_t)(x / TX) * NBV + bv) * TE + (size_t)(x % TX) * TV +
+                              (wv & (TV - 1));
+            *reinterpret_cast<pack<T>*>(Tt + gi) = o;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------

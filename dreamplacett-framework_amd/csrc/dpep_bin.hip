@@ -1,5 +1,7 @@
 // dpep_bin.hip -- host launchers of the strip-binned scatter and gather
 // (kernels in dpep_bin.h).
+#include <type_traits>
+
 #include "dpep_bin.h"
 
 namespace dpep {
@@ -10,14 +12,36 @@ static unsigned g1_of(int nc)
     return (unsigned)(g > 0 ? g : 1);
 }
 
+// k_strip_acc is instantiated per row length N (its row DCT is templated).
+template <typename T, typename Fn>
+static hipError_t dispatch_n(int N, Fn&& fn)
+{
+    switch (N) {
+    case 8: return fn(std::integral_constant<int, 8>{});
+    case 16: return fn(std::integral_constant<int, 16>{});
+    case 32: return fn(std::integral_constant<int, 32>{});
+    case 64: return fn(std::integral_constant<int, 64>{});
+    case 128: return fn(std::integral_constant<int, 128>{});
+    case 256: return fn(std::integral_constant<int, 256>{});
+    case 512: return fn(std::integral_constant<int, 512>{});
+    case 1024: return fn(std::integral_constant<int, 1024>{});
+    case 2048: return fn(std::integral_constant<int, 2048>{});
+    case 4096: return fn(std::integral_constant<int, 4096>{});
+    case 8192:
+        if constexpr (sizeof(T) == 4) return fn(std::integral_constant<int, 8192>{});
+        else return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+    }
+}
+
 template <typename T>
 hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
                               const T* sy, int nc, const Grid& g,
-                              BinArgs b, const T* d0n, T* dens, hipStream_t s,
-                              hipEvent_t* ev)
+                              BinArgs b, const SpectralArgs& a, const T* d0n, T* dens,
+                              T* Tt, hipStream_t s, hipEvent_t* ev)
 {
     b.G1 = (int)g1_of(nc);
-    const size_t tile = (size_t)b.R * g.N * sizeof(unsigned long long) + 16;
+    if (b.R != strip_rows(g.N)) return hipErrorInvalidValue;   // the kernel's R
     const size_t count_lds = (size_t)(b.S + kBinThreads + 1) * sizeof(unsigned);
     const size_t hist = (size_t)b.S * sizeof(unsigned);
     hipError_t e;
@@ -28,8 +52,13 @@ hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
     k_bin_fill<T><<<b.G1, kBinThreads, hist, s>>>(px, py, sx, sy, nc, g, b);
     if ((e = hipGetLastError())) return e;
     if (ev && (e = hipEventRecord(ev[2], s))) return e;
-    k_strip_acc<T><<<b.Wmax, kAccThreads, tile, s>>>(g, b, d0n, dens);
-    if ((e = hipGetLastError())) return e;
+    e = dispatch_n<T>(g.N, [&](auto lc) -> hipError_t {
+        constexpr int L = decltype(lc)::value;
+        k_strip_acc<T, L><<<b.Wmax, kAccThreads, acc_lds_bytes<T, L>(), s>>>(g, b, a, d0n,
+                                                                             dens, Tt);
+        return hipGetLastError();
+    });
+    if (e) return e;
     if (ev && (e = hipEventRecord(ev[3], s))) return e;
     return hipSuccess;
 }
@@ -53,9 +82,14 @@ hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
 template <typename T>
 static hipError_t prepare_bin_type()
 {
-    hipError_t e = hipFuncSetAttribute((const void*)k_strip_acc<T>,
+    hipError_t e = hipSuccess;
+    for (int N = 8; N <= (sizeof(T) == 4 ? 8192 : 4096) && !e; N *= 2)
+        e = dispatch_n<T>(N, [&](auto lc) -> hipError_t {
+            constexpr int L = decltype(lc)::value;
+            return hipFuncSetAttribute((const void*)k_strip_acc<T, L>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)kAccLds);
+                                       (int)acc_lds_bytes<T, L>());
+        });
     if (e) return e;
     return hipFuncSetAttribute((const void*)k_gather_bin<T>,
                                hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -71,11 +105,13 @@ hipError_t bin_prepare()
 
 template hipError_t launch_bin_scatter<float>(const float*, const float*, const float*,
                                               const float*, int, const Grid&, BinArgs,
-                                              const float*, float*, hipStream_t, hipEvent_t*);
+                                              const SpectralArgs&, const float*, float*,
+                                              float*, hipStream_t, hipEvent_t*);
 template hipError_t launch_bin_scatter<double>(const double*, const double*,
                                                const double*, const double*, int,
-                                               const Grid&, BinArgs, const double*,
-                                               double*, hipStream_t, hipEvent_t*);
+                                               const Grid&, BinArgs, const SpectralArgs&,
+                                               const double*, double*, double*,
+                                               hipStream_t, hipEvent_t*);
 template hipError_t launch_bin_gather<float>(const float*, const float*, const float*,
                                              const float*, int, const Grid&,
                                              const BinArgs&, const float*, const float*,

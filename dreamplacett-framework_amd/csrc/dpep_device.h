@@ -270,15 +270,19 @@ __device__ __forceinline__ void dft_r(vec2_t<T>* v)
 
 // One Stockham stage over the FFT held in `buf` (LDS, padded indexing).
 // t: this thread's index within the FFT's TPF threads.  tw: exp(-2 pi i m/L).
+// act = false: a thread of the workgroup that holds no FFT; it only takes
+// part in the barriers.
 template <typename T, int L, int R, int NS, bool INV>
 __device__ __forceinline__ void fft_stage(vec2_t<T>* buf, int t,
-                                          const vec2_t<T>* __restrict__ tw)
+                                          const vec2_t<T>* __restrict__ tw,
+                                          bool act)
 {
     using C = vec2_t<T>;
     constexpr int E = fft_e(L);
     constexpr int TPF = L / E;
     constexpr int NB = E / R;
     C v[NB][R];
+    if (act) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         const int j = t + TPF * b;
@@ -309,7 +313,9 @@ __device__ __forceinline__ void fft_stage(vec2_t<T>* buf, int t,
         }
         dft_r<T, R, INV>(v[b]);
     }
+    }
     __syncthreads();
+    if (act) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         const int j = t + TPF * b;
@@ -318,27 +324,32 @@ __device__ __forceinline__ void fft_stage(vec2_t<T>* buf, int t,
 #pragma unroll
         for (int r = 0; r < R; ++r) buf[lds_pad(base + r * NS)] = v[b][r];
     }
+    }
     __syncthreads();
 }
 
 template <typename T, int L, int NS, bool INV>
 __device__ __forceinline__ void fft_stages(vec2_t<T>* buf, int t,
-                                           const vec2_t<T>* __restrict__ tw)
+                                           const vec2_t<T>* __restrict__ tw,
+                                           bool act)
 {
     if constexpr (NS < L) {
         constexpr int REM = L / NS;
         constexpr int R = REM >= fft_e(L) ? fft_e(L) : REM;
-        fft_stage<T, L, R, NS, INV>(buf, t, tw);
-        fft_stages<T, L, NS * R, INV>(buf, t, tw);
+        fft_stage<T, L, R, NS, INV>(buf, t, tw, act);
+        fft_stages<T, L, NS * R, INV>(buf, t, tw, act);
     }
 }
 
-// Full in-place FFT; caller must __syncthreads() before (data in LDS).
+// Full in-place FFT; caller must __syncthreads() before (data in LDS).  Every
+// thread of the workgroup calls it (the stages hold barriers); threads with
+// act = false hold no FFT.
 template <typename T, int L, bool INV>
 __device__ __forceinline__ void fft_lds(vec2_t<T>* buf, int t,
-                                        const vec2_t<T>* __restrict__ tw)
+                                        const vec2_t<T>* __restrict__ tw,
+                                        bool act = true)
 {
-    fft_stages<T, L, 1, INV>(buf, t, tw);
+    fft_stages<T, L, 1, INV>(buf, t, tw, act);
 }
 
 }  // namespace dpep

@@ -34,9 +34,6 @@ struct SpectralArgs {
 
 // Launchers (return hipError_t of the launch).  T = float or double.
 template <typename T>
-hipError_t launch_row_dct(const SpectralArgs& a, const T* density, T* Tt,
-                          hipStream_t s);
-template <typename T>
 hipError_t launch_col_pass(const SpectralArgs& a, const T* Tt, T* Ux, T* Uy,
                            hipStream_t s);
 template <typename T>
@@ -80,7 +77,6 @@ struct BinArgs {
 
 // Host-side sizing of the binning buffers (shared with the CPU emulator).
 constexpr size_t kTileBytes = 131072;  // LDS tile of K4 (uint64 words) and G1
-constexpr size_t kAccLds = kTileBytes + 16;   // K4: tile + the last-chunk flag
 
 struct BinPlan {
     int S, R, lgR, G1max, CH, Wmax;
@@ -112,14 +108,14 @@ inline BinPlan make_bin_plan(int M, int N, int nc_max, size_t elem_bytes)
     return p;
 }
 
-// Strip-binned scatter (K1, K3, K4) and gather (G1, G2); ev (nullable)
-// receives 4 events: after K1, again after K1 (the strip scan runs inside
-// it), after K3 and after K4.
+// Strip-binned scatter (K1, K3, K4; K4 also runs the row DCT, writing T)
+// and gather (G1, G2); ev (nullable) receives 4 events: after K1, again
+// after K1 (the strip scan runs inside it), after K3 and after K4.
 template <typename T>
 hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
                               const T* sy, int nc, const Grid& g, BinArgs b,
-                              const T* d0n, T* dens, hipStream_t s,
-                              hipEvent_t* ev);
+                              const SpectralArgs& a, const T* d0n, T* dens, T* Tt,
+                              hipStream_t s, hipEvent_t* ev);
 template <typename T>
 hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
                              const T* sy, int nc, const Grid& g,

@@ -31,13 +31,15 @@
 // (the FFT's rounding is relative to the pair, not to each column).
 //
 // Passes and HBM traffic (MN = M*N elements):
-//   P1  k_row_dct : rho rows (along y)  -> T        tiled      read MN, write MN
+//   P1  (in k_strip_acc, dpep_bin.h): each strip's rows, already in LDS after
+//       the density flush -> T tiled                             write MN
 //   P2  k_col_pass: T rows (along x)    -> Ux, Uy   tiled      read MN, write 2MN
 //                   (DCT-II, weights, two inverse transforms)
 //   P3  k_row_inv : Ux, Uy rows (y)     -> fx, fy, phi         read 2MN, write 3MN
-// Tiles of TX x TV elements (TX = rows of a P1 workgroup, TV = rows of a P2
-// workgroup) make every global access a run of >= 128 contiguous bytes while
-// P1 and P2 write "transposed" relative to the rows they process.
+// Tiles of TX x TV elements (TX = 2 fpw(N), the rows of a P3 type-B
+// workgroup; TV = 2 fpw(M), the columns of a P2 workgroup) make every global
+// access a run of >= 128 contiguous bytes while P1 and P2 write "transposed"
+// relative to the rows they process.
 #pragma once
 
 #include "dpep_internal.h"
@@ -135,77 +137,6 @@ __device__ __forceinline__ vec2_t<T> pack2(vec2_t<T> v1, vec2_t<T> v2)
 {
     // v1 + i v2
     return vec2_t<T>{v1.x - v2.y, v1.y + v2.x};
-}
-
-// ---------------------------------------------------------------------------
-// P1: forward DCT-II along y of 2F rows of rho; writes T (tiled).
-// ---------------------------------------------------------------------------
-template <typename T, int L, int F>
-__global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_dct(
-    SpectralArgs a, const T* __restrict__ density_in, T* __restrict__ Tt)
-{
-    using C = vec2_t<T>;
-    constexpr int E = fft_e(L), TPF = L / E, NT = F * TPF, LP = lds_len(L);
-    constexpr int TX = 2 * F;
-    extern __shared__ __align__(16) unsigned char smem[];
-    C* sb = reinterpret_cast<C*>(smem);
-    const int tid = threadIdx.x, f = tid / TPF, t = tid % TPF;
-    C* buf = sb + f * LP;
-    const int x0 = blockIdx.x * TX;
-    const size_t base = (size_t)x0 * L;
-
-    constexpr int V = kVec<T>, NV = TX * L / (NT * V);
-    static_assert(NV * NT * V == TX * L, "P1 block is not a whole number of vectors");
-    {
-        const pack<T>* src = reinterpret_cast<const pack<T>*>(density_in + base);
-        pack<T> r[NV];
-#pragma unroll
-        for (int i = 0; i < NV; ++i) r[i] = src[tid + i * NT];
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int e0 = (tid + i * NT) * V;
-            const int row = e0 / L, m0 = e0 % L;
-            C* rowp = sb + (row >> 1) * LP;
-#pragma unroll
-            for (int q = 0; q < V; ++q)
-                comp<T>(rowp[lds_pad(makhoul_pos<L>(m0 + q))], row & 1) = r[i].v[q];
-        }
-    }
-    __syncthreads();
-    fft_lds<T, L, false>(buf, t, reinterpret_cast<const C*>(a.twN));
-
-    const C* post = reinterpret_cast<const C*>(a.postN);
-    const T scale = (T)2 / (T)L;
-    C Xk[E / 2], Xm[E / 2];
-#pragma unroll
-    for (int i = 0; i < E / 2; ++i)
-        dct_post<T, L>(buf, t + TPF * i, post, scale, Xk[i], Xm[i]);
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < E / 2; ++i) {
-        const int s = t + TPF * i;
-        buf[lds_pad(s)] = Xk[i];
-        buf[lds_pad(s == 0 ? L / 2 : L - s)] = Xm[i];
-    }
-    __syncthreads();
-
-    const int TV = a.tiles.TV;
-    const int lgTV = __builtin_ctz(TV);
-    const int lgTE = __builtin_ctz(TX) + lgTV;
-    pack<T>* out = reinterpret_cast<pack<T>*>(Tt + base);
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int e0 = (tid + i * NT) * V;        // V consecutive v of one x
-        const int bv = e0 >> lgTE;
-        const int w = e0 & ((1 << lgTE) - 1);
-        const int x_in = w >> lgTV;
-        const int v = (bv << lgTV) + (w & (TV - 1));
-        const C* rowp = sb + (x_in >> 1) * LP;
-        pack<T> o;
-#pragma unroll
-        for (int q = 0; q < V; ++q) o.v[q] = comp_of<T>(rowp[lds_pad(v + q)], x_in & 1);
-        out[tid + i * NT] = o;
-    }
 }
 
 // ---------------------------------------------------------------------------

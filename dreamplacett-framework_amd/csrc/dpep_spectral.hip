@@ -46,19 +46,6 @@ static hipError_t dispatch_len(int L, Fn&& fn)
 }
 
 template <typename T>
-hipError_t launch_row_dct(const SpectralArgs& a, const T* density, T* Tt,
-                          hipStream_t s)
-{
-    return dispatch_len<T>(a.N, [&](auto lc) -> hipError_t {
-        constexpr int L = decltype(lc)::value;
-        constexpr int F = fpw<T>(L);
-        const dim3 grid(a.M / (2 * F)), block(threads_of<T, L>());
-        k_row_dct<T, L, F><<<grid, block, lds_bytes<T, L>(), s>>>(a, density, Tt);
-        return hipGetLastError();
-    });
-}
-
-template <typename T>
 hipError_t launch_col_pass(const SpectralArgs& a, const T* Tt, T* Ux, T* Uy,
                            hipStream_t s)
 {
@@ -91,9 +78,6 @@ static hipError_t prepare_len()
     constexpr int F = fpw<T>(L);
     const int bytes = (int)lds_bytes<T, L>();
     hipError_t e;
-    if ((e = hipFuncSetAttribute((const void*)k_row_dct<T, L, F>,
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, bytes)))
-        return e;
     if ((e = hipFuncSetAttribute((const void*)k_col_pass<T, L, F>,
                                  hipFuncAttributeMaxDynamicSharedMemorySize, bytes)))
         return e;
@@ -127,10 +111,6 @@ hipError_t spectral_prepare()
     return prepare_type<double>();
 }
 
-template hipError_t launch_row_dct<float>(const SpectralArgs&, const float*,
-                                          float*, hipStream_t);
-template hipError_t launch_row_dct<double>(const SpectralArgs&, const double*,
-                                           double*, hipStream_t);
 template hipError_t launch_col_pass<float>(const SpectralArgs&, const float*,
                                            float*, float*, hipStream_t);
 template hipError_t launch_col_pass<double>(const SpectralArgs&, const double*,

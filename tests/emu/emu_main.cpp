@@ -158,12 +158,12 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     memset(b.B, 0, mn * 8);
     memset(b.bigflag, 0, p.S * sizeof(unsigned));
     const size_t hist = (size_t)p.S * sizeof(unsigned);
-    const size_t tile = (size_t)p.R * N * 8;
     for (int rep = 0; rep < 2; ++rep) {   // two steps: B / flags must be clean again
         launch(b.G1, kBinThreads, (size_t)(p.S + kBinThreads + 1) * sizeof(unsigned),
                [&] { k_bin_count<T>(px, py, sx, sy, nc, g, b); });
         launch(b.G1, kBinThreads, hist, [&] { k_bin_fill<T>(px, py, sx, sy, nc, g, b); });
-        launch(p.Wmax, kAccThreads, tile + 16, [&] { k_strip_acc<T>(g, b, d0n, dens); });
+        launch(p.Wmax, kAccThreads, acc_lds_bytes<T, LN>(),
+               [&] { k_strip_acc<T, LN>(g, b, a, d0n, dens, Tt); });
         if (*b.ticket) { fprintf(stderr, "K1 ticket left set\n"); return 4; }
         for (int s2 = 0; s2 < p.S; ++s2)
             if (b.done[s2]) { fprintf(stderr, "strip chunk counter left set\n"); return 4; }
@@ -171,12 +171,6 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
             if (b.bigflag[s2]) { fprintf(stderr, "bigflag left set\n"); return 4; }
         for (int s2 = 0; s2 < kCountSlots * p.S; ++s2)
             if (b.xtot[s2]) { fprintf(stderr, "slot totals left set\n"); return 4; }
-    }
-    {
-        constexpr int F = fpw<T>(LN);
-        const size_t shm = (size_t)F * lds_len(LN) * sizeof(vec2_t<T>);
-        const unsigned nt = F * (LN / fft_e(LN));
-        launch(M / (2 * F), nt, shm, [&] { k_row_dct<T, LN, F>(a, dens, Tt); });
     }
     {
         constexpr int F = fpw<T>(LM);
