@@ -32,7 +32,7 @@ HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "kernels_c3_1.1M_2048.md")
 # kernel name prefix in the rocprofv3 summary for each bench kernel key
 PMC_NAMES = {"bin_count": "k_bin_count", "bin_fill": "k_bin_fill",
-             "strip_acc": "k_strip_acc", "row_dct": "k_row_dct",
+             "strip_acc": "k_strip_acc",
              "col_pass": "k_col_pass", "row_inv": "k_row_inv",
              "gather": ("k_gather_bin", "k_gather_out")}
 METRIC = ("ms per potential step (scatter+DCT+field), 1.1M cells @2048^2; "
@@ -46,11 +46,8 @@ def kernel_bytes(nc, M, N, esz, potential=True):
     nmaps = 3 if potential else 2
     return {
         "bin_count": 4 * esz * nc,                     # read cells
-        "bin_scan": 0,                                 # strip table only
         "bin_fill": 4 * esz * nc,                      # read cells (+ sorted entries: scratch)
-        "strip_acc": 2 * esz * mn,                     # read D0, write rho (+ entries: scratch)
-        "strip_red": 0,                                # split strips only
-        "row_dct": 2 * esz * mn,                       # read rho, write T
+        "strip_acc": 3 * esz * mn,                     # read D0, write rho and T (row DCT fused)
         "col_pass": 3 * esz * mn,                      # read T, write Ux, Uy
         "row_inv": (2 + nmaps) * esz * mn,             # read Ux, Uy, write maps
         "gather": 6 * esz * nc + 2 * esz * mn,         # cells, fields, forces
@@ -77,13 +74,15 @@ def pmc_traffic(key):
 
 
 def step_bytes(nc, M, N, esz, potential=True):
-    """The step's byte model: 10 e Nc + 14 e MN (e = element size), i.e.
-    40 Nc + 56 MN at float32; e MN less without the potential.  Cells are
-    read twice (scatter, gather) and the forces written; the maps: D0 and rho
-    (2), P1 (2), P2 (3), P3 (2 in, 3 out), the gather's two field maps (2).
-    The potential's own column transforms are not needed (Up = Uy / w_v),
-    so the 3-pass model's 64 MN round trip of Up is not moved."""
-    return 10 * esz * nc + (14 if potential else 13) * esz * M * N
+    """The step's byte model: 10 e Nc + 13 e MN (e = element size), i.e.
+    40 Nc + 52 MN at float32; e MN less without the potential.  Cells are
+    read twice (scatter, gather) and the forces written; the maps: D0 in,
+    rho and T out (3, the row DCT runs on the accumulated strips), the column
+    pass (1 in, 2 out), the row inverse (2 in, 3 out) and the gather's two
+    field maps (2).  The potential needs no column transforms of its own
+    (Up = Uy / w_v) and the density is not re-read, so the 3-pass model's
+    64 MN is not what this step has to move."""
+    return 10 * esz * nc + (13 if potential else 12) * esz * M * N
 
 
 def cpu_baseline(w, seconds, max_steps=20):

@@ -49,8 +49,9 @@ int fail(int code, const char* fmt, ...)
                         hipGetErrorString(e_));                              \
     } while (0)
 
-// bin_count, bin_scan, bin_fill, strip_acc, strip_red, P1, P2, P3, gather
-constexpr int kNumStages = 9;
+// strip count (+ table), strip fill, strip accumulate (+ row DCT), column
+// pass, row inverse, gather
+constexpr int kNumStages = 6;
 
 bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
@@ -193,13 +194,12 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
     if (prof) HIP_TRY(hipEventRecord(pe[0], s));
     HIP_TRY(launch_bin_scatter<T>(px, py, sx, sy, nc, c->grid, c->bins, c->sargs, d0n,
                                   dens, (T*)c->d_T, s, prof ? pe + 1 : nullptr));
-    if (prof) HIP_TRY(hipEventRecord(pe[5], s));
-    if (prof) HIP_TRY(hipEventRecord(pe[6], s));
+
     HIP_TRY(launch_col_pass<T>(c->sargs, (T*)c->d_T, (T*)c->d_Ux, (T*)c->d_Uy, s));
-    if (prof) HIP_TRY(hipEventRecord(pe[7], s));
+    if (prof) HIP_TRY(hipEventRecord(pe[4], s));
     HIP_TRY(launch_row_inv<T>(c->sargs, (const T*)c->d_Ux, (const T*)c->d_Uy, fx, fy,
                               phi, s));
-    if (prof) HIP_TRY(hipEventRecord(pe[8], s));
+    if (prof) HIP_TRY(hipEventRecord(pe[5], s));
     if (gather)
         HIP_TRY(launch_bin_gather<T>(px, py, sx, sy, nc, c->grid, c->bins, fx, fy,
                                      gx, gy, s));
@@ -305,6 +305,11 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
     a.M = M; a.N = N;
     a.tiles.TX = 2 * spectral_fpw(N, dtype);
     a.tiles.TV = 2 * spectral_fpw(M, dtype);
+    {
+        int R = 8;   // rows per strip, as the binning plan sizes them
+        while (R > 1 && (size_t)R * N * 8 > kTileBytes) R >>= 1;
+        a.tiles.TXT = R > a.tiles.TX ? R : a.tiles.TX;
+    }
     a.wu_step = 2.0 * M_PI / M;
     a.wv_step = 2.0 * M_PI / N * (g.bsx / g.bsy);
     a.potential = (flags & DPEP_FLAG_NO_POTENTIAL) ? 0 : 1;
@@ -496,9 +501,9 @@ int dpep_get_timings(dpep_ctx* c, float* out)
     if (c->profiling && c->prof_steps > 0) {
         const hipEvent_t* pe = &c->prof_ev[(size_t)((c->prof_steps - 1) % c->prof_slots) *
                                            (kNumStages + 1)];
-        out[1] = elapsed(pe[0], pe[5]);              // binning + accumulation
-        out[5] = elapsed(pe[5], pe[8]);              // P1 + P2 + P3
-        out[2] = elapsed(pe[8], pe[kNumStages]);     // gather
+        out[1] = elapsed(pe[0], pe[3]);              // binning, accumulation, P1
+        out[5] = elapsed(pe[3], pe[5]);              // P2 + P3
+        out[2] = elapsed(pe[5], pe[kNumStages]);     // gather
     } else {
         out[5] = total;
     }

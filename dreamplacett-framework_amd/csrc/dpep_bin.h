@@ -561,7 +561,7 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     // ---- T in the tile layout: bands of min(R, TX) rows ------------------
     {
         constexpr int V = kVec<T>;
-        const int TX = a.tiles.TX, TV = a.tiles.TV;
+        const int TX = a.tiles.TXT, TV = a.tiles.TV;
         const int lgTV = __builtin_ctz(TV);
         const int TE = TX * TV, NBV = L / TV;
         const int TXe = R < TX ? R : TX;

@@ -48,10 +48,9 @@ hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
     k_bin_count<T><<<b.G1, kBinThreads, count_lds, s>>>(px, py, sx, sy, nc, g, b);
     if ((e = hipGetLastError())) return e;
     if (ev && (e = hipEventRecord(ev[0], s))) return e;
-    if (ev && (e = hipEventRecord(ev[1], s))) return e;
     k_bin_fill<T><<<b.G1, kBinThreads, hist, s>>>(px, py, sx, sy, nc, g, b);
     if ((e = hipGetLastError())) return e;
-    if (ev && (e = hipEventRecord(ev[2], s))) return e;
+    if (ev && (e = hipEventRecord(ev[1], s))) return e;
     e = dispatch_n<T>(g.N, [&](auto lc) -> hipError_t {
         constexpr int L = decltype(lc)::value;
         k_strip_acc<T, L><<<b.Wmax, kAccThreads, acc_lds_bytes<T, L>(), s>>>(g, b, a, d0n,
@@ -59,7 +58,7 @@ hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
         return hipGetLastError();
     });
     if (e) return e;
-    if (ev && (e = hipEventRecord(ev[3], s))) return e;
+    if (ev && (e = hipEventRecord(ev[2], s))) return e;
     return hipSuccess;
 }
 

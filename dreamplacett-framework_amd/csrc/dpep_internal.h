@@ -11,13 +11,15 @@ namespace dpep {
 
 // Rows per workgroup of the spectral passes are 2*F where F is the number of
 // complex FFTs a workgroup holds in LDS.  The intermediate matrices are
-// stored in tiles of (2*F_N) x (2*F_M) elements so that every pass moves
-// whole tiles (>= 128 contiguous bytes) through HBM.
+// stored in tiles (T: TXT x TV, Ux / Uy: TX x TV elements) so that the passes
+// move runs of whole tiles through HBM while writing "transposed".
 int spectral_fpw(int L, int dtype);
 
 struct Tiles {
-    int TX;   // tile extent along x  (= 2 * F of the length-N passes)
-    int TV;   // tile extent along v  (= 2 * F of the length-M pass)
+    int TX;   // tile extent along x of Ux, Uy (= 2 * F of the length-N passes)
+    int TV;   // tile extent along v of T, Ux, Uy (= 2 * F of the length-M pass)
+    int TXT;  // tile extent along x of T: max(TX, rows per strip), so that
+              // the column pass reads whole >= 128-byte tiles
 };
 
 struct SpectralArgs {
@@ -109,8 +111,7 @@ inline BinPlan make_bin_plan(int M, int N, int nc_max, size_t elem_bytes)
 }
 
 // Strip-binned scatter (K1, K3, K4; K4 also runs the row DCT, writing T)
-// and gather (G1, G2); ev (nullable) receives 4 events: after K1, again
-// after K1 (the strip scan runs inside it), after K3 and after K4.
+// and gather (G1, G2); ev (nullable) receives 3 events: after K1, K3, K4.
 template <typename T>
 hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
                               const T* sy, int nc, const Grid& g, BinArgs b,

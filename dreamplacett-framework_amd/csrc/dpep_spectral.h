@@ -36,20 +36,24 @@
 //   P2  k_col_pass: T rows (along x)    -> Ux, Uy   tiled      read MN, write 2MN
 //                   (DCT-II, weights, two inverse transforms)
 //   P3  k_row_inv : Ux, Uy rows (y)     -> fx, fy, phi         read 2MN, write 3MN
-// Tiles of TX x TV elements (TX = 2 fpw(N), the rows of a P3 type-B
-// workgroup; TV = 2 fpw(M), the columns of a P2 workgroup) make every global
-// access a run of >= 128 contiguous bytes while P1 and P2 write "transposed"
-// relative to the rows they process.
+// T is stored in tiles of TXT x TV elements and Ux, Uy in tiles of TX x TV
+// (TV = 2 fpw(M), the columns of a P2 workgroup; TX = 2 fpw(N), the rows of
+// a P3 type-B workgroup; TXT >= the rows of a strip, the rows P1 writes at
+// once): every global access is a run of whole tiles while P1 and P2 write
+// "transposed" relative to the rows they process.
 #pragma once
 
 #include "dpep_internal.h"
 
 namespace dpep {
 
+// FFTs held by one workgroup of the length-L passes.  Two at L = 2048 (not
+// four): twice the workgroups, two of them per CU, measured 2-3 us faster
+// per pass at 2048 x 2048.
 template <typename T>
 __host__ __device__ constexpr int fpw(int L)
 {
-    return sizeof(T) == 4 ? (L <= 2048 ? 4 : 2) : 2;
+    return sizeof(T) == 4 ? (L <= 1024 ? 4 : 2) : 2;
 }
 
 template <typename T>
@@ -155,8 +159,10 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
     C* sb = reinterpret_cast<C*>(smem);
     const int tid = threadIdx.x, f = tid / TPF, t = tid % TPF;
     C* buf = sb + f * LP;
-    const int TX = a.tiles.TX;
+    const int TX = a.tiles.TX;            // Ux, Uy tiles (stores)
     const int lgTX = __builtin_ctz(TX);
+    const int TXT = a.tiles.TXT;          // T tiles (loads)
+    const int lgTXT = __builtin_ctz(TXT);
     const int NBV = a.N / TV;
     const int b2 = blockIdx.x;
     const int v0 = b2 * TV;
@@ -164,26 +170,29 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
     const int tile_elems = TX * TV;
     const int lgTE = lgTX + lgTV;
 
-    // load the tiles (bx, b2) for every bx: each vector holds V consecutive
-    // columns v (pairs of them form the complex input of one FFT) of one x
+    // load the tiles (bx, b2) of T for every bx: each vector holds V
+    // consecutive columns v (pairs of them form the complex input of one
+    // FFT) of one x
     constexpr int V = kVec<T>, NV = L * TV / (NT * V);
     static_assert(NV * NT * V == L * TV && V % 2 == 0 && TV % V == 0, "P2 vector split");
     {
+        const int tile_t = TXT * TV;
+        const int lgTET = lgTXT + lgTV;
         pack<T> r[NV];
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int e0 = (tid + i * NT) * V;
-            const int bx = e0 >> lgTE;
-            const int w = e0 & (tile_elems - 1);
+            const int bx = e0 >> lgTET;
+            const int w = e0 & (tile_t - 1);
             r[i] = *reinterpret_cast<const pack<T>*>(
-                Tt + ((size_t)bx * NBV + b2) * tile_elems + w);
+                Tt + ((size_t)bx * NBV + b2) * tile_t + w);
         }
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int e0 = (tid + i * NT) * V;
-            const int bx = e0 >> lgTE;
-            const int w = e0 & (tile_elems - 1);
-            const int x = (bx << lgTX) + (w >> lgTV);
+            const int bx = e0 >> lgTET;
+            const int w = e0 & (tile_t - 1);
+            const int x = (bx << lgTXT) + (w >> lgTV);
             const int v_in = w & (TV - 1);
             const int px = lds_pad(makhoul_pos<L>(x));
 #pragma unroll

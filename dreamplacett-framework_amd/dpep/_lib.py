@@ -33,8 +33,8 @@ DPEP_FLAG_NO_GATHER = 0x8
 NUM_TIMINGS = 9
 TIMING_KEYS = ("h2d", "scatter", "gather", "d2h_den", "upload", "compute",
                "download", "fw", "total")
-KERNEL_KEYS = ("bin_count", "bin_scan", "bin_fill", "strip_acc", "strip_red",
-               "row_dct", "col_pass", "row_inv", "gather", "step")
+KERNEL_KEYS = ("bin_count", "bin_fill", "strip_acc", "col_pass", "row_inv",
+               "gather", "step")
 
 # Every symbol include/dpep.h declares, with (restype, argtypes).
 _vp = ctypes.c_void_p

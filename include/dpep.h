@@ -144,9 +144,10 @@ int dpep_get_timings(dpep_ctx* ctx, float* out);
 /* Per-kernel average durations in microseconds over the steps recorded
  * since profiling was enabled (at most `slots` of them), measured with HIP
  * events around each launch on the stream the kernels run on:
- * [0] strip count, [1] strip scan, [2] strip fill, [3] strip accumulate,
- * [4] strip reduce, [5] row DCT, [6] column DCT + inverse, [7] row inverse,
- * [8] gather, [9] whole step.  n = floats in out. */
+ * [0] strip count (with the strip table), [1] strip fill, [2] strip
+ * accumulate with the row DCT (and the reduction of split strips),
+ * [3] column DCT + inverse, [4] row inverse, [5] gather, [6] whole step.
+ * n = floats in out. */
 int dpep_get_kernel_times(dpep_ctx* ctx, float* out, int n);
 
 /* slots > 0 enables per-kernel event timing for a ring of `slots` steps

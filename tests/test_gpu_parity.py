@@ -201,7 +201,7 @@ def test_timings_and_kernel_times():
         t = ctx.timings()
     assert set(kt) == set(dpep.KERNEL_KEYS)
     assert all(v > 0 for v in kt.values())
-    assert kt["step"] >= kt["strip_acc"] + kt["row_dct"]
+    assert kt["step"] >= kt["strip_acc"] + kt["col_pass"]
     assert set(t) == set(dpep.TIMING_KEYS) and t["total"] > 0
 
 
