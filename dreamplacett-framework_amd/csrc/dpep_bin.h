@@ -625,9 +625,35 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
         const int kg1 = kg0 + RG - 1;
         __syncthreads();                    // previous group's readers done
         const size_t gb = (size_t)kg0 * N;
-        for (int e = tid; e < RG * N; e += kAccThreads) {
-            lfx[e] = fx[gb + e];
-            lfy[e] = fy[gb + e];
+        {
+            // 16-byte vectors, all of a thread's loads in flight at once
+            using V16 = typename std::conditional<sizeof(T) == 4, float4, double2>::type;
+            constexpr int V = 16 / (int)sizeof(T);
+            // RG rows of both maps fill at most kTileBytes
+            constexpr int PV = (int)(kTileBytes / (2 * 16) / kAccThreads);
+            const int nv = RG * N / V;
+            const V16* gx4 = reinterpret_cast<const V16*>(fx + gb);
+            const V16* gy4 = reinterpret_cast<const V16*>(fy + gb);
+            V16* lx4 = reinterpret_cast<V16*>(lfx);
+            V16* ly4 = reinterpret_cast<V16*>(lfy);
+            if (nv == PV * kAccThreads) {
+                V16 vx[PV], vy[PV];
+#pragma unroll
+                for (int j = 0; j < PV; ++j) {
+                    vx[j] = gx4[tid + j * kAccThreads];
+                    vy[j] = gy4[tid + j * kAccThreads];
+                }
+#pragma unroll
+                for (int j = 0; j < PV; ++j) {
+                    lx4[tid + j * kAccThreads] = vx[j];
+                    ly4[tid + j * kAccThreads] = vy[j];
+                }
+            } else {
+                for (int e = tid; e < nv; e += kAccThreads) {
+                    lx4[e] = gx4[e];
+                    ly4[e] = gy4[e];
+                }
+            }
         }
         __syncthreads();
         const bool first = kg0 == k0;
