@@ -393,6 +393,54 @@ int dpep_set_initial_density(dpep_ctx* c, const void* d0n)
     return DPEP_OK;
 }
 
+int dpep_set_fixed_cells(dpep_ctx* c, const void* px, const void* py,
+                         const void* sx, const void* sy, int n,
+                         double target_density)
+{
+    if (int rc = check_ctx(c)) return rc;
+    if (n < 0) return fail(DPEP_ERR_ARG, "n=%d must be >= 0", n);
+    if (n > 0 && (!px || !py || !sx || !sy))
+        return fail(DPEP_ERR_ARG, "fixed-cell array is NULL");
+    if (!isfinite(target_density) || target_density < 0.0)
+        return fail(DPEP_ERR_ARG, "target_density=%g must be finite and >= 0",
+                    target_density);
+    // one-time set-up: the fixed cells get their own device copy for the call
+    void* buf = nullptr;
+    const size_t bytes = (size_t)(n > 0 ? n : 1) * c->esz;
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    HIP_TRY(hipMalloc(&buf, 4 * bytes));
+    char* d = static_cast<char*>(buf);
+    int rc = DPEP_OK;
+    auto run = [&]() -> int {
+        if (n > 0) {
+            HIP_TRY(hipMemcpyAsync(d, px, (size_t)n * c->esz, hipMemcpyHostToDevice, c->stream));
+            HIP_TRY(hipMemcpyAsync(d + bytes, py, (size_t)n * c->esz, hipMemcpyHostToDevice,
+                                   c->stream));
+            HIP_TRY(hipMemcpyAsync(d + 2 * bytes, sx, (size_t)n * c->esz,
+                                   hipMemcpyHostToDevice, c->stream));
+            HIP_TRY(hipMemcpyAsync(d + 3 * bytes, sy, (size_t)n * c->esz,
+                                   hipMemcpyHostToDevice, c->stream));
+        }
+        if (c->dtype == DPEP_DTYPE_F32)
+            HIP_TRY(launch_fixed_density<float>((const float*)d, (const float*)(d + bytes),
+                                                (const float*)(d + 2 * bytes),
+                                                (const float*)(d + 3 * bytes), n, c->grid,
+                                                target_density, c->bins.B,
+                                                (float*)c->d_d0n, c->stream));
+        else
+            HIP_TRY(launch_fixed_density<double>((const double*)d, (const double*)(d + bytes),
+                                                 (const double*)(d + 2 * bytes),
+                                                 (const double*)(d + 3 * bytes), n, c->grid,
+                                                 target_density, c->bins.B,
+                                                 (double*)c->d_d0n, c->stream));
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        return DPEP_OK;
+    };
+    rc = run();
+    (void)hipFree(buf);
+    return rc;
+}
+
 int dpep_set_cells(dpep_ctx* c, const void* px, const void* py,
                    const void* sx, const void* sy, int nc)
 {

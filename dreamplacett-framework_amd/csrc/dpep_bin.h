@@ -694,6 +694,49 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
 }
 
 // ---------------------------------------------------------------------------
+// Fixed-cell density D0n = target_density * sum of exact overlaps / bin area
+// (no stretch: DREAMPlace's fixed density map, the initial_density_map the
+// reference's client uploads at integration/scatter_ttnn_client.py:786-795).
+// One workgroup per fixed cell walks its bin rectangle and adds uint64 fixed
+// point into the side map B (exact, order-free); a second kernel converts
+// and re-zeroes B.  A set-up computation, run once per placement.
+// ---------------------------------------------------------------------------
+constexpr int kFixedThreads = 256;
+
+template <typename T>
+__global__ __launch_bounds__(kFixedThreads) void k_fixed_overlap(
+    const T* __restrict__ px, const T* __restrict__ py, const T* __restrict__ sx,
+    const T* __restrict__ sy, int n, Grid g, double scale,
+    unsigned long long* __restrict__ B)
+{
+    const int i = blockIdx.x;
+    if (i >= n) return;
+    CellSpan c;
+    if (!cell_span((double)px[i], (double)py[i], (double)sx[i], (double)sy[i], g, c))
+        return;
+    const int nrow = c.bxh - c.bxl + 1, ncol = c.byh - c.byl + 1;
+    const long long total = (long long)nrow * ncol;
+    for (long long e = threadIdx.x; e < total; e += kFixedThreads) {
+        const int k = c.bxl + (int)(e / ncol), q = c.byl + (int)(e % ncol);
+        const double tx = overlap_1d(c.x, c.w, g.xl, g.bsx, k);
+        const double ty = overlap_1d(c.y, c.h, g.yl, g.bsy, q);
+        const double v = tx * ty * g.inv_ba;
+        if (v > 0.0) atomicAdd(&B[(size_t)k * g.N + q], to_fixed(v, scale));
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_fixed_flush(unsigned long long* __restrict__ B,
+                                                     T* __restrict__ d0n, size_t mn,
+                                                     double factor)
+{
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= mn) return;
+    d0n[i] = (T)((double)B[i] * factor);
+    B[i] = 0ull;
+}
+
+// ---------------------------------------------------------------------------
 // G2: forces in cell order: gx[i], gy[i] from the record pos[i]; tall cells
 // are gathered here in float64; cells that contribute nothing get zero.
 // ---------------------------------------------------------------------------

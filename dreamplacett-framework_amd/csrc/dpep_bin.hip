@@ -1,5 +1,7 @@
 // dpep_bin.hip -- host launchers of the strip-binned scatter and gather
 // (kernels in dpep_bin.h).
+#include <math.h>
+
 #include <type_traits>
 
 #include "dpep_bin.h"
@@ -79,6 +81,28 @@ hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
 }
 
 template <typename T>
+hipError_t launch_fixed_density(const T* px, const T* py, const T* sx, const T* sy,
+                                int n, const Grid& g, double target_density,
+                                void* B, T* d0n, hipStream_t s)
+{
+    // contributions <= 1 bin area each, at most n of them per bin
+    const double scale = ldexp(1.0, fix_exponent(n));
+    unsigned long long* Bm = reinterpret_cast<unsigned long long*>(B);
+    Grid gn = g;
+    gn.stretch = 0;                    // fixed cells keep their own sizes
+    if (n > 0) {
+        k_fixed_overlap<T><<<(unsigned)n, kFixedThreads, 0, s>>>(px, py, sx, sy, n, gn,
+                                                               scale, Bm);
+        hipError_t e = hipGetLastError();
+        if (e) return e;
+    }
+    const size_t mn = (size_t)g.M * g.N;
+    k_fixed_flush<T><<<(unsigned)((mn + 255) / 256), 256, 0, s>>>(Bm, d0n, mn,
+                                                                  target_density / scale);
+    return hipGetLastError();
+}
+
+template <typename T>
 static hipError_t prepare_bin_type()
 {
     hipError_t e = hipSuccess;
@@ -111,6 +135,13 @@ template hipError_t launch_bin_scatter<double>(const double*, const double*,
                                                const Grid&, BinArgs, const SpectralArgs&,
                                                const double*, double*, double*,
                                                hipStream_t, hipEvent_t*);
+template hipError_t launch_fixed_density<float>(const float*, const float*, const float*,
+                                                const float*, int, const Grid&, double,
+                                                void*, float*, hipStream_t);
+template hipError_t launch_fixed_density<double>(const double*, const double*,
+                                                 const double*, const double*, int,
+                                                 const Grid&, double, void*, double*,
+                                                 hipStream_t);
 template hipError_t launch_bin_gather<float>(const float*, const float*, const float*,
                                              const float*, int, const Grid&,
                                              const BinArgs&, const float*, const float*,

@@ -123,6 +123,13 @@ hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
                              const BinArgs& b, const T* fx, const T* fy,
                              T* gx, T* gy, hipStream_t s);
 
+// D0n = target_density * exact overlap of n fixed cells / bin area, through
+// the side map B (left at zero).
+template <typename T>
+hipError_t launch_fixed_density(const T* px, const T* py, const T* sx, const T* sy,
+                                int n, const Grid& g, double target_density,
+                                void* B, T* d0n, hipStream_t s);
+
 // Sets the dynamic-LDS limits of every spectral / binning kernel (once).
 hipError_t spectral_prepare();
 hipError_t bin_prepare();

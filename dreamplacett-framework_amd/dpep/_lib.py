@@ -49,6 +49,8 @@ _SIGNATURES = {
                                    ctypes.POINTER(_vp)]),
     "dpep_destroy": (ctypes.c_int, [_vp]),
     "dpep_set_initial_density": (ctypes.c_int, [_vp, _vp]),
+    "dpep_set_fixed_cells": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_int,
+                                            ctypes.c_double]),
     "dpep_set_cells": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_int]),
     "dpep_compute": (ctypes.c_int, [_vp]),
     "dpep_sync": (ctypes.c_int, [_vp]),
@@ -183,6 +185,16 @@ class Context:
                              f"expected {self.M * self.N}")
         _check(self._lib.dpep_set_initial_density(self.handle, _ptr(d)),
                "dpep_set_initial_density", self._lib)
+
+    def set_fixed_cells(self, px, py, sx, sy, target_density: float = 1.0) -> None:
+        """Initial density from fixed cells (macros), computed on the GPU:
+        target_density * exact overlap / bin area (no stretch)."""
+        n = int(np.asarray(px).size)
+        arrs = [self._arr(a, n, nm) for a, nm in ((px, "px"), (py, "py"),
+                                                    (sx, "sx"), (sy, "sy"))]
+        _check(self._lib.dpep_set_fixed_cells(self.handle, *[_ptr(a) for a in arrs], n,
+                                              float(target_density)),
+               "dpep_set_fixed_cells", self._lib)
 
     def set_cells(self, px, py, sx, sy) -> None:
         n = int(np.asarray(px).size)

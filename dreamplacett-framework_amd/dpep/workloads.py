@@ -137,7 +137,7 @@ def _design_210k(seed: int, n_mov: int, M: int, N: int, die: float):
     sy = np.concatenate([sy, np.full(n_fill, ROW_HEIGHT)])
     meta = {"movable": n_mov, "fillers": n_fill, "macros": 540,
             "macro_union_area": union, "macro_sum_area": float((mw * mh).sum()),
-            "die": die}
+            "die": die, "fixed_cells": (mx, my, mw, mh)}
     return s, sx, sy, d0n, meta
 
 
@@ -193,6 +193,7 @@ def config3(seed: int = 0, n_mov: int = 1_100_000, M: int = 2048,
     py[c_idx] = np.clip(centres[which, 1] + gy - 0.5 * h, 0.0, die - h)
     ba = (die / M) * (die / N)
     meta = {"movable": n_mov, "macros": n_macros, "die": die,
+            "fixed_cells": (mx, my, mw, mh),
             "cluster_centres": centres.tolist(), "cluster_fraction": 0.2,
             "macro_union_area_fraction": float(np.minimum(d0n, 1.0).sum() * ba / die ** 2)}
     return _finish("C3", M, N, die, px, py, sx, sy, d0n, meta)
@@ -208,7 +209,8 @@ def config4(seed: int = 0, n_mov: int = 2_000_000, M: int = 4096,
     mx, my, mw, mh = _macros(s[1], n_macros, 300.0, 4000.0, die)
     d0n = fixed_density(mx, my, mw, mh, M, N, 0.0, 0.0, die, die)
     px, py = _uniform_pos(s[2], n_mov, sx, sy, die)
-    meta = {"movable": n_mov, "macros": n_macros, "die": die}
+    meta = {"movable": n_mov, "macros": n_macros, "die": die,
+            "fixed_cells": (mx, my, mw, mh)}
     return _finish("C4", M, N, die, px, py, sx, sy, d0n, meta)
 
 

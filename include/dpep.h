@@ -99,6 +99,17 @@ int dpep_destroy(dpep_ctx* ctx);
  * initial density is zero. */
 int dpep_set_initial_density(dpep_ctx* ctx, const void* d0n);
 
+/* Computes the initial density from n fixed cells (host memory: lower-left
+ * corners and sizes, no stretch): D0n = target_density * sum of exact
+ * cell/bin overlaps / bin_area, replacing any previous initial density.
+ * This is the initial_density_map / bin_area that the reference's client
+ * receives from DREAMPlace and uploads once
+ * (integration/scatter_ttnn_client.py:786-795), computed on the GPU.
+ * A set-up call: it allocates a temporary device copy of the cells. */
+int dpep_set_fixed_cells(dpep_ctx* ctx, const void* px, const void* py,
+                         const void* sx, const void* sy, int n,
+                         double target_density);
+
 /* Uploads nc <= nc_max cells (host memory) into the context's device
  * buffers.  Replaces the server's H2D (:1335-1349). */
 int dpep_set_cells(dpep_ctx* ctx, const void* px, const void* py,

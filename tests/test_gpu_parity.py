@@ -282,3 +282,60 @@ def test_c5_hundred_steps(oracle, dtype):
                 ref = oracle.step(*cells, w.M, w.N, w.xl, w.yl, w.xh, w.yh,
                                   d0n=w.d0n.astype(dtype))
                 check(out, ref, dtype, f"C5 step {step}")
+
+
+# --------------------------------------------------------------------------
+# fixed-cell initial density D0 on the GPU
+# --------------------------------------------------------------------------
+def _fixed_oracle(oracle, w, fx, fy, fw, fh, target):
+    """D0n = target * exact overlap / bin area: the oracle's density of the
+    fixed cells with no stretch and ratio 1."""
+    return target * oracle.density(np.asarray(fx, np.float64), np.asarray(fy, np.float64),
+                                   np.asarray(fw, np.float64), np.asarray(fh, np.float64),
+                                   w.M, w.N, w.xl, w.yl, w.xh, w.yh, stretch=False)
+
+
+@pytest.mark.parametrize("cfg,grid,dtype", [(1, 512, np.float32), (3, 2048, np.float32),
+                                            (1, 256, np.float64)])
+def test_fixed_cells_density(oracle, cfg, grid, dtype):
+    import dpep
+    from dpep import workloads
+    w = workloads.small(cfg, seed=9, cells=1000, grid=grid)
+    mx, my, mw, mh = (np.asarray(a, dtype) for a in w.meta["fixed_cells"])
+    # plus edge cases: outside the die, straddling its border, zero size,
+    # exactly on bin edges, a copy of an existing macro (overlap)
+    bs = w.bsx
+    ex = np.array([-500.0, w.xh - 10 * bs, 3 * bs, 5 * bs, mx[0]], dtype)
+    ey = np.array([-500.0, 4 * bs, 7 * bs, 9 * bs, my[0]], dtype)
+    ew = np.array([100.0, 40 * bs, 0.0, 2 * bs, mw[0]], dtype)
+    eh = np.array([100.0, 3 * bs, 5.0, 3 * bs, mh[0]], dtype)
+    fx, fy = np.concatenate([mx, ex]), np.concatenate([my, ey])
+    fw, fh = np.concatenate([mw, ew]), np.concatenate([mh, eh])
+    target = 0.9
+    with dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh, dtype=dtype) as ctx:
+        ctx.set_fixed_cells(fx, fy, fw, fh, target)
+        out = ctx.step(*w.cells(dtype))
+        ctx.set_fixed_cells(fx, fy, fw, fh, target)      # B left clean: same again
+        out2 = ctx.step(*w.cells(dtype))
+    d0 = _fixed_oracle(oracle, w, fx, fy, fw, fh, target)
+    px, py, sx, sy = w.cells(dtype)
+    ref = oracle.step(px, py, sx, sy, w.M, w.N, w.xl, w.yl, w.xh, w.yh,
+                      d0n=d0.astype(dtype))
+    check(out, ref, dtype, f"fixed C{cfg}")
+    assert np.array_equal(out["density"], out2["density"])
+    # no movable cells: the density is D0 itself
+    with dpep.Context(w.M, w.N, 1, w.xl, w.yl, w.xh, w.yh, dtype=dtype) as ctx:
+        ctx.set_fixed_cells(fx, fy, fw, fh, target)
+        only = ctx.step(*(np.zeros(0, dtype),) * 4)
+    assert rel_linf(only["density"], d0) <= TOL[dtype][0]
+
+
+def test_fixed_cells_empty_and_errors():
+    import dpep
+    with dpep.Context(16, 16, 10, 0.0, 0.0, 160.0, 160.0) as ctx:
+        ctx.set_initial_density(np.ones((16, 16), np.float32))
+        ctx.set_fixed_cells(*(np.zeros(0, np.float32),) * 4)   # no fixed cells
+        out = ctx.step(*(np.zeros(0, np.float32),) * 4)
+        assert not out["density"].any()
+        with pytest.raises(ValueError):
+            ctx.set_fixed_cells(*(np.zeros(1, np.float32),) * 4, target_density=-1.0)
