@@ -60,3 +60,34 @@ def test_client_against_oracle(tmp_path, oracle, inprocess):
         assert t["gather_mode"] == "hip" and t["n_iters"] == 4
     finally:
         c.stop()
+
+
+def test_server_dumps_replay_to_the_same_density(tmp_path, monkeypatch):
+    """EXPORT_POS_PATH / EXPORT_DENSITY_PATH from the server, replayed through
+    dpep.replay: the same cells (bitwise) and the same density (the step is
+    deterministic)."""
+    from dpep import replay
+    if not os.path.exists(SERVER_BIN):
+        pytest.fail(f"server binary missing: {SERVER_BIN}")
+    pos = tmp_path / "pos.bin"
+    dens = tmp_path / "dens.bin"
+    monkeypatch.setenv("EXPORT_POS_PATH", str(pos))
+    monkeypatch.setenv("EXPORT_DENSITY_PATH", str(dens))
+    w = workloads.small(3, seed=23, cells=20000, grid=256)
+    c = ScatterTTNNClient(ipc_dir=str(tmp_path / "ipc"), num_bins_x=w.M,
+                          num_bins_y=w.N, nc_max=w.nc, xl=w.xl, yl=w.yl,
+                          xh=w.xh, yh=w.yh, server_binary=SERVER_BIN, as_torch=False,
+                          ready_timeout=120, step_timeout=60)
+    c.set_initial_density(w.d0n)
+    c.start()
+    try:
+        px, py, sx, sy = w.cells(np.float32)
+        out = c.call_full(px, py, sx, sy)
+    finally:
+        c.stop()
+    d = replay.read_positions(str(pos) + ".iter1.bin")
+    assert d.nc == w.nc and np.array_equal(d.px, px) and np.array_equal(d.sy, sy)
+    assert np.array_equal(replay.read_density(str(dens), w.M, w.N), out["density"])
+    r = replay.replay(d, w.d0n.astype(np.float32))
+    assert np.array_equal(r["density"], out["density"])
+    assert np.array_equal(r["field_x"], out["field_x"])
