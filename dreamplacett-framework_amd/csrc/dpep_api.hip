@@ -299,7 +299,7 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
     g.minw = M_SQRT2 * g.bsx;
     g.minh = M_SQRT2 * g.bsy;
     g.stretch = (flags & DPEP_FLAG_NO_STRETCH) ? 0 : 1;
-    g.fix_scale = ldexp(1.0, fix_exponent(nc_max));
+    g.fix_scale = ldexp(1.0, fix_exponent_of(nc_max, (int)c->esz));
 
     SpectralArgs& a = c->sargs;
     a.M = M; a.N = N;

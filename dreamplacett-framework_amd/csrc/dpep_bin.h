@@ -22,8 +22,8 @@
 //                 partials, tall cells gathered directly
 //
 // Accumulation is fixed point everywhere: round(v * 2^f) added as uint64
-// (LDS, the side map B, partial slots), with f = fix_exponent(nc_max) so a
-// bin's sum cannot overflow (each contribution is <= 1).  Integer sums are
+// (LDS, the side map B, partial slots), with f = fix_exponent_of(nc_max,
+// dtype) so a bin's sum cannot overflow (each contribution is <= 1).  Integer sums are
 // exact and independent of order, so the density -- and everything computed
 // from it -- is bitwise reproducible run to run.  (On gfx950 ds_add_u64 also
 // runs about seven times faster than ds_add_f32.)
@@ -94,7 +94,7 @@ __device__ __forceinline__ void stretch_of(const vec4_t<T>& r, int stretch, T& x
         const T m = (T)1.41421356237309504880;
         wc = r.z > m ? r.z : m;
         hc = r.w > m ? r.w : m;
-        ratio = (r.z * r.w) / (wc * hc);
+        ratio = (r.z * r.w) * fast_rcp(wc * hc);
     }
     xr = r.x + wc;
     yr = r.y + hc;
@@ -126,11 +126,11 @@ __device__ __forceinline__ unsigned long long to_fixed(double v, double scale)
     return (unsigned long long)__double2ull_rn(v * scale);
 }
 
-// The scale is a power of two, so v * scale is exact in float as in double
-// and both round to the same integer: float32 contributions need no float64.
+// float32 contributions: the scale is 2^31 (fix_exponent_of), v <= 1, so
+// v * scale is exact and below 2^32: a 32-bit round-to-nearest conversion.
 __device__ __forceinline__ unsigned long long to_fixed(float v, float scale)
 {
-    return (unsigned long long)__float2ull_rn(v * scale);
+    return (unsigned long long)__float2uint_rn(v * scale);
 }
 
 // ---------------------------------------------------------------------------
@@ -443,13 +443,21 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
             stretch_of<T>(rg[j], g.stretch, xr, yr, rat);
             const T dx = rg[j].x, dy = rg[j].y;
             const int ka = max(sb.bxl, k0), kb = min(sb.bxl + sb.nx, k1);
+            // y overlaps of the (usual) first 4 columns, shared by the rows
+            T tyv[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                tyv[q] = q <= sb.ny ? min(yr, (T)(q + 1)) - max(dy, (T)q) : (T)0;
             for (int k = ka; k <= kb; ++k) {
                 const T jx = (T)(k - sb.bxl);
                 const T tx = min(xr, jx + (T)1) - max(dx, jx);
                 if (!(tx > (T)0)) continue;
                 const T rtx = rat * tx;
                 A* trow = tile + (k - k0) * N + sb.byl;
-                for (int q = 0; q <= sb.ny; ++q) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (tyv[q] > (T)0) atomicAdd(&trow[q], to_fixed(rtx * tyv[q], fs));
+                for (int q = 4; q <= sb.ny; ++q) {
                     const T ty = min(yr, (T)(q + 1)) - max(dy, (T)q);
                     if (!(ty > (T)0)) continue;
                     atomicAdd(&trow[q], to_fixed(rtx * ty, fs));

@@ -18,7 +18,7 @@ struct Grid {
     double inv_ba;            // 1 / (bsx * bsy)
     double inv_bsx, inv_bsy;  // 1 / bsx, 1 / bsy
     double minw, minh;        // sqrt2 * bsx, sqrt2 * bsy (stretch floor)
-    double fix_scale;         // 2^fix_exponent(nc_max): fixed-point scale
+    double fix_scale;         // 2^fix_exponent_of(nc_max, dtype): fixed-point scale
     int stretch;              // 1: DREAMPlace small-cell stretch
 };
 
@@ -33,6 +33,16 @@ __host__ __device__ inline int fix_exponent(int nc_max)
     while (lg < 31 && (1ll << lg) < (long long)(nc_max > 1 ? nc_max : 1)) ++lg;
     int f = 62 - lg;
     return f > 52 ? 52 : (f < 20 ? 20 : f);
+}
+
+// The scale of a context: float32 contributions use 2^31 (never above
+// fix_exponent for nc_max < 2^31), so round(v * 2^31) of a contribution
+// v <= 1 fits 32 bits and converts in two instructions; the quantum 2^-31
+// is far below float32's own rounding of v.  float64 keeps fix_exponent.
+__host__ __device__ inline int fix_exponent_of(int nc_max, int elem_bytes)
+{
+    const int f = fix_exponent(nc_max);
+    return elem_bytes == 4 && f > 31 ? 31 : f;
 }
 
 template <typename T> struct vec2;

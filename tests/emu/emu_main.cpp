@@ -92,7 +92,7 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     g.bsx = (xh - xl) / M; g.bsy = (yh - yl) / N; g.inv_ba = 1.0 / (g.bsx * g.bsy);
     g.inv_bsx = 1.0 / g.bsx; g.inv_bsy = 1.0 / g.bsy;
     g.minw = M_SQRT2 * g.bsx; g.minh = M_SQRT2 * g.bsy; g.stretch = 1;
-    g.fix_scale = ldexp(1.0, fix_exponent(nc));
+    g.fix_scale = ldexp(1.0, fix_exponent_of(nc, (int)sizeof(T)));
     (void)det;
     std::mt19937_64 rng(1234);
     std::uniform_real_distribution<double> U(0, 1);

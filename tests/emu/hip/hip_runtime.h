@@ -53,6 +53,10 @@ inline unsigned long long __double2ull_rn(double x)
     return (unsigned long long)std::nearbyint(x);
 }
 #define __builtin_amdgcn_rcpf(x) (1.0f / (x))
+inline unsigned __float2uint_rn(float x)
+{
+    return (unsigned)std::nearbyint(x);
+}
 inline unsigned long long __float2ull_rn(float x)
 {
     return (unsigned long long)std::nearbyint(x);
