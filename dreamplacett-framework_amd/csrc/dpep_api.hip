@@ -145,8 +145,8 @@ static void release(dpep_ctx* c)
     void* bufs[] = {c->d_px, c->d_py, c->d_sx, c->d_sy, c->d_d0n,
                     c->d_density, c->d_potential, c->d_fx, c->d_fy, c->d_gx,
                     c->d_gy, c->d_T, c->d_Ux, c->d_Uy, c->d_twM,
-                    c->d_postM, c->d_twN, c->d_postN, b.cnt, b.xtot, b.xoff, b.strip_off,
-                    b.nch, b.item_start, b.items, b.nitems, b.ticket, b.done, b.recg,
+                    c->d_postM, c->d_twN, c->d_postN, b.cnt, b.xtot, b.strip_off,
+                    b.nch, b.item_start, b.items, b.nitems, b.done, b.recg,
                     b.recm, b.pos, b.pos2, b.gtmp,
                     b.bigflag, b.B, b.partial};
     for (void* p : bufs)
@@ -176,10 +176,10 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
     const BinArgs& b = c->bins;
     if (!a.twM || !a.postM || !a.twN || !a.postN || !d0n || !dens || !fx ||
         !fy || !c->d_T || !c->d_Ux || !c->d_Uy || (a.potential && !phi) ||
-        !b.xtot || !b.xoff ||
+        !b.xtot ||
         (nc > 0 && (!px || !py || !sx || !sy)) ||
         (gather && (!gx || !gy)) || !b.cnt || !b.strip_off || !b.nch ||
-        !b.item_start || !b.items || !b.nitems || !b.ticket || !b.done || !b.recg ||
+        !b.item_start || !b.items || !b.nitems || !b.done || !b.recg ||
         !b.recm || !b.pos || !b.pos2 ||
         !b.gtmp || !b.bigflag || !b.B || !b.partial)
         return fail(DPEP_ERR_STATE, "internal: a kernel argument is NULL");
@@ -338,16 +338,13 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
         b.S = p.S; b.R = p.R; b.lgR = p.lgR; b.G1 = 1; b.CH = p.CH; b.Wmax = p.Wmax;
         HIP_TRY(hipMalloc((void**)&b.cnt, (size_t)p.G1max * p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.xtot, (size_t)kCountSlots * p.S * sizeof(unsigned)));
-        HIP_TRY(hipMalloc((void**)&b.xoff, (size_t)kCountSlots * p.S * sizeof(unsigned)));
         HIP_TRY(hipMemset(b.xtot, 0, (size_t)kCountSlots * p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.strip_off, (size_t)(p.S + 1) * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.nch, (size_t)p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.item_start, (size_t)p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.items, (size_t)p.Wmax * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.nitems, sizeof(unsigned)));
-        HIP_TRY(hipMalloc((void**)&b.ticket, sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.done, (size_t)p.S * sizeof(unsigned)));
-        HIP_TRY(hipMemset(b.ticket, 0, sizeof(unsigned)));
         HIP_TRY(hipMemset(b.done, 0, (size_t)p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc(&b.recg, p.cap * p.geo_bytes));
         HIP_TRY(hipMalloc((void**)&b.recm, p.cap * sizeof(unsigned)));

@@ -8,10 +8,11 @@
 //
 //   k_bin_count   per-workgroup strip histograms; each nonzero count  K1
 //                 is added to one of kCountSlots totals per strip and
-//                 the returned old total is the workgroup's base; the
-//                 last workgroup to finish builds the strip table
-//                 (strip and slot offsets, chunk list)
-//   k_bin_fill    cells -> strip-sorted records; tall cells -> B      K3
+//                 the returned old total is the workgroup's base
+//   k_bin_fill    each workgroup scans the strip totals for its own   K3
+//                 offsets (workgroup 0 publishes the strip table and
+//                 chunk list); cells -> strip-sorted records; tall
+//                 cells -> B
 //   k_strip_acc   one work item = (strip, chunk): LDS accumulate,     K4
 //                 flush rho = D0 + tile (+B); a strip split into
 //                 several chunks is summed by its last chunk to finish
@@ -134,9 +135,8 @@ __device__ __forceinline__ unsigned long long to_fixed(float v, float scale)
 }
 
 // ---------------------------------------------------------------------------
-// Strip table, built by the last K1 workgroup: strip_off = exclusive scan of
-// the strip totals, xoff = first entry of each (slot, strip), the chunk list.
-// LDS: tot[S] | tmp[kBinThreads].  Leaves the slot totals at zero.
+// Strip table: strip_off = exclusive scan of the strip totals, the first
+// entry of each (workgroup, strip), the chunk list.  Built in K3's prologue.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ unsigned block_exclusive_scan(unsigned v,
                                                          unsigned* tmp,
@@ -158,73 +158,72 @@ __device__ __forceinline__ unsigned block_exclusive_scan(unsigned v,
     return incl - v;
 }
 
-// The slot totals are only ever touched by device-scope atomics (K1's adds,
-// the reads and the reset here), which are performed coherently across the
-// XCDs' separate L2 caches: no fence is needed, and none is taken (a
-// device-scope fence writes back the whole L2 of the XCD).
-__device__ __forceinline__ unsigned coherent_load(unsigned* p) { return atomicAdd(p, 0u); }
-
-__device__ __forceinline__ void build_strip_table(const BinArgs& b, unsigned* tot,
-                                                  unsigned* tmp)
+// Offsets of this K3 workgroup's strip entries, from K1's slot totals: every
+// workgroup scans the strip totals itself (S values, a few microseconds of
+// L2 reads spread over the grid) instead of one workgroup building a table
+// behind all of K1.  cur[s] = first entry of workgroup g in strip s =
+// strip offset + totals of the slots before g's + g's base within its slot.
+// Workgroup 0 also publishes the strip table for K4 / G1 (strip offsets,
+// chunk counts, the work-item list).  LDS: cur[S] | tot[S] | tmp[kBinThreads].
+__device__ __forceinline__ void strip_offsets(const BinArgs& b, unsigned* cur,
+                                              unsigned* tot, unsigned* tmp)
 {
     const int tid = threadIdx.x;
     const int S = b.S;
-    // strip totals = sum of the slot totals
+    const int x = (int)(blockIdx.x % kCountSlots);
+    const unsigned* row = b.cnt + (size_t)blockIdx.x * S;
     for (int s = tid; s < S; s += kBinThreads) {
-        unsigned t = 0u;
+        unsigned t = 0u, pre = 0u;
 #pragma unroll
-        for (int x = 0; x < kCountSlots; ++x) t += coherent_load(&b.xtot[(size_t)x * S + s]);
+        for (int xx = 0; xx < kCountSlots; ++xx) {
+            const unsigned v = b.xtot[(size_t)xx * S + s];
+            pre += xx < x ? v : 0u;
+            t += v;
+        }
         tot[s] = t;
+        cur[s] = pre + row[s];
     }
     __syncthreads();
-    // exclusive scan of the totals (each thread a run of strips)
+    // exclusive scan of the strip totals (each thread a run of strips)
     const int per = (S + kBinThreads - 1) / kBinThreads;
     const int r0 = min(tid * per, S), r1 = min(r0 + per, S);
     unsigned run = 0u;
     for (int s = r0; s < r1; ++s) run += tot[s];
     unsigned total;
     unsigned base = block_exclusive_scan(run, tmp, total);
+    const bool pub = blockIdx.x == 0;         // uniform across the group
+    unsigned nrun = 0u;
     for (int s = r0; s < r1; ++s) {
         const unsigned t = tot[s];
-        b.strip_off[s] = base;
-        tot[s] = base;          // tot now holds the strip offsets
-        base += t;
-        const unsigned n = (t + (unsigned)b.CH - 1u) / (unsigned)b.CH;
-        b.nch[s] = n > 1u ? n : 1u;
-    }
-    if (tid == 0) b.strip_off[S] = total;
-    __syncthreads();
-    // slot offsets; the slot totals are consumed here and left at zero
-    for (int s = tid; s < S; s += kBinThreads) {
-        unsigned off = tot[s];
-#pragma unroll
-        for (int x = 0; x < kCountSlots; ++x) {
-            const unsigned v = atomicExch(&b.xtot[(size_t)x * S + s], 0u);
-            b.xoff[(size_t)x * S + s] = off;
-            off += v;
+        cur[s] += base;
+        if (pub) {
+            b.strip_off[s] = base;
+            const unsigned n = (t + (unsigned)b.CH - 1u) / (unsigned)b.CH;
+            nrun += n > 1u ? n : 1u;
         }
+        base += t;
     }
+    if (!pub) return;
+    if (tid == 0) b.strip_off[S] = total;
     // work items (strip, chunk)
-    unsigned nrun = 0u;
-    for (int s = r0; s < r1; ++s) nrun += b.nch[s];
     unsigned ntotal;
     unsigned ibase = block_exclusive_scan(nrun, tmp, ntotal);
     for (int s = r0; s < r1; ++s) {
-        const unsigned n = b.nch[s];
+        const unsigned t = tot[s];
+        unsigned n = (t + (unsigned)b.CH - 1u) / (unsigned)b.CH;
+        n = n > 1u ? n : 1u;
+        b.nch[s] = n;
         b.item_start[s] = ibase;
         for (unsigned c = 0; c < n; ++c)
             if (ibase + c < (unsigned)b.Wmax) b.items[ibase + c] = (unsigned)s | (c << 16);
         ibase += n;
     }
-    if (tid == 0) {
-        *b.nitems = ntotal < (unsigned)b.Wmax ? ntotal : (unsigned)b.Wmax;
-        atomicExch(b.ticket, 0u);      // every K1 workgroup has taken its ticket
-    }
+    if (tid == 0) *b.nitems = ntotal < (unsigned)b.Wmax ? ntotal : (unsigned)b.Wmax;
 }
 
 // ---------------------------------------------------------------------------
-// K1: per-workgroup strip histogram; the last workgroup builds the table.
-// LDS: hist[S] | tmp[kBinThreads] | flag.
+// K1: per-workgroup strip histogram, added into the slot totals.
+// LDS: hist[S].
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(kBinThreads) void k_bin_count(
@@ -234,7 +233,6 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_count(
 {
     extern __shared__ __align__(16) unsigned char smem[];
     unsigned* hist = reinterpret_cast<unsigned*>(smem);
-    unsigned* flag = hist + b.S + kBinThreads;
     const int tid = threadIdx.x;
     for (int s = tid; s < b.S; s += kBinThreads) hist[s] = 0u;
     __syncthreads();
@@ -264,21 +262,14 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_count(
     }
     __syncthreads();
     // workgroup g adds into slot g % kCountSlots: a label only, it spreads the
-    // atomics over kCountSlots addresses per strip
+    // atomics over kCountSlots addresses per strip; the returned old total is
+    // g's base within its slot
     unsigned* row = b.cnt + (size_t)blockIdx.x * b.S;
     unsigned* slot = b.xtot + (size_t)(blockIdx.x % kCountSlots) * b.S;
     for (int s = tid; s < b.S; s += kBinThreads) {
         const unsigned h = hist[s];
         row[s] = h ? atomicAdd(&slot[s], h) : 0u;
     }
-    // Every slot add of this workgroup has returned (its result was stored
-    // above) before the barrier, hence before the ticket: the last workgroup
-    // to take one sees all totals.
-    __syncthreads();
-    if (tid == 0) *flag = atomicAdd(b.ticket, 1u) == gridDim.x - 1 ? 1u : 0u;
-    __syncthreads();
-    if (*flag == 0u) return;                 // uniform across the group
-    build_strip_table(b, hist, hist + b.S);
 }
 
 // ---------------------------------------------------------------------------
@@ -293,9 +284,7 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill(
     extern __shared__ __align__(16) unsigned char smem[];
     unsigned* cur = reinterpret_cast<unsigned*>(smem);
     const int tid = threadIdx.x;
-    const unsigned* row = b.cnt + (size_t)blockIdx.x * b.S;
-    const unsigned* xo = b.xoff + (size_t)(blockIdx.x % kCountSlots) * b.S;
-    for (int s = tid; s < b.S; s += kBinThreads) cur[s] = xo[s] + row[s];
+    strip_offsets(b, cur, cur + b.S, cur + 2 * b.S);
     __syncthreads();
     vec4_t<T>* recg = reinterpret_cast<vec4_t<T>*>(b.recg);
     unsigned long long* Bm = reinterpret_cast<unsigned long long*>(b.B);
@@ -407,6 +396,8 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     extern __shared__ __align__(16) unsigned char smem[];
     A* tile = reinterpret_cast<A*>(smem);
     const int w = blockIdx.x;
+    if (w == 0)   // K3 has read the slot totals: zero them for the next step
+        for (int e = threadIdx.x; e < kCountSlots * b.S; e += kAccThreads) b.xtot[e] = 0u;
     if (w >= (int)*b.nitems) return;            // uniform across the group
     const unsigned item = b.items[w];
     const int s = (int)(item & 0xFFFFu);

@@ -44,13 +44,13 @@ hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
 {
     b.G1 = (int)g1_of(nc);
     if (b.R != strip_rows(g.N)) return hipErrorInvalidValue;   // the kernel's R
-    const size_t count_lds = (size_t)(b.S + kBinThreads + 1) * sizeof(unsigned);
-    const size_t hist = (size_t)b.S * sizeof(unsigned);
+    const size_t count_lds = (size_t)b.S * sizeof(unsigned);
+    const size_t fill_lds = (size_t)(2 * b.S + kBinThreads) * sizeof(unsigned);
     hipError_t e;
     k_bin_count<T><<<b.G1, kBinThreads, count_lds, s>>>(px, py, sx, sy, nc, g, b);
     if ((e = hipGetLastError())) return e;
     if (ev && (e = hipEventRecord(ev[0], s))) return e;
-    k_bin_fill<T><<<b.G1, kBinThreads, hist, s>>>(px, py, sx, sy, nc, g, b);
+    k_bin_fill<T><<<b.G1, kBinThreads, fill_lds, s>>>(px, py, sx, sy, nc, g, b);
     if ((e = hipGetLastError())) return e;
     if (ev && (e = hipEventRecord(ev[1], s))) return e;
     e = dispatch_n<T>(g.N, [&](auto lc) -> hipError_t {

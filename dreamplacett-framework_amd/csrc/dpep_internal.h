@@ -59,13 +59,11 @@ struct BinArgs {
     int Wmax;               // capacity of the work-item list
     unsigned* cnt;          // [G1max][S] base of workgroup g in its slot
     unsigned* xtot;         // [kCountSlots][S] slot totals (zero between steps)
-    unsigned* xoff;         // [kCountSlots][S] first entry of each slot
     unsigned* strip_off;    // [S + 1] entry offset of each strip
     unsigned* nch;          // [S] chunks per strip
     unsigned* item_start;   // [S] first work item of each strip
     unsigned* items;        // [Wmax] strip | chunk << 16
     unsigned* nitems;       // [1]
-    unsigned* ticket;       // [1] K1 workgroups done (zero between steps)
     unsigned* done;         // [S] K4 chunks done per strip (zero between steps)
     void* recg;             // [2 nc_max] record geometry, vec4 of T
     unsigned* recm;         // [2 nc_max] record span word

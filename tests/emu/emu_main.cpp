@@ -136,7 +136,6 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     if (b.G1 < 1) b.G1 = 1;
     b.cnt = exact<unsigned>((size_t)b.G1 * p.S);
     b.xtot = exact<unsigned>((size_t)kCountSlots * p.S);
-    b.xoff = exact<unsigned>((size_t)kCountSlots * p.S);
     memset(b.xtot, 0, (size_t)kCountSlots * p.S * sizeof(unsigned));
     b.strip_off = exact<unsigned>(p.S + 1);
     b.nch = exact<unsigned>(p.S);
@@ -146,9 +145,7 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     if (sizeof(vec4_t<T>) != p.geo_bytes) { fprintf(stderr, "record size mismatch\n"); return 4; }
     b.recg = malloc(p.cap * p.geo_bytes);
     b.recm = exact<unsigned>(p.cap);
-    b.ticket = exact<unsigned>(1);
     b.done = exact<unsigned>(p.S);
-    *b.ticket = 0u;
     memset(b.done, 0, p.S * sizeof(unsigned));
     b.pos = exact<unsigned>(nc > 0 ? nc : 1);
     b.pos2 = exact<unsigned>(nc > 0 ? nc : 1);
@@ -160,12 +157,11 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     memset(b.bigflag, 0, p.S * sizeof(unsigned));
     const size_t hist = (size_t)p.S * sizeof(unsigned);
     for (int rep = 0; rep < 2; ++rep) {   // two steps: B / flags must be clean again
-        launch(b.G1, kBinThreads, (size_t)(p.S + kBinThreads + 1) * sizeof(unsigned),
-               [&] { k_bin_count<T>(px, py, sx, sy, nc, g, b); });
-        launch(b.G1, kBinThreads, hist, [&] { k_bin_fill<T>(px, py, sx, sy, nc, g, b); });
+        launch(b.G1, kBinThreads, hist, [&] { k_bin_count<T>(px, py, sx, sy, nc, g, b); });
+        launch(b.G1, kBinThreads, (size_t)(2 * p.S + kBinThreads) * sizeof(unsigned),
+               [&] { k_bin_fill<T>(px, py, sx, sy, nc, g, b); });
         launch(p.Wmax, kAccThreads, acc_lds_bytes<T, LN>(),
                [&] { k_strip_acc<T, LN>(g, b, a, d0n, dens, Tt); });
-        if (*b.ticket) { fprintf(stderr, "K1 ticket left set\n"); return 4; }
         for (int s2 = 0; s2 < p.S; ++s2)
             if (b.done[s2]) { fprintf(stderr, "strip chunk counter left set\n"); return 4; }
         for (int s2 = 0; s2 < p.S; ++s2)
