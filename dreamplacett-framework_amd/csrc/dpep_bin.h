@@ -656,38 +656,65 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
         }
         __syncthreads();
         const bool first = kg0 == k0;
-        for (unsigned e = e0 + tid; e < e1; e += kAccThreads) {
-            const vec4_t<T> rg = recg[e];
-            const SpanBox sb = span_of(b.recm[e], k0);
-            T xr, yr, rat;
-            stretch_of<T>(rg, g.stretch, xr, yr, rat);
-            const T dx = rg.x, dy = rg.y;
-            const int ka = max(sb.bxl, kg0), kb = min(sb.bxl + sb.nx, kg1);
-            T ax = (T)0, ay = (T)0;
-            for (int k = ka; k <= kb; ++k) {
-                const T jx = (T)(k - sb.bxl);
-                const T tx = min(xr, jx + (T)1) - max(dx, jx);
-                if (!(tx > (T)0)) continue;
-                const T* rx = lfx + (size_t)(k - kg0) * N + sb.byl;
-                const T* ry = lfy + (size_t)(k - kg0) * N + sb.byl;
-                T sx_ = (T)0, sy_ = (T)0;
-                for (int q = 0; q <= sb.ny; ++q) {
-                    const T ty = min(yr, (T)(q + 1)) - max(dy, (T)q);
-                    if (!(ty > (T)0)) continue;
-                    sx_ += ty * rx[q];
-                    sy_ += ty * ry[q];
+        constexpr int kBatch = 4;       // record loads in flight per thread
+        for (unsigned eb = e0 + tid; eb < e1; eb += kBatch * kAccThreads) {
+            vec4_t<T> rgb[kBatch];
+            unsigned rmb[kBatch];
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                const unsigned e = eb + j * kAccThreads;
+                if (e < e1) {
+                    rgb[j] = recg[e];
+                    rmb[j] = b.recm[e];
                 }
-                ax += tx * sx_;
-                ay += tx * sy_;
             }
-            const T sc = rat * ba;
-            vec2_t<T> v = {sc * ax, sc * ay};
-            if (!first) {
-                const vec2_t<T> o = out[e];
-                v.x += o.x;
-                v.y += o.y;
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                const unsigned e = eb + j * kAccThreads;
+                if (e >= e1) continue;
+                const vec4_t<T>& rg = rgb[j];
+                const SpanBox sb = span_of(rmb[j], k0);
+                T xr, yr, rat;
+                stretch_of<T>(rg, g.stretch, xr, yr, rat);
+                const T dx = rg.x, dy = rg.y;
+                const int ka = max(sb.bxl, kg0), kb = min(sb.bxl + sb.nx, kg1);
+                // y overlaps of the (usual) first 4 columns, shared by the rows
+                T tyv[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    tyv[q] = q <= sb.ny ? min(yr, (T)(q + 1)) - max(dy, (T)q) : (T)0;
+                T ax = (T)0, ay = (T)0;
+                for (int k = ka; k <= kb; ++k) {
+                    const T jx = (T)(k - sb.bxl);
+                    const T tx = min(xr, jx + (T)1) - max(dx, jx);
+                    if (!(tx > (T)0)) continue;
+                    const T* rx = lfx + (size_t)(k - kg0) * N + sb.byl;
+                    const T* ry = lfy + (size_t)(k - kg0) * N + sb.byl;
+                    T sx_ = (T)0, sy_ = (T)0;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if (tyv[q] > (T)0) {
+                            sx_ += tyv[q] * rx[q];
+                            sy_ += tyv[q] * ry[q];
+                        }
+                    for (int q = 4; q <= sb.ny; ++q) {
+                        const T ty = min(yr, (T)(q + 1)) - max(dy, (T)q);
+                        if (!(ty > (T)0)) continue;
+                        sx_ += ty * rx[q];
+                        sy_ += ty * ry[q];
+                    }
+                    ax += tx * sx_;
+                    ay += tx * sy_;
+                }
+                const T sc = rat * ba;
+                vec2_t<T> v = {sc * ax, sc * ay};
+                if (!first) {
+                    const vec2_t<T> o = out[e];
+                    v.x += o.x;
+                    v.y += o.y;
+                }
+                out[e] = v;
             }
-            out[e] = v;
         }
     }
 }
