@@ -763,31 +763,59 @@ __global__ __launch_bounds__(256) void k_fixed_flush(unsigned long long* __restr
 }
 
 // ---------------------------------------------------------------------------
-// G2: forces in cell order: gx[i], gy[i] from the record pos[i]; tall cells
-// are gathered here in float64; cells that contribute nothing get zero.
+// G2: forces in cell order: gx[i], gy[i] from the record pos[i]; cells that
+// contribute nothing get zero.  Tall cells are gathered in float64 by the
+// whole workgroup, one cell at a time: the threads split the cell's bins and
+// a fixed-shape tree in LDS sums their parts (deterministic), so a wide cell
+// costs one round of loads instead of a serial walk over its bins.
+// LDS: ntall | list[kCellsPerGroup] | red[2][kBinThreads] (doubles).
 // ---------------------------------------------------------------------------
+constexpr size_t kGatherOutLds =
+    ((1 + kCellsPerGroup) * sizeof(unsigned) + 15) / 16 * 16 + 2 * kBinThreads * sizeof(double);
+
 template <typename T>
-__device__ __forceinline__ void gather_one(const CellSpan& c, const Grid& g,
-                                           const T* __restrict__ fx,
-                                           const T* __restrict__ fy,
-                                           double& ax, double& ay)
+__device__ __forceinline__ void gather_tall(int i, const T* __restrict__ px,
+                                            const T* __restrict__ py,
+                                            const T* __restrict__ sx,
+                                            const T* __restrict__ sy, const Grid& g,
+                                            const T* __restrict__ fx,
+                                            const T* __restrict__ fy, double* red,
+                                            T* __restrict__ gx, T* __restrict__ gy)
 {
-    ax = 0.0;
-    ay = 0.0;
-    for (int k = c.bxl; k <= c.bxh; ++k) {
-        const double tx = overlap_1d(c.x, c.w, g.xl, g.bsx, k);
-        if (tx <= 0.0) continue;
-        const size_t row = (size_t)k * g.N;
-        for (int q = c.byl; q <= c.byh; ++q) {
+    const int tid = threadIdx.x;
+    CellSpan c;
+    double ax = 0.0, ay = 0.0;
+    const bool ok = load_span(px, py, sx, sy, i, g, c);     // uniform: same cell
+    if (ok) {
+        const int ny1 = c.byh - c.byl + 1;
+        const long long nb = (long long)(c.bxh - c.bxl + 1) * ny1;
+        for (long long e = tid; e < nb; e += kBinThreads) {
+            const int k = c.bxl + (int)(e / ny1), q = c.byl + (int)(e % ny1);
+            const double tx = overlap_1d(c.x, c.w, g.xl, g.bsx, k);
             const double ty = overlap_1d(c.y, c.h, g.yl, g.bsy, q);
-            if (ty <= 0.0) continue;
             const double a = tx * ty;
-            ax += a * (double)fx[row + q];
-            ay += a * (double)fy[row + q];
+            if (a > 0.0) {
+                const size_t gi = (size_t)k * g.N + q;
+                ax += a * (double)fx[gi];
+                ay += a * (double)fy[gi];
+            }
         }
     }
-    ax *= c.ratio;
-    ay *= c.ratio;
+    red[tid] = ax;
+    red[kBinThreads + tid] = ay;
+    __syncthreads();
+    for (int h = kBinThreads / 2; h > 0; h >>= 1) {
+        if (tid < h) {
+            red[tid] += red[tid + h];
+            red[kBinThreads + tid] += red[kBinThreads + tid + h];
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        gx[i] = ok ? (T)(red[0] * c.ratio) : (T)0;
+        gy[i] = ok ? (T)(red[kBinThreads] * c.ratio) : (T)0;
+    }
+    __syncthreads();                      // red is reused by the next cell
 }
 
 // One workgroup per K3 block of kCellsPerGroup cells (same cell-to-thread
@@ -800,6 +828,13 @@ __global__ __launch_bounds__(kBinThreads) void k_gather_out(
     BinArgs b, const T* __restrict__ fx, const T* __restrict__ fy,
     T* __restrict__ gx, T* __restrict__ gy)
 {
+    extern __shared__ __align__(16) unsigned char smem[];
+    unsigned* ntall = reinterpret_cast<unsigned*>(smem);
+    unsigned* list = ntall + 1;
+    double* red = reinterpret_cast<double*>(
+        smem + ((1 + kCellsPerGroup) * sizeof(unsigned) + 15) / 16 * 16);
+    if (threadIdx.x == 0) *ntall = 0u;
+    __syncthreads();
     const int c0 = blockIdx.x * kCellsPerGroup + threadIdx.x;
     const vec2_t<T>* res = reinterpret_cast<const vec2_t<T>*>(b.gtmp);
     unsigned p[kCellsPerThread], p2[kCellsPerThread];
@@ -819,17 +854,17 @@ __global__ __launch_bounds__(kBinThreads) void k_gather_out(
     for (int j = 0; j < kCellsPerThread; ++j) {
         const int i = c0 + j * kBinThreads;
         if (i >= nc) break;
-        T ox = v[j].x + v2[j].x, oy = v[j].y + v2[j].y;
         if (p[j] == kPosTall) {
-            CellSpan c;
-            double ax = 0.0, ay = 0.0;
-            if (load_span(px, py, sx, sy, i, g, c)) gather_one(c, g, fx, fy, ax, ay);
-            ox = (T)ax;
-            oy = (T)ay;
+            list[atomicAdd(ntall, 1u)] = (unsigned)i;
+            continue;
         }
-        gx[i] = ox;
-        gy[i] = oy;
+        gx[i] = v[j].x + v2[j].x;
+        gy[i] = v[j].y + v2[j].y;
     }
+    __syncthreads();
+    const unsigned n = *ntall;                // uniform across the group
+    for (unsigned t = 0; t < n; ++t)
+        gather_tall<T>((int)list[t], px, py, sx, sy, g, fx, fy, red, gx, gy);
 }
 
 }  // namespace dpep

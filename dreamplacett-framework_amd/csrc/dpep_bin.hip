@@ -75,7 +75,7 @@ hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
     k_gather_bin<T><<<b.Wmax, kAccThreads, lds, s>>>(g, b, fx, fy);
     hipError_t e = hipGetLastError();
     if (e) return e;
-    k_gather_out<T><<<g1_of(nc), kBinThreads, 0, s>>>(px, py, sx, sy, nc, g, b, fx, fy, gx,
+    k_gather_out<T><<<g1_of(nc), kBinThreads, kGatherOutLds, s>>>(px, py, sx, sy, nc, g, b, fx, fy, gx,
                                                       gy);
     return hipGetLastError();
 }

@@ -183,7 +183,7 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     if (nc > 0) {
         const size_t glds = (size_t)gather_rows<T>(p.R, N) * N * 2 * sizeof(T);
         launch(p.Wmax, kAccThreads, glds, [&] { k_gather_bin<T>(g, b, fx, fy); });
-        launch(b.G1, kBinThreads, 0, [&] { k_gather_out<T>(px, py, sx, sy, nc, g, b, fx, fy, gx, gy); });
+        launch(b.G1, kBinThreads, kGatherOutLds, [&] { k_gather_out<T>(px, py, sx, sy, nc, g, b, fx, fy, gx, gy); });
     }
     {
         const unsigned char* Bb = (const unsigned char*)b.B;
