@@ -324,7 +324,11 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill(
                     atomicAdd(&Bm[rowi + q], to_fixed(stx * ty, g.fix_scale));
                 }
             }
-            for (int s = s0; s <= s1; ++s) b.bigflag[s] = 1u;
+            // the strips' column range in B: highest + 1, N - lowest
+            for (int s = s0; s <= s1; ++s) {
+                atomicMax(&b.bigflag[s], (unsigned)(c.byh + 1));
+                atomicMax(&b.bigflag[b.S + s], (unsigned)(g.N - c.byl));
+            }
             b.pos[i] = kPosTall;
             b.pos2[i] = kPosNone;
             continue;
@@ -485,7 +489,9 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
 
     // ---- flush: rho = D0 + tile (+B), kept in registers ------------------
     constexpr int PER = (RN + kAccThreads - 1) / kAccThreads;
-    const bool bf = b.bigflag[s] != 0u;
+    // columns [blo, bhi) of the strip's rows hold tall cells' sums in B
+    const int bhi = (int)b.bigflag[s], blo = N - (int)b.bigflag[b.S + s];
+    const bool bf = bhi != 0;
     T rv[PER];
     {
         A v[PER];
@@ -502,7 +508,8 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
 #pragma unroll
             for (int j = 0; j < PER; ++j) {
                 const int e = tid + j * kAccThreads;
-                if (e < RN) {
+                const int col = e & (N - 1);
+                if (e < RN && col >= blo && col < bhi) {
                     v[j] += Bm[gbase + e];
                     Bm[gbase + e] = 0ull;
                 }
@@ -518,7 +525,10 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
         }
     }
     __syncthreads();   // the tile is dead (the FFT buffers alias it); bigflag read
-    if (bf && tid == 0) b.bigflag[s] = 0u;
+    if (bf && tid == 0) {
+        b.bigflag[s] = 0u;
+        b.bigflag[b.S + s] = 0u;
+    }
 
     // ---- row DCT-II of the strip's R rows: rows (2p, 2p+1) -> FFT slot p --
     constexpr int LP = lds_len(L), E = fft_e(L), TPF = L / E;

@@ -70,7 +70,8 @@ struct BinArgs {
     unsigned* pos;          // [nc_max] record of cell i, or kPosTall / kPosNone
     unsigned* pos2;         // [nc_max] second-strip record of cell i, or kPosNone
     void* gtmp;             // [2 nc_max] vec2 forces in record order
-    unsigned* bigflag;      // [S] strip has rows in B
+    unsigned* bigflag;      // [2S] per strip: 1 + highest, N - lowest column
+                            // of its rows in B (0: none; zero between steps)
     void* B;                // [M*N] uint64, zero between steps
     void* partial;          // [Wmax][R*N] uint64
 };

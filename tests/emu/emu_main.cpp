@@ -150,11 +150,11 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     b.pos = exact<unsigned>(nc > 0 ? nc : 1);
     b.pos2 = exact<unsigned>(nc > 0 ? nc : 1);
     b.gtmp = exact<vec2_t<T>>(p.cap);
-    b.bigflag = exact<unsigned>(p.S);
+    b.bigflag = exact<unsigned>(2 * p.S);
     b.B = malloc(mn * 8);
     b.partial = malloc(p.partial_elems * 8);
     memset(b.B, 0, mn * 8);
-    memset(b.bigflag, 0, p.S * sizeof(unsigned));
+    memset(b.bigflag, 0, 2 * p.S * sizeof(unsigned));
     const size_t hist = (size_t)p.S * sizeof(unsigned);
     for (int rep = 0; rep < 2; ++rep) {   // two steps: B / flags must be clean again
         launch(b.G1, kBinThreads, hist, [&] { k_bin_count<T>(px, py, sx, sy, nc, g, b); });
@@ -164,7 +164,7 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
                [&] { k_strip_acc<T, LN>(g, b, a, d0n, dens, Tt); });
         for (int s2 = 0; s2 < p.S; ++s2)
             if (b.done[s2]) { fprintf(stderr, "strip chunk counter left set\n"); return 4; }
-        for (int s2 = 0; s2 < p.S; ++s2)
+        for (int s2 = 0; s2 < 2 * p.S; ++s2)
             if (b.bigflag[s2]) { fprintf(stderr, "bigflag left set\n"); return 4; }
         for (int s2 = 0; s2 < kCountSlots * p.S; ++s2)
             if (b.xtot[s2]) { fprintf(stderr, "slot totals left set\n"); return 4; }

@@ -80,6 +80,14 @@ inline unsigned atomicAdd(unsigned* p, unsigned v)
 {
     return __atomic_fetch_add(p, v, __ATOMIC_RELAXED);
 }
+inline unsigned atomicMax(unsigned* p, unsigned v)
+{
+    std::atomic_ref<unsigned> r(*p);
+    unsigned o = r.load();
+    while (o < v && !r.compare_exchange_weak(o, v)) {
+    }
+    return o;
+}
 inline float atomicAdd(float* p, float v) { return unsafeAtomicAdd(p, v); }
 inline double atomicAdd(double* p, double v) { return unsafeAtomicAdd(p, v); }
 
