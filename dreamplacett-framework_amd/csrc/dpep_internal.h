@@ -45,7 +45,7 @@ hipError_t launch_row_inv(const SpectralArgs& a, const T* Ux, const T* Uy,
 // Strip binning (kernels in dpep_bin.h)
 // ---------------------------------------------------------------------------
 constexpr int kBinThreads = 256;       // K1 / K3 workgroup size
-constexpr int kCellsPerThread = 8;     // K1 / K3 cells per thread
+constexpr int kCellsPerThread = 4;     // K1 / K3 cells per thread
 constexpr int kCellsPerGroup = kBinThreads * kCellsPerThread;
 constexpr int kAccThreads = 1024;      // K4 workgroup size
 constexpr int kCountSlots = 8;         // strip-total counters per strip
