@@ -623,8 +623,8 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
     const int R = b.R, N = g.N;
     const int RG = gather_rows<T>(R, N);
     const int k0 = s * R;
-    T* lfx = reinterpret_cast<T*>(smem);
-    T* lfy = lfx + (size_t)RG * N;
+    // both fields of a bin side by side: one 2-element LDS read per bin
+    vec2_t<T>* lf = reinterpret_cast<vec2_t<T>*>(smem);
     const unsigned e0 = b.strip_off[s] + (unsigned)chunk * (unsigned)b.CH;
     const unsigned e1 = min(e0 + (unsigned)b.CH, b.strip_off[s + 1]);
     const vec4_t<T>* recg = reinterpret_cast<const vec4_t<T>*>(b.recg);
@@ -643,8 +643,17 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
             const int nv = RG * N / V;
             const V16* gx4 = reinterpret_cast<const V16*>(fx + gb);
             const V16* gy4 = reinterpret_cast<const V16*>(fy + gb);
-            V16* lx4 = reinterpret_cast<V16*>(lfx);
-            V16* ly4 = reinterpret_cast<V16*>(lfy);
+            V16* l4 = reinterpret_cast<V16*>(lf);
+            // V bins of fx and of fy -> V interleaved (fx, fy) pairs
+            auto put = [&](int e, const V16& x, const V16& y) {
+                if constexpr (sizeof(T) == 4) {
+                    l4[2 * e] = V16{x.x, y.x, x.y, y.y};
+                    l4[2 * e + 1] = V16{x.z, y.z, x.w, y.w};
+                } else {
+                    l4[2 * e] = V16{x.x, y.x};
+                    l4[2 * e + 1] = V16{x.y, y.y};
+                }
+            };
             if (nv == PV * kAccThreads) {
                 V16 vx[PV], vy[PV];
 #pragma unroll
@@ -653,15 +662,9 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
                     vy[j] = gy4[tid + j * kAccThreads];
                 }
 #pragma unroll
-                for (int j = 0; j < PV; ++j) {
-                    lx4[tid + j * kAccThreads] = vx[j];
-                    ly4[tid + j * kAccThreads] = vy[j];
-                }
+                for (int j = 0; j < PV; ++j) put(tid + j * kAccThreads, vx[j], vy[j]);
             } else {
-                for (int e = tid; e < nv; e += kAccThreads) {
-                    lx4[e] = gx4[e];
-                    ly4[e] = gy4[e];
-                }
+                for (int e = tid; e < nv; e += kAccThreads) put(e, gx4[e], gy4[e]);
             }
         }
         __syncthreads();
@@ -698,20 +701,21 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
                     const T jx = (T)(k - sb.bxl);
                     const T tx = min(xr, jx + (T)1) - max(dx, jx);
                     if (!(tx > (T)0)) continue;
-                    const T* rx = lfx + (size_t)(k - kg0) * N + sb.byl;
-                    const T* ry = lfy + (size_t)(k - kg0) * N + sb.byl;
+                    const vec2_t<T>* rf = lf + (size_t)(k - kg0) * N + sb.byl;
                     T sx_ = (T)0, sy_ = (T)0;
 #pragma unroll
                     for (int q = 0; q < 4; ++q)
                         if (tyv[q] > (T)0) {
-                            sx_ += tyv[q] * rx[q];
-                            sy_ += tyv[q] * ry[q];
+                            const vec2_t<T> f = rf[q];
+                            sx_ += tyv[q] * f.x;
+                            sy_ += tyv[q] * f.y;
                         }
                     for (int q = 4; q <= sb.ny; ++q) {
                         const T ty = min(yr, (T)(q + 1)) - max(dy, (T)q);
                         if (!(ty > (T)0)) continue;
-                        sx_ += ty * rx[q];
-                        sy_ += ty * ry[q];
+                        const vec2_t<T> f = rf[q];
+                        sx_ += ty * f.x;
+                        sy_ += ty * f.y;
                     }
                     ax += tx * sx_;
                     ay += tx * sy_;
