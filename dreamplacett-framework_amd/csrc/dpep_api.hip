@@ -148,7 +148,7 @@ static void release(dpep_ctx* c)
                     c->d_postM, c->d_twN, c->d_postN, b.cnt, b.xtot, b.strip_off,
                     b.nch, b.item_start, b.items, b.nitems, b.done, b.recg,
                     b.recm, b.pos, b.pos2, b.gtmp,
-                    b.bigflag, b.B, b.partial};
+                    b.bigflag, b.B, b.chunk, b.items_g};
     for (void* p : bufs)
         if (p) (void)hipFree(p);
     for (auto& e : c->ev)
@@ -181,7 +181,7 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
         (gather && (!gx || !gy)) || !b.cnt || !b.strip_off || !b.nch ||
         !b.item_start || !b.items || !b.nitems || !b.done || !b.recg ||
         !b.recm || !b.pos || !b.pos2 ||
-        !b.gtmp || !b.bigflag || !b.B || !b.partial)
+        !b.gtmp || !b.bigflag || !b.B || !b.chunk || !b.items_g)
         return fail(DPEP_ERR_STATE, "internal: a kernel argument is NULL");
     if (nc > c->nc_max)
         return fail(DPEP_ERR_ARG, "nc=%d exceeds nc_max=%d", nc, c->nc_max);
@@ -335,15 +335,25 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
         BinPlan& p = c->plan;
         p = make_bin_plan(M, N, nc_max, c->esz);
         BinArgs& b = c->bins;
-        b.S = p.S; b.R = p.R; b.lgR = p.lgR; b.G1 = 1; b.CH = p.CH; b.Wmax = p.Wmax;
+        b.S = p.S; b.R = p.R; b.lgR = p.lgR; b.G1 = 1; b.ch_force = 0;
+        {
+            int acc = 0, gat = 0, cus = 0;
+            HIP_TRY(dtype == DPEP_DTYPE_F32 ? bin_occupancy<float>(N, p.R, acc, gat)
+                                            : bin_occupancy<double>(N, p.R, acc, gat));
+            HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount,
+                                          c->device));
+            set_item_grids(b, acc, gat, cus);
+        }
         HIP_TRY(hipMalloc((void**)&b.cnt, (size_t)p.G1max * p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.xtot, (size_t)kCountSlots * p.S * sizeof(unsigned)));
         HIP_TRY(hipMemset(b.xtot, 0, (size_t)kCountSlots * p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.strip_off, (size_t)(p.S + 1) * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.nch, (size_t)p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.item_start, (size_t)p.S * sizeof(unsigned)));
-        HIP_TRY(hipMalloc((void**)&b.items, (size_t)p.Wmax * sizeof(unsigned)));
-        HIP_TRY(hipMalloc((void**)&b.nitems, sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.items, (size_t)b.Wacc * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.items_g, (size_t)b.Wgat * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.nitems, 2 * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.chunk, 2 * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.done, (size_t)p.S * sizeof(unsigned)));
         HIP_TRY(hipMemset(b.done, 0, (size_t)p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc(&b.recg, p.cap * p.geo_bytes));
@@ -353,7 +363,6 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
         HIP_TRY(hipMalloc(&b.gtmp, p.cap * 2 * c->esz));
         HIP_TRY(hipMalloc((void**)&b.bigflag, (size_t)2 * p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc(&b.B, (size_t)M * N * accb));
-        HIP_TRY(hipMalloc(&b.partial, p.partial_elems * accb));
         // B and the strip flags must start at zero; each step leaves them so.
         HIP_TRY(hipMemset(b.B, 0, (size_t)M * N * accb));
         HIP_TRY(hipMemset(b.bigflag, 0, (size_t)2 * p.S * sizeof(unsigned)));

@@ -14,8 +14,8 @@
 //                 chunk list); cells -> strip-sorted records; tall
 //                 cells -> B
 //   k_strip_acc   one work item = (strip, chunk): LDS accumulate,     K4
-//                 flush rho = D0 + tile (+B); a strip split into
-//                 several chunks is summed by its last chunk to finish
+//                 flush rho = D0 + tile (+B); the chunks of a split
+//                 strip add into B and the last one to finish flushes
 //   k_gather_bin  one work item = (strip, chunk): the strip's field   G1
 //                 rows staged in LDS, each record's partial force over
 //                 the rows of this strip, in record order
@@ -23,7 +23,7 @@
 //                 partials, tall cells gathered directly
 //
 // Accumulation is fixed point everywhere: round(v * 2^f) added as uint64
-// (LDS, the side map B, partial slots), with f = fix_exponent_of(nc_max,
+// (LDS, the side map B), with f = fix_exponent_of(nc_max,
 // dtype) so a bin's sum cannot overflow (each contribution is <= 1).  Integer sums are
 // exact and independent of order, so the density -- and everything computed
 // from it -- is bitwise reproducible run to run.  (On gfx950 ds_add_u64 also
@@ -164,7 +164,8 @@ __device__ __forceinline__ unsigned block_exclusive_scan(unsigned v,
 // behind all of K1.  cur[s] = first entry of workgroup g in strip s =
 // strip offset + totals of the slots before g's + g's base within its slot.
 // Workgroup 0 also publishes the strip table for K4 / G1 (strip offsets,
-// chunk counts, the work-item list).  LDS: cur[S] | tot[S] | tmp[kBinThreads].
+// chunk sizes and counts, the two work-item lists).  LDS: cur[S] | tot[S] |
+// tmp[kBinThreads] | cand[kChunkCands].
 __device__ __forceinline__ void strip_offsets(const BinArgs& b, unsigned* cur,
                                               unsigned* tot, unsigned* tmp)
 {
@@ -192,33 +193,80 @@ __device__ __forceinline__ void strip_offsets(const BinArgs& b, unsigned* cur,
     unsigned total;
     unsigned base = block_exclusive_scan(run, tmp, total);
     const bool pub = blockIdx.x == 0;         // uniform across the group
-    unsigned nrun = 0u;
     for (int s = r0; s < r1; ++s) {
         const unsigned t = tot[s];
         cur[s] += base;
-        if (pub) {
-            b.strip_off[s] = base;
-            const unsigned n = (t + (unsigned)b.CH - 1u) / (unsigned)b.CH;
-            nrun += n > 1u ? n : 1u;
-        }
+        if (pub) b.strip_off[s] = base;
         base += t;
     }
     if (!pub) return;
     if (tid == 0) b.strip_off[S] = total;
-    // work items (strip, chunk)
-    unsigned ntotal;
-    unsigned ibase = block_exclusive_scan(nrun, tmp, ntotal);
-    for (int s = r0; s < r1; ++s) {
-        const unsigned t = tot[s];
-        unsigned n = (t + (unsigned)b.CH - 1u) / (unsigned)b.CH;
-        n = n > 1u ? n : 1u;
-        b.nch[s] = n;
-        b.item_start[s] = ibase;
-        for (unsigned c = 0; c < n; ++c)
-            if (ibase + c < (unsigned)b.Wmax) b.items[ibase + c] = (unsigned)s | (c << 16);
-        ibase += n;
+    // Chunk sizes of this step: the smallest kChunkMin << k whose item count
+    // sum_s max(1, ceil(t_s / chunk)) fits the workgroups the device holds at
+    // once (Pacc for K4, Pgat for G1), so a skewed placement spreads its heavy
+    // strips over otherwise idle CUs; every strip in one item when even the
+    // largest does not fit.
+    unsigned* cand = tmp + kBinThreads;
+    for (int k = tid; k < kChunkCands; k += kBinThreads) cand[k] = 0u;
+    __syncthreads();
+    int lg_min = 0;
+    while ((1 << lg_min) < kChunkMin) ++lg_min;
+    // each lane starts at its own candidate: the lanes of a wave add into
+    // different LDS words (same-word atomics from a whole wave serialise)
+    for (int j = 0; j < kChunkCands; ++j) {
+        const int k = (j + tid) % kChunkCands;
+        const unsigned sh = (unsigned)(lg_min + k), ch = 1u << sh;
+        unsigned c = 0u;
+        for (int s = r0; s < r1; ++s) {
+            const unsigned n = (tot[s] + (ch - 1u)) >> sh;
+            c += n > 1u ? n : 1u;
+        }
+        if (c) atomicAdd(&cand[k], c);
     }
-    if (tid == 0) *b.nitems = ntotal < (unsigned)b.Wmax ? ntotal : (unsigned)b.Wmax;
+    __syncthreads();
+    auto pick = [&](int P) -> unsigned {
+        if (b.ch_force > 0) return (unsigned)b.ch_force;
+        for (int k = 0; k < kChunkCands; ++k)
+            if (cand[k] <= (unsigned)P) return (unsigned)kChunkMin << k;
+        return (unsigned)kChunkMin << (kChunkCands - 1);
+    };
+    // K4 splits no strip into chunks below kAccChunkMin records: a split
+    // chunk pays device-scope atomics for its whole tile and the strip's
+    // flush waits for the last chunk, which only the accumulation of large
+    // strips repays (uniform 512^2 grids measured slower split).  G1's
+    // chunks are independent and split down to the candidate size.
+    unsigned cha = pick(b.Pacc);
+    if (b.ch_force <= 0 && cha < (unsigned)kAccChunkMin) cha = (unsigned)kAccChunkMin;
+    const unsigned chg = pick(b.Pgat);
+    if (tid == 0) {
+        b.chunk[0] = cha;
+        b.chunk[1] = chg;
+    }
+    // work items (strip, chunk) of K4, then of G1
+    for (int list = 0; list < 2; ++list) {
+        const unsigned ch = list == 0 ? cha : chg;
+        unsigned* items = list == 0 ? b.items : b.items_g;
+        const unsigned W = (unsigned)(list == 0 ? b.Wacc : b.Wgat);
+        unsigned nrun = 0u;
+        for (int s = r0; s < r1; ++s) {
+            const unsigned n = (tot[s] + ch - 1u) / ch;
+            nrun += n > 1u ? n : 1u;
+        }
+        unsigned ntotal;
+        unsigned ibase = block_exclusive_scan(nrun, tmp, ntotal);
+        for (int s = r0; s < r1; ++s) {
+            unsigned n = (tot[s] + ch - 1u) / ch;
+            n = n > 1u ? n : 1u;
+            if (list == 0) {
+                b.nch[s] = n;
+                b.item_start[s] = ibase;
+            }
+            for (unsigned c = 0; c < n; ++c)
+                if (ibase + c < W) items[ibase + c] = (unsigned)s | (c << 16);
+            ibase += n;
+        }
+        if (tid == 0) b.nitems[list] = ntotal < W ? ntotal : W;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -368,8 +416,8 @@ __device__ __forceinline__ void flush_value(unsigned long long v, size_t gi,
 // (rho = D0 + tile (+B)) and runs the strip's row DCT-II (the first spectral
 // pass) on the rows it already holds, writing T in the tile layout: the
 // density is never read back.  A strip split into n > 1 chunks: each chunk
-// writes its tile to its partial slot; the last chunk to finish adds the
-// other n - 1 slots to its own tile and completes the strip.
+// adds its tile into the strip's rows of the side map B; the last chunk to
+// finish reads them back and completes the strip.
 // ---------------------------------------------------------------------------
 __host__ __device__ constexpr int strip_rows(int N)
 {
@@ -402,20 +450,21 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     const int w = blockIdx.x;
     if (w == 0)   // K3 has read the slot totals: zero them for the next step
         for (int e = threadIdx.x; e < kCountSlots * b.S; e += kAccThreads) b.xtot[e] = 0u;
-    if (w >= (int)*b.nitems) return;            // uniform across the group
+    if (w >= (int)b.nitems[0]) return;          // uniform across the group
     const unsigned item = b.items[w];
     const int s = (int)(item & 0xFFFFu);
     const int chunk = (int)(item >> 16);
     const int tid = threadIdx.x;
     const int k0 = s * R, k1 = k0 + R - 1;
     const unsigned n = b.nch[s];
+    const unsigned CH = b.chunk[0];
     unsigned* last_flag = reinterpret_cast<unsigned*>(tile + RN);   // LDS word
     for (int e = tid; e < RN; e += kAccThreads) tile[e] = 0ull;
     __syncthreads();
 
-    const unsigned e0 = b.strip_off[s] + (unsigned)chunk * (unsigned)b.CH;
+    const unsigned e0 = b.strip_off[s] + (unsigned)chunk * CH;
     const unsigned eend = b.strip_off[s + 1];
-    const unsigned e1 = min(e0 + (unsigned)b.CH, eend);
+    const unsigned e1 = min(e0 + CH, eend);
     const vec4_t<T>* recg = reinterpret_cast<const vec4_t<T>*>(b.recg);
     const T fs = (T)g.fix_scale;
     constexpr int kBatch = 4;       // record loads in flight per thread
@@ -465,32 +514,33 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     const size_t gbase = (size_t)k0 * N;
     const double inv = 1.0 / g.fix_scale;
     A* Bm = reinterpret_cast<A*>(b.B);
-    A* part = reinterpret_cast<A*>(b.partial);
     if (n > 1u) {
-        // publish this chunk's tile; the last chunk of the strip continues
-        A* slot = part + (size_t)w * RN;
-        for (int e = tid; e < RN; e += kAccThreads) slot[e] = tile[e];
-        __threadfence();
+        // A strip split into n chunks: every chunk but the last to finish
+        // adds its tile into the strip's rows of B (device-scope atomics
+        // whose results are awaited, so they are performed before the
+        // ticket is taken; no fence); the last one folds B in its flush.
+        unsigned long long got = 0ull;
+        for (int e = tid; e < RN; e += kAccThreads) {
+            const A v = tile[e];
+            if (v) got |= atomicAdd(&Bm[gbase + e], v);
+        }
+        // never true (sums stay below 2^63); it makes the results live
+        if (got >> 63) *last_flag = 0u;
         __syncthreads();
         if (tid == 0) *last_flag = atomicAdd(&b.done[s], 1u) == n - 1u ? 1u : 0u;
         __syncthreads();
         if (*last_flag == 0u) return;           // uniform across the group
-        __threadfence();
-        const unsigned w0 = b.item_start[s];
-        for (int e = tid; e < RN; e += kAccThreads) {
-            A v = tile[e];
-            for (unsigned c = 0; c < n; ++c)
-                if (w0 + c != (unsigned)w) v += part[(size_t)(w0 + c) * RN + e];
-            tile[e] = v;
-        }
         if (tid == 0) b.done[s] = 0u;
-        __syncthreads();
     }
 
     // ---- flush: rho = D0 + tile (+B), kept in registers ------------------
     constexpr int PER = (RN + kAccThreads - 1) / kAccThreads;
-    // columns [blo, bhi) of the strip's rows hold tall cells' sums in B
-    const int bhi = (int)b.bigflag[s], blo = N - (int)b.bigflag[b.S + s];
+    // columns [blo, bhi) of the strip's rows hold sums in B: the tall cells'
+    // range, or all of them for a split strip (read at device scope: the
+    // other chunks added them in this launch)
+    const bool split = n > 1u;
+    const int bhi = split ? N : (int)b.bigflag[s];
+    const int blo = split ? 0 : N - (int)b.bigflag[b.S + s];
     const bool bf = bhi != 0;
     T rv[PER];
     {
@@ -500,7 +550,7 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
         for (int j = 0; j < PER; ++j) {
             const int e = tid + j * kAccThreads;
             if (e < RN) {
-                v[j] = tile[e];
+                v[j] = split ? 0ull : tile[e];  // a split strip's tiles are all in B
                 d[j] = d0n[gbase + e];
             }
         }
@@ -510,7 +560,9 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
                 const int e = tid + j * kAccThreads;
                 const int col = e & (N - 1);
                 if (e < RN && col >= blo && col < bhi) {
-                    v[j] += Bm[gbase + e];
+                    v[j] += split ? __hip_atomic_load(&Bm[gbase + e], __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT)
+                                  : Bm[gbase + e];
                     Bm[gbase + e] = 0ull;
                 }
             }
@@ -525,7 +577,7 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
         }
     }
     __syncthreads();   // the tile is dead (the FFT buffers alias it); bigflag read
-    if (bf && tid == 0) {
+    if (tid == 0 && (split || b.bigflag[s] != 0u)) {
         b.bigflag[s] = 0u;
         b.bigflag[b.S + s] = 0u;
     }
@@ -615,18 +667,19 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
 {
     extern __shared__ __align__(16) unsigned char smem[];
     const int w = blockIdx.x;
-    if (w >= (int)*b.nitems) return;            // uniform across the group
-    const unsigned item = b.items[w];
+    if (w >= (int)b.nitems[1]) return;          // uniform across the group
+    const unsigned item = b.items_g[w];
     const int s = (int)(item & 0xFFFFu);
     const int chunk = (int)(item >> 16);
     const int tid = threadIdx.x;
     const int R = b.R, N = g.N;
+    const unsigned CH = b.chunk[1];
     const int RG = gather_rows<T>(R, N);
     const int k0 = s * R;
     // both fields of a bin side by side: one 2-element LDS read per bin
     vec2_t<T>* lf = reinterpret_cast<vec2_t<T>*>(smem);
-    const unsigned e0 = b.strip_off[s] + (unsigned)chunk * (unsigned)b.CH;
-    const unsigned e1 = min(e0 + (unsigned)b.CH, b.strip_off[s + 1]);
+    const unsigned e0 = b.strip_off[s] + (unsigned)chunk * CH;
+    const unsigned e1 = min(e0 + CH, b.strip_off[s + 1]);
     const vec4_t<T>* recg = reinterpret_cast<const vec4_t<T>*>(b.recg);
     vec2_t<T>* out = reinterpret_cast<vec2_t<T>*>(b.gtmp);
     const T ba = (T)(g.bsx * g.bsy);

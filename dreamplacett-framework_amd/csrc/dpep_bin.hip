@@ -45,7 +45,7 @@ hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
     b.G1 = (int)g1_of(nc);
     if (b.R != strip_rows(g.N)) return hipErrorInvalidValue;   // the kernel's R
     const size_t count_lds = (size_t)b.S * sizeof(unsigned);
-    const size_t fill_lds = (size_t)(2 * b.S + kBinThreads) * sizeof(unsigned);
+    const size_t fill_lds = (size_t)(2 * b.S + kBinThreads + kChunkCands) * sizeof(unsigned);
     hipError_t e;
     k_bin_count<T><<<b.G1, kBinThreads, count_lds, s>>>(px, py, sx, sy, nc, g, b);
     if ((e = hipGetLastError())) return e;
@@ -55,7 +55,7 @@ hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
     if (ev && (e = hipEventRecord(ev[1], s))) return e;
     e = dispatch_n<T>(g.N, [&](auto lc) -> hipError_t {
         constexpr int L = decltype(lc)::value;
-        k_strip_acc<T, L><<<b.Wmax, kAccThreads, acc_lds_bytes<T, L>(), s>>>(g, b, a, d0n,
+        k_strip_acc<T, L><<<b.Wacc, kAccThreads, acc_lds_bytes<T, L>(), s>>>(g, b, a, d0n,
                                                                              dens, Tt);
         return hipGetLastError();
     });
@@ -72,7 +72,7 @@ hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
 {
     if (nc <= 0) return hipSuccess;
     const size_t lds = (size_t)gather_rows<T>(b.R, g.N) * g.N * 2 * sizeof(T);
-    k_gather_bin<T><<<b.Wmax, kAccThreads, lds, s>>>(g, b, fx, fy);
+    k_gather_bin<T><<<b.Wgat, kAccThreads, lds, s>>>(g, b, fx, fy);
     hipError_t e = hipGetLastError();
     if (e) return e;
     k_gather_out<T><<<g1_of(nc), kBinThreads, kGatherOutLds, s>>>(px, py, sx, sy, nc, g, b, fx, fy, gx,
@@ -100,6 +100,21 @@ hipError_t launch_fixed_density(const T* px, const T* py, const T* sx, const T* 
     k_fixed_flush<T><<<(unsigned)((mn + 255) / 256), 256, 0, s>>>(Bm, d0n, mn,
                                                                   target_density / scale);
     return hipGetLastError();
+}
+
+template <typename T>
+hipError_t bin_occupancy(int N, int R, int& acc_per_cu, int& gat_per_cu)
+{
+    acc_per_cu = gat_per_cu = 0;
+    hipError_t e = dispatch_n<T>(N, [&](auto lc) -> hipError_t {
+        constexpr int L = decltype(lc)::value;
+        return hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &acc_per_cu, (const void*)k_strip_acc<T, L>, kAccThreads, acc_lds_bytes<T, L>());
+    });
+    if (e) return e;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &gat_per_cu, (const void*)k_gather_bin<T>, kAccThreads,
+        (size_t)gather_rows<T>(R, N) * N * 2 * sizeof(T));
 }
 
 template <typename T>
@@ -135,6 +150,8 @@ template hipError_t launch_bin_scatter<double>(const double*, const double*,
                                                const Grid&, BinArgs, const SpectralArgs&,
                                                const double*, double*, double*,
                                                hipStream_t, hipEvent_t*);
+template hipError_t bin_occupancy<float>(int, int, int&, int&);
+template hipError_t bin_occupancy<double>(int, int, int&, int&);
 template hipError_t launch_fixed_density<float>(const float*, const float*, const float*,
                                                 const float*, int, const Grid&, double,
                                                 void*, float*, hipStream_t);

@@ -51,19 +51,27 @@ constexpr int kAccThreads = 1024;      // K4 workgroup size
 constexpr int kCountSlots = 8;         // strip-total counters per strip
 constexpr int kMaxSpanY = 4095;        // larger y spans take the tall path
 
+// Chunk sizes a step may choose for K4 / G1 work items: kChunkMin << k.
+constexpr int kChunkMin = 1024;
+constexpr int kChunkCands = 21;        // up to 2^30 records: never splits
+constexpr int kAccChunkMin = 16384;    // smallest K4 chunk a step chooses
+
 // Shared between host (sizing) and device.
 struct BinArgs {
     int S, R, lgR;          // strips, rows per strip, log2 R
     int G1;                 // K1/K3 workgroups of this step
-    int CH;                 // entries per K4 work item (chunk)
-    int Wmax;               // capacity of the work-item list
+    int Pacc, Pgat;         // K4 / G1 workgroups the device holds at once
+    int Wacc, Wgat;         // K4 / G1 grids = capacities of their item lists
+    int ch_force;           // > 0: every chunk this many records (tests only)
     unsigned* cnt;          // [G1max][S] base of workgroup g in its slot
     unsigned* xtot;         // [kCountSlots][S] slot totals (zero between steps)
     unsigned* strip_off;    // [S + 1] entry offset of each strip
-    unsigned* nch;          // [S] chunks per strip
-    unsigned* item_start;   // [S] first work item of each strip
-    unsigned* items;        // [Wmax] strip | chunk << 16
-    unsigned* nitems;       // [1]
+    unsigned* chunk;        // [2] records per K4 / G1 item, chosen per step
+    unsigned* nch;          // [S] K4 chunks per strip
+    unsigned* item_start;   // [S] first K4 work item of each strip
+    unsigned* items;        // [Wacc] K4 items: strip | chunk << 16
+    unsigned* nitems;       // [2] K4, G1 item counts
+    unsigned* items_g;      // [Wgat] G1 items
     unsigned* done;         // [S] K4 chunks done per strip (zero between steps)
     void* recg;             // [2 nc_max] record geometry, vec4 of T
     unsigned* recm;         // [2 nc_max] record span word
@@ -72,18 +80,17 @@ struct BinArgs {
     void* gtmp;             // [2 nc_max] vec2 forces in record order
     unsigned* bigflag;      // [2S] per strip: 1 + highest, N - lowest column
                             // of its rows in B (0: none; zero between steps)
-    void* B;                // [M*N] uint64, zero between steps
-    void* partial;          // [Wmax][R*N] uint64
+    void* B;                // [M*N] uint64, zero between steps: tall cells and
+                            // the chunks of split strips add into it
 };
 
 // Host-side sizing of the binning buffers (shared with the CPU emulator).
 constexpr size_t kTileBytes = 131072;  // LDS tile of K4 (uint64 words) and G1
 
 struct BinPlan {
-    int S, R, lgR, G1max, CH, Wmax;
+    int S, R, lgR, G1max;
     size_t cap;             // records (2 per cell)
     size_t geo_bytes;       // bytes of one record's geometry (4 elements)
-    size_t partial_elems;   // Wmax * R * N
 };
 
 inline BinPlan make_bin_plan(int M, int N, int nc_max, size_t elem_bytes)
@@ -100,13 +107,17 @@ inline BinPlan make_bin_plan(int M, int N, int nc_max, size_t elem_bytes)
     const long long nc = nc_max > 1 ? nc_max : 1;
     p.G1max = (int)((nc + kCellsPerGroup - 1) / kCellsPerGroup);
     p.cap = (size_t)(2 * nc);
-    long long ch = (long long)(3.0 * 1.15 * (double)nc / p.S) + 1;
-    if (ch < 8192) ch = 8192;
-    ch = (ch + kAccThreads - 1) / kAccThreads * kAccThreads;
-    p.CH = (int)ch;
-    p.Wmax = p.S + (int)((p.cap + ch - 1) / ch) + 1;
-    p.partial_elems = (size_t)p.Wmax * R * N;
     return p;
+}
+
+// The work-item grids of K4 and G1 from the per-CU occupancy of each (both
+// at least one workgroup per strip).
+inline void set_item_grids(BinArgs& b, int acc_per_cu, int gat_per_cu, int cus)
+{
+    b.Pacc = (acc_per_cu > 0 ? acc_per_cu : 1) * (cus > 0 ? cus : 1);
+    b.Pgat = (gat_per_cu > 0 ? gat_per_cu : 1) * (cus > 0 ? cus : 1);
+    b.Wacc = b.Pacc > b.S ? b.Pacc : b.S;
+    b.Wgat = b.Pgat > b.S ? b.Pgat : b.S;
 }
 
 // Strip-binned scatter (K1, K3, K4; K4 also runs the row DCT, writing T)
@@ -128,6 +139,10 @@ template <typename T>
 hipError_t launch_fixed_density(const T* px, const T* py, const T* sx, const T* sy,
                                 int n, const Grid& g, double target_density,
                                 void* B, T* d0n, hipStream_t s);
+
+// Workgroups of K4 (row length N) and G1 that one CU holds at once.
+template <typename T>
+hipError_t bin_occupancy(int N, int R, int& acc_per_cu, int& gat_per_cu);
 
 // Sets the dynamic-LDS limits of every spectral / binning kernel (once).
 hipError_t spectral_prepare();

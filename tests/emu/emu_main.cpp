@@ -125,13 +125,15 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
 
     // strip binning buffers, exact sizes
     BinPlan p = make_bin_plan(M, N, nc, sizeof(T));
-    if (ch > 0) {
-        p.CH = ch;
-        p.Wmax = p.S + (int)((p.cap + ch - 1) / ch) + 1;
-        p.partial_elems = (size_t)p.Wmax * p.R * N;
-    }
     BinArgs b{};
-    b.S = p.S; b.R = p.R; b.lgR = p.lgR; b.CH = p.CH; b.Wmax = p.Wmax;
+    b.S = p.S; b.R = p.R; b.lgR = p.lgR;
+    if (ch > 0) {   // fixed chunks: every list can hold all of them
+        b.ch_force = ch;
+        b.Pacc = b.Pgat = p.S + (int)((p.cap + ch - 1) / ch) + 1;
+        b.Wacc = b.Wgat = b.Pacc;
+    } else {        // chosen per step, as on the device, for a 2-CU "device"
+        set_item_grids(b, 2, 3, 2);
+    }
     b.G1 = (nc + kCellsPerGroup - 1) / kCellsPerGroup;
     if (b.G1 < 1) b.G1 = 1;
     b.cnt = exact<unsigned>((size_t)b.G1 * p.S);
@@ -140,8 +142,10 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     b.strip_off = exact<unsigned>(p.S + 1);
     b.nch = exact<unsigned>(p.S);
     b.item_start = exact<unsigned>(p.S);
-    b.items = exact<unsigned>(p.Wmax);
-    b.nitems = exact<unsigned>(1);
+    b.items = exact<unsigned>(b.Wacc);
+    b.items_g = exact<unsigned>(b.Wgat);
+    b.nitems = exact<unsigned>(2);
+    b.chunk = exact<unsigned>(2);
     if (sizeof(vec4_t<T>) != p.geo_bytes) { fprintf(stderr, "record size mismatch\n"); return 4; }
     b.recg = malloc(p.cap * p.geo_bytes);
     b.recm = exact<unsigned>(p.cap);
@@ -152,15 +156,15 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     b.gtmp = exact<vec2_t<T>>(p.cap);
     b.bigflag = exact<unsigned>(2 * p.S);
     b.B = malloc(mn * 8);
-    b.partial = malloc(p.partial_elems * 8);
     memset(b.B, 0, mn * 8);
     memset(b.bigflag, 0, 2 * p.S * sizeof(unsigned));
     const size_t hist = (size_t)p.S * sizeof(unsigned);
     for (int rep = 0; rep < 2; ++rep) {   // two steps: B / flags must be clean again
         launch(b.G1, kBinThreads, hist, [&] { k_bin_count<T>(px, py, sx, sy, nc, g, b); });
-        launch(b.G1, kBinThreads, (size_t)(2 * p.S + kBinThreads) * sizeof(unsigned),
+        launch(b.G1, kBinThreads,
+               (size_t)(2 * p.S + kBinThreads + kChunkCands) * sizeof(unsigned),
                [&] { k_bin_fill<T>(px, py, sx, sy, nc, g, b); });
-        launch(p.Wmax, kAccThreads, acc_lds_bytes<T, LN>(),
+        launch(b.Wacc, kAccThreads, acc_lds_bytes<T, LN>(),
                [&] { k_strip_acc<T, LN>(g, b, a, d0n, dens, Tt); });
         for (int s2 = 0; s2 < p.S; ++s2)
             if (b.done[s2]) { fprintf(stderr, "strip chunk counter left set\n"); return 4; }
@@ -182,7 +186,7 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     }
     if (nc > 0) {
         const size_t glds = (size_t)gather_rows<T>(p.R, N) * N * 2 * sizeof(T);
-        launch(p.Wmax, kAccThreads, glds, [&] { k_gather_bin<T>(g, b, fx, fy); });
+        launch(b.Wgat, kAccThreads, glds, [&] { k_gather_bin<T>(g, b, fx, fy); });
         launch(b.G1, kBinThreads, kGatherOutLds, [&] { k_gather_out<T>(px, py, sx, sy, nc, g, b, fx, fy, gx, gy); });
     }
     {
@@ -190,8 +194,9 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
         for (size_t i = 0; i < mn * 8; ++i)
             if (Bb[i]) { fprintf(stderr, "side map B not re-zeroed at byte %zu (row %zu)\n", i, i / 8 / N); return 4; }
     }
-    printf("emu plan S=%d R=%d CH=%d Wmax=%d items=%u records=%u\n", p.S, p.R, p.CH,
-           p.Wmax, *b.nitems, b.strip_off[p.S]);
+    printf("emu plan S=%d R=%d chunks=%u/%u items=%u/%u of %d/%d records=%u\n", p.S, p.R,
+           b.chunk[0], b.chunk[1], b.nitems[0], b.nitems[1], b.Wacc, b.Wgat,
+           b.strip_off[p.S]);
 
     // oracle
     std::vector<double> dpx(nc), dpy(nc), dsx(nc), dsy(nc), dd0(mn), rho(mn), rphi(mn), rfx(mn), rfy(mn), rgx(nc), rgy(nc);

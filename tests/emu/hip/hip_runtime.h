@@ -44,6 +44,10 @@ extern dim3 blockDim, gridDim;
 extern std::barrier<>* emu_barrier;
 inline void __syncthreads() { emu_barrier->arrive_and_wait(); }
 inline void __threadfence() { std::atomic_thread_fence(std::memory_order_seq_cst); }
+// __hip_atomic_load is a clang builtin, available to host code as well
+#ifndef __HIP_MEMORY_SCOPE_AGENT
+#define __HIP_MEMORY_SCOPE_AGENT 3
+#endif
 
 using std::floor;
 using std::isfinite;

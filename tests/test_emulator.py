@@ -44,6 +44,7 @@ CASES = [
     "f32 64 64 2000 ch=64 tall", "f32 256 32 600", "f32 32 256 400 tall",
     "f32 32 2048 500",
     "f32 16 4096 2000 tall", "f64 16 4096 100",
+    "f32 16 128 9000 tall",  # chunks chosen per step: both strips split
 ]
 
 
