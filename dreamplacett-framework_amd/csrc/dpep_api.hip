@@ -147,7 +147,7 @@ static void release(dpep_ctx* c)
                     c->d_gy, c->d_T, c->d_Ux, c->d_Uy, c->d_twM,
                     c->d_postM, c->d_twN, c->d_postN, b.cnt, b.xtot, b.strip_off,
                     b.nch, b.item_start, b.items, b.nitems, b.done, b.recg,
-                    b.recm, b.pos, b.pos2, b.gtmp,
+                    b.recm, b.pos, b.gtmp,
                     b.bigflag, b.B, b.chunk, b.items_g};
     for (void* p : bufs)
         if (p) (void)hipFree(p);
@@ -180,7 +180,7 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
         (nc > 0 && (!px || !py || !sx || !sy)) ||
         (gather && (!gx || !gy)) || !b.cnt || !b.strip_off || !b.nch ||
         !b.item_start || !b.items || !b.nitems || !b.done || !b.recg ||
-        !b.recm || !b.pos || !b.pos2 ||
+        !b.recm || !b.pos ||
         !b.gtmp || !b.bigflag || !b.B || !b.chunk || !b.items_g)
         return fail(DPEP_ERR_STATE, "internal: a kernel argument is NULL");
     if (nc > c->nc_max)
@@ -358,8 +358,7 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
         HIP_TRY(hipMemset(b.done, 0, (size_t)p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc(&b.recg, p.cap * p.geo_bytes));
         HIP_TRY(hipMalloc((void**)&b.recm, p.cap * sizeof(unsigned)));
-        HIP_TRY(hipMalloc((void**)&b.pos, (size_t)(nc_max > 0 ? nc_max : 1) * sizeof(unsigned)));
-        HIP_TRY(hipMalloc((void**)&b.pos2, (size_t)(nc_max > 0 ? nc_max : 1) * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.pos, (size_t)(nc_max > 0 ? nc_max : 1) * sizeof(unsigned long long)));
         HIP_TRY(hipMalloc(&b.gtmp, p.cap * 2 * c->esz));
         HIP_TRY(hipMalloc((void**)&b.bigflag, (size_t)2 * p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc(&b.B, (size_t)M * N * accb));

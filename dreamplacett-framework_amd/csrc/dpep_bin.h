@@ -35,7 +35,7 @@
 // [0, 1), and the cell's original extents w, h, from which K4 and G1 re-derive
 // the stretched extents and the area ratio), and one span word.  Short
 // arithmetic on small numbers, which float32 carries to ~1e-7 of a bin
-// (absolute die coordinates would not).  K3 also writes pos[i] and pos2[i],
+// (absolute die coordinates would not).  K3 also writes pos[i] (both slots),
 // the records of cell i (in cell order, coalesced), so G2 can write the
 // forces in cell order instead of G1 scattering them.
 //
@@ -101,8 +101,14 @@ __device__ __forceinline__ void stretch_of(const vec4_t<T>& r, int stretch, T& x
     yr = r.y + hc;
 }
 
-constexpr unsigned kPosTall = 0xFFFFFFFFu;     // pos[i]: tall cell (side map)
-constexpr unsigned kPosNone = 0xFFFFFFFEu;     // pos[i]: contributes nothing
+constexpr unsigned kPosTall = 0xFFFFFFFFu;     // record slot: tall cell (side map)
+constexpr unsigned kPosNone = 0xFFFFFFFEu;     // record slot: none
+
+// pos[i]: the records of cell i in its first and second strip, one word
+__device__ __forceinline__ unsigned long long pos_pair(unsigned p0, unsigned p1)
+{
+    return (unsigned long long)p0 | ((unsigned long long)p1 << 32);
+}
 
 // Strips [s0, s1] a cell occupies and whether it takes the tall path.
 __device__ __forceinline__ void cell_strips(const CellSpan& c, int R, int lgR,
@@ -352,8 +358,7 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill(
         if (i >= nc) break;
         CellSpan c;
         if (!cell_span((double)cx[j], (double)cy[j], (double)cw[j], (double)chh[j], g, c)) {
-            b.pos[i] = kPosNone;
-            b.pos2[i] = kPosNone;
+            b.pos[i] = pos_pair(kPosNone, kPosNone);
             continue;
         }
         int s0, s1;
@@ -377,8 +382,7 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill(
                 atomicMax(&b.bigflag[s], (unsigned)(c.byh + 1));
                 atomicMax(&b.bigflag[b.S + s], (unsigned)(g.N - c.byl));
             }
-            b.pos[i] = kPosTall;
-            b.pos2[i] = kPosNone;
+            b.pos[i] = pos_pair(kPosTall, kPosNone);
             continue;
         }
         // strip-relative record, evaluated in float64 and rounded once
@@ -390,14 +394,13 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill(
         const unsigned p0 = atomicAdd(&cur[s0], 1u);
         recg[p0] = geo;
         b.recm[p0] = span_word(c.bxl - (s0 << b.lgR), nx, ny, c.byl);
-        b.pos[i] = p0;
         unsigned p1 = kPosNone;
         if (s1 != s0) {
             p1 = atomicAdd(&cur[s1], 1u);
             recg[p1] = geo;
             b.recm[p1] = span_word(c.bxl - (s1 << b.lgR), nx, ny, c.byl);
         }
-        b.pos2[i] = p1;
+        b.pos[i] = pos_pair(p0, p1);
     }
 }
 
@@ -910,8 +913,9 @@ __global__ __launch_bounds__(kBinThreads) void k_gather_out(
 #pragma unroll
     for (int j = 0; j < kCellsPerThread; ++j) {
         const int i = c0 + j * kBinThreads;
-        p[j] = i < nc ? b.pos[i] : kPosNone;
-        p2[j] = i < nc ? b.pos2[i] : kPosNone;
+        const unsigned long long pp = i < nc ? b.pos[i] : pos_pair(kPosNone, kPosNone);
+        p[j] = (unsigned)pp;
+        p2[j] = (unsigned)(pp >> 32);
     }
     vec2_t<T> v[kCellsPerThread], v2[kCellsPerThread];
 #pragma unroll

@@ -75,8 +75,8 @@ struct BinArgs {
     unsigned* done;         // [S] K4 chunks done per strip (zero between steps)
     void* recg;             // [2 nc_max] record geometry, vec4 of T
     unsigned* recm;         // [2 nc_max] record span word
-    unsigned* pos;          // [nc_max] record of cell i, or kPosTall / kPosNone
-    unsigned* pos2;         // [nc_max] second-strip record of cell i, or kPosNone
+    unsigned long long* pos;   // [nc_max] records of cell i: first strip (or
+                               // kPosTall / kPosNone) | second strip << 32
     void* gtmp;             // [2 nc_max] vec2 forces in record order
     unsigned* bigflag;      // [2S] per strip: 1 + highest, N - lowest column
                             // of its rows in B (0: none; zero between steps)

@@ -151,8 +151,7 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     b.recm = exact<unsigned>(p.cap);
     b.done = exact<unsigned>(p.S);
     memset(b.done, 0, p.S * sizeof(unsigned));
-    b.pos = exact<unsigned>(nc > 0 ? nc : 1);
-    b.pos2 = exact<unsigned>(nc > 0 ? nc : 1);
+    b.pos = exact<unsigned long long>(nc > 0 ? nc : 1);
     b.gtmp = exact<vec2_t<T>>(p.cap);
     b.bigflag = exact<unsigned>(2 * p.S);
     b.B = malloc(mn * 8);
