@@ -365,7 +365,7 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill(
         bool tall;
         cell_strips(c, b.R, b.lgR, s0, s1, tall);
         if (tall) {
-            const double sc = c.ratio * g.inv_ba;
+            const double sc = c.ratio() * g.inv_ba;
             for (int k = c.bxl; k <= c.bxh; ++k) {
                 const double tx = overlap_1d(c.x, c.w, g.xl, g.bsx, k);
                 if (tx <= 0.0) continue;
@@ -884,8 +884,9 @@ __device__ __forceinline__ void gather_tall(int i, const T* __restrict__ px,
         __syncthreads();
     }
     if (tid == 0) {
-        gx[i] = ok ? (T)(red[0] * c.ratio) : (T)0;
-        gy[i] = ok ? (T)(red[kBinThreads] * c.ratio) : (T)0;
+        const double rat = ok ? c.ratio() : 0.0;
+        gx[i] = ok ? (T)(red[0] * rat) : (T)0;
+        gy[i] = ok ? (T)(red[kBinThreads] * rat) : (T)0;
     }
     __syncthreads();                      // red is reused by the next cell
 }

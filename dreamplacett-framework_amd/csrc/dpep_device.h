@@ -93,8 +93,15 @@ __device__ __forceinline__ unsigned xcd_logical_block(unsigned b, unsigned n)
 // contraction disabled so the GPU reproduces the float64 oracle's spans.
 // ---------------------------------------------------------------------------
 struct CellSpan {
-    double x, y, w, h, ratio;
+    double x, y, w, h;      // stretched corner and extents
+    double sx, sy;          // original extents
     int bxl, bxh, byl, byh;
+    // area ratio sx*sy / (w*h) (1 without stretch); a float64 division, so
+    // only the paths that need it (tall cells) evaluate it
+    __device__ __forceinline__ double ratio() const
+    {
+        return (sx == w && sy == h) ? 1.0 : (sx * sy) / (w * h);
+    }
 };
 
 // Index of the bin containing v (origin + k*bs <= v < origin + (k+1)*bs for
@@ -119,13 +126,12 @@ __device__ __forceinline__ bool cell_span(double px, double py, double sx,
     if (!(isfinite(px) && isfinite(py) && isfinite(sx) && isfinite(sy)))
         return false;
     if (!(sx > 0.0 && sy > 0.0)) return false;
-    double w = sx, h = sy, x = px, y = py, ratio = 1.0;
+    double w = sx, h = sy, x = px, y = py;
     if (g.stretch) {
         w = sx > g.minw ? sx : g.minw;
         h = sy > g.minh ? sy : g.minh;
         x = px + 0.5 * (sx - w);
         y = py + 0.5 * (sy - h);
-        ratio = (sx * sy) / (w * h);
     }
     double fxl = floor_bin(x, g.xl, g.bsx, g.inv_bsx);
     double fxh = floor_bin(x + w, g.xl, g.bsx, g.inv_bsx);
@@ -136,7 +142,7 @@ __device__ __forceinline__ bool cell_span(double px, double py, double sx,
     fxh = fxh > (double)(g.M - 1) ? (double)(g.M - 1) : fxh;
     fyh = fyh > (double)(g.N - 1) ? (double)(g.N - 1) : fyh;
     if (fxl > fxh || fyl > fyh) return false;
-    c.x = x; c.y = y; c.w = w; c.h = h; c.ratio = ratio;
+    c.x = x; c.y = y; c.w = w; c.h = h; c.sx = sx; c.sy = sy;
     c.bxl = (int)fxl; c.bxh = (int)fxh;
     c.byl = (int)fyl; c.byh = (int)fyh;
     return true;
