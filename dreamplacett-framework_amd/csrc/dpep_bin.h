@@ -470,19 +470,24 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     const unsigned e1 = min(e0 + CH, eend);
     const vec4_t<T>* recg = reinterpret_cast<const vec4_t<T>*>(b.recg);
     const T fs = (T)g.fix_scale;
-    // one record per thread per pass (measured faster here than 2, 4 or 8
-    // loads in flight: the 16 waves of the CU already overlap them)
+    // one record per thread per pass, the next one's loads in flight while
+    // it is added (measured faster here than 2, 4 or 8 records per pass, or
+    // than two ahead)
     constexpr int kBatch = 1;
+    vec4_t<T> rgn{};
+    unsigned rmn = 0u;
+    if (e0 + tid < e1) {
+        rgn = recg[e0 + tid];
+        rmn = b.recm[e0 + tid];
+    }
     for (unsigned eb = e0 + tid; eb < e1; eb += kBatch * kAccThreads) {
         vec4_t<T> rg[kBatch];
         unsigned rm[kBatch];
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
-            const unsigned e = eb + j * kAccThreads;
-            if (e < e1) {
-                rg[j] = recg[e];
-                rm[j] = b.recm[e];
-            }
+        rg[0] = rgn;
+        rm[0] = rmn;
+        if (eb + kAccThreads < e1) {     // the next record, in flight meanwhile
+            rgn = recg[eb + kAccThreads];
+            rmn = b.recm[eb + kAccThreads];
         }
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
@@ -727,17 +732,21 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
         }
         __syncthreads();
         const bool first = kg0 == k0;
-        constexpr int kBatch = 2;       // record loads in flight per thread (measured best)
+        constexpr int kBatch = 1;       // one record per pass, the next one in flight
+        vec4_t<T> rgn{};
+        unsigned rmn = 0u;
+        if (e0 + tid < e1) {
+            rgn = recg[e0 + tid];
+            rmn = b.recm[e0 + tid];
+        }
         for (unsigned eb = e0 + tid; eb < e1; eb += kBatch * kAccThreads) {
             vec4_t<T> rgb[kBatch];
             unsigned rmb[kBatch];
-#pragma unroll
-            for (int j = 0; j < kBatch; ++j) {
-                const unsigned e = eb + j * kAccThreads;
-                if (e < e1) {
-                    rgb[j] = recg[e];
-                    rmb[j] = b.recm[e];
-                }
+            rgb[0] = rgn;
+            rmb[0] = rmn;
+            if (eb + kAccThreads < e1) {
+                rgn = recg[eb + kAccThreads];
+                rmn = b.recm[eb + kAccThreads];
             }
 #pragma unroll
             for (int j = 0; j < kBatch; ++j) {
