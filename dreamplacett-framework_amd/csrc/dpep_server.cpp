@@ -116,7 +116,9 @@ int main(int argc, char** argv)
     fflush(stdout);
 
     dpep_ctx* ctx = nullptr;
-    if (dpep_create(M, N, NC_max, xl, yl, xh, yh, DPEP_DTYPE_F32, 0u, &ctx) != DPEP_OK)
+    // the shm header reports every step's timings
+    if (dpep_create(M, N, NC_max, xl, yl, xh, yh, DPEP_DTYPE_F32, DPEP_FLAG_STEP_TIMINGS,
+                    &ctx) != DPEP_OK)
         fatal("dpep_create");
 
     // Open the shm file the client created (poll briefly, :1258-1267).

@@ -29,6 +29,7 @@ DPEP_FLAG_DETERMINISTIC = 0x1
 DPEP_FLAG_NO_POTENTIAL = 0x2
 DPEP_FLAG_NO_STRETCH = 0x4
 DPEP_FLAG_NO_GATHER = 0x8
+DPEP_FLAG_STEP_TIMINGS = 0x10
 
 NUM_TIMINGS = 9
 TIMING_KEYS = ("h2d", "scatter", "gather", "d2h_den", "upload", "compute",
@@ -134,7 +135,7 @@ class Context:
                  xl: float, yl: float, xh: float, yh: float,
                  dtype=np.float32, deterministic: bool = False,
                  potential: bool = True, stretch: bool = True,
-                 gather: bool = True):
+                 gather: bool = True, step_timings: bool = False):
         self._lib = load_library()
         self.M, self.N, self.nc_max = int(num_bins_x), int(num_bins_y), int(nc_max)
         self.dtype = np.dtype(dtype)
@@ -150,6 +151,8 @@ class Context:
             flags |= DPEP_FLAG_NO_STRETCH
         if not gather:
             flags |= DPEP_FLAG_NO_GATHER
+        if step_timings:
+            flags |= DPEP_FLAG_STEP_TIMINGS
         self.flags = flags
         self.potential = potential
         self.gather = gather

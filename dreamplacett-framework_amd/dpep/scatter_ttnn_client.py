@@ -145,7 +145,7 @@ class ScatterTTNNClient:
         if self.inprocess:
             from ._lib import Context
             self._ctx = Context(self.M, self.N, self.nc_max, self.xl, self.yl,
-                                self.xh, self.yh)
+                                self.xh, self.yh, step_timings=True)
             if self._d0_pending is not None:
                 self._ctx.set_initial_density(self._d0_pending)
             self._ready = True

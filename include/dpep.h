@@ -59,6 +59,12 @@ extern "C" {
                                         (the TT path's semantics,
                                         scatter_ttnn_client.py:628-649)    */
 #define DPEP_FLAG_NO_GATHER 0x8u     /* skip the per-cell force gather     */
+#define DPEP_FLAG_STEP_TIMINGS 0x10u /* record a HIP event at the start and
+                                        end of every step, for the compute
+                                        slot of dpep_get_timings (each event
+                                        costs a few microseconds of GPU time
+                                        per step; without the flag the slot
+                                        reads 0 unless profiling is on)    */
 
 /* timing slots, the reference's 9-float shm header order
  * (integration/scatter_ttnn_client.py:151-163): h2d, scatter, gather,

@@ -191,7 +191,7 @@ def test_timings_and_kernel_times():
     import dpep
     from dpep import workloads
     w = workloads.small(3, seed=8, cells=50000, grid=256)
-    with dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh) as ctx:
+    with dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh, step_timings=True) as ctx:
         ctx.set_cells(*w.cells(np.float32))
         ctx.set_profiling(4)
         for _ in range(4):
