@@ -10,9 +10,9 @@
 //                 is added to one of kCountSlots totals per strip and
 //                 the returned old total is the workgroup's base
 //   k_bin_fill    each workgroup scans the strip totals for its own   K3
-//                 offsets (workgroup 0 publishes the strip table and
-//                 chunk list); cells -> strip-sorted records; tall
-//                 cells -> B
+//                 offsets (workgroup 0 publishes the strip table, the
+//                 step's chunk sizes and the K4 / G1 item lists);
+//                 cells -> strip-sorted records; tall cells -> B
 //   k_strip_acc   one work item = (strip, chunk): LDS accumulate,     K4
 //                 flush rho = D0 + tile (+B); the chunks of a split
 //                 strip add into B and the last one to finish flushes
@@ -20,13 +20,13 @@
 //                 rows staged in LDS, each record's partial force over
 //                 the rows of this strip, in record order
 //   k_gather_out  forces back to cell order: sum of the (one or two)  G2
-//                 partials, tall cells gathered directly
+//                 partials; tall cells gathered by the whole workgroup
 //
 // Accumulation is fixed point everywhere: round(v * 2^f) added as uint64
-// (LDS, the side map B), with f = fix_exponent_of(nc_max,
-// dtype) so a bin's sum cannot overflow (each contribution is <= 1).  Integer sums are
-// exact and independent of order, so the density -- and everything computed
-// from it -- is bitwise reproducible run to run.  (On gfx950 ds_add_u64 also
+// (LDS, the side map B), with f = fix_exponent_of(nc_max, dtype) so a bin's
+// sum cannot overflow (each contribution is <= 1).  Integer sums are exact
+// and independent of order, so the density -- and everything computed from
+// it -- is bitwise reproducible run to run.  (On gfx950 ds_add_u64 also
 // runs about seven times faster than ds_add_f32.)
 //
 // K3 evaluates each cell's stretch and span once, in float64, and stores a
@@ -41,8 +41,8 @@
 //
 // A cell whose span covers more than R rows or more than kMaxSpanY + 1
 // columns ("tall") skips the sort: K3 adds it with global atomics into the
-// side map B (zero between steps), marks the strips it touches, and K4 folds
-// and re-zeroes those rows of B.  Every other cell touches at most two
+// side map B (zero between steps), records the column range it touches in
+// each of its strips, and K4 folds and re-zeroes those columns of B.  Every other cell touches at most two
 // strips, so the record arrays hold 2*nc_max.
 #pragma once
 
