@@ -594,6 +594,19 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
 
     // ---- row DCT-II of the strip's R rows: rows (2p, 2p+1) -> FFT slot p --
     constexpr int LP = lds_len(L), E = fft_e(L), TPF = L / E;
+    const bool act = tid < (R / 2) * TPF;
+    const int f = act ? tid / TPF : 0, t = tid % TPF;
+    // the transform's twiddles, loaded before the rows go to LDS (float32;
+    // at float64 the registers they would hold while the rows are live
+    // spill, so they are read where used)
+    const C* post = reinterpret_cast<const C*>(a.postN);
+    FftTw<T, L, E> twp;
+    C pst[E / 2];
+    if constexpr (sizeof(T) == 4) {
+        fft_tw_fetch<T, L, E>(twp, t, reinterpret_cast<const C*>(a.twN));
+#pragma unroll
+        for (int i = 0; i < E / 2; ++i) pst[i] = post_of<T, L>(post, t + TPF * i);
+    }
     C* sbuf = reinterpret_cast<C*>(smem);
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
@@ -604,18 +617,20 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
         }
     }
     __syncthreads();
-    const bool act = tid < (R / 2) * TPF;
-    const int f = act ? tid / TPF : 0, t = tid % TPF;
     C* buf = sbuf + f * LP;
-    fft_lds<T, L, false>(buf, t, reinterpret_cast<const C*>(a.twN), act);
+    if constexpr (sizeof(T) == 4)
+        fft_lds<T, L, false>(buf, t, twp, act);
+    else
+        fft_lds<T, L, false>(buf, t, reinterpret_cast<const C*>(a.twN), act);
     {
-        const C* post = reinterpret_cast<const C*>(a.postN);
         const T scale = (T)2 / (T)L;
         C Xk[E / 2], Xm[E / 2];
         if (act) {
 #pragma unroll
             for (int i = 0; i < E / 2; ++i)
-                dct_post<T, L>(buf, t + TPF * i, post, scale, Xk[i], Xm[i]);
+                dct_post<T, L>(buf, t + TPF * i,
+                               sizeof(T) == 4 ? pst[i] : post_of<T, L>(post, t + TPF * i),
+                               scale, Xk[i], Xm[i]);
         }
         __syncthreads();
         if (act) {

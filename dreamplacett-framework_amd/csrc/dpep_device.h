@@ -163,9 +163,10 @@ __device__ __forceinline__ double overlap_1d(double lo, double ext,
 
 // ---------------------------------------------------------------------------
 // LDS FFT.  One complex FFT of length L is computed by TPF = L / E threads,
-// each holding E = min(16, L) elements per stage.  Stages are radix 16 while
-// the remaining factor allows, then one radix 2/4/8 stage (Stockham autosort:
-// natural order in and out, in place through registers between barriers).
+// each holding E elements per stage (E = min(16, L) unless a pass picks a
+// smaller power of two).  Stages are radix E while the remaining factor
+// allows, then one smaller radix (Stockham autosort: natural order in and
+// out, in place through registers between barriers).
 // ---------------------------------------------------------------------------
 __host__ __device__ constexpr int fft_e(int L) { return L < 16 ? L : 16; }
 __host__ __device__ constexpr int lds_pad(int e) { return e + (e >> 5); }
@@ -284,19 +285,86 @@ __device__ __forceinline__ void dft_r(vec2_t<T>* v)
     else dft16<T, INV>(v);
 }
 
+// Radix of the stage that starts at sub-length NS when each thread holds E
+// elements: E while the remaining factor allows, then the remainder.
+template <int L, int NS, int E>
+__host__ __device__ constexpr int fft_radix()
+{
+    return L / NS >= E ? E : L / NS;
+}
+
+__host__ __device__ constexpr int ilog2c(int x) { return x <= 1 ? 0 : 1 + ilog2c(x / 2); }
+
+// Twiddle-table reads of one thread in the stages from sub-length NS on:
+// E/R butterflies per stage, log2(R) reads each (the power-of-two exponents;
+// the others are products of them), none in the first stage.
+template <int L, int NS, int E>
+__host__ __device__ constexpr int fft_tw_count()
+{
+    if constexpr (NS >= L) {
+        return 0;
+    } else {
+        constexpr int R = fft_radix<L, NS, E>();
+        return (NS > 1 ? (E / R) * ilog2c(R) : 0) + fft_tw_count<L, NS * R, E>();
+    }
+}
+
+template <int L, int NS, int E>
+__host__ __device__ constexpr int fft_tw_next(int off)
+{
+    return off + (NS > 1 ? (E / fft_radix<L, NS, E>()) * ilog2c(fft_radix<L, NS, E>()) : 0);
+}
+
+// Every twiddle a thread's stages read, loaded into registers up front: the
+// loads then overlap the pass's data loads instead of each stage waiting on
+// its own between the LDS reads and the butterflies.  Entries are the
+// forward twiddles exp(-2 pi i m / L); inverse stages conjugate them.
+template <typename T, int L, int E = fft_e(L)>
+struct FftTw {
+    static constexpr int N = fft_tw_count<L, 1, E>();
+    vec2_t<T> w[N > 0 ? N : 1];
+};
+
+// The twiddles of the stage at sub-length NS, entries [OFF, OFF + count).
+template <typename T, int L, int E, int NS, int OFF>
+__device__ __forceinline__ void fft_tw_stage(FftTw<T, L, E>& p, int t,
+                                             const vec2_t<T>* __restrict__ tw)
+{
+    constexpr int R = fft_radix<L, NS, E>();
+    constexpr int TPF = L / E, NB = E / R, LG = ilog2c(R);
+    if constexpr (NS > 1) {
+        constexpr int S = L / (NS * R);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int k = (t + TPF * b) % NS;
+#pragma unroll
+            for (int q = 0; q < LG; ++q) p.w[OFF + b * LG + q] = tw[(1 << q) * k * S];
+        }
+    }
+}
+
+template <typename T, int L, int E, int NS = 1, int OFF = 0>
+__device__ __forceinline__ void fft_tw_fetch(FftTw<T, L, E>& p, int t,
+                                             const vec2_t<T>* __restrict__ tw)
+{
+    if constexpr (NS < L) {
+        fft_tw_stage<T, L, E, NS, OFF>(p, t, tw);
+        fft_tw_fetch<T, L, E, NS * fft_radix<L, NS, E>(), fft_tw_next<L, NS, E>(OFF)>(p, t, tw);
+    }
+}
+
 // One Stockham stage over the FFT held in `buf` (LDS, padded indexing).
-// t: this thread's index within the FFT's TPF threads.  tw: exp(-2 pi i m/L).
-// act = false: a thread of the workgroup that holds no FFT; it only takes
-// part in the barriers.
-template <typename T, int L, int R, int NS, bool INV>
+// t: this thread's index within the FFT's TPF = L / E threads.  pw: this
+// stage's twiddles in the thread's FftTw.  act = false: a thread of the
+// workgroup that holds no FFT; it only takes part in the barriers.
+template <typename T, int L, int E, int R, int NS, bool INV>
 __device__ __forceinline__ void fft_stage(vec2_t<T>* buf, int t,
-                                          const vec2_t<T>* __restrict__ tw,
-                                          bool act)
+                                          const vec2_t<T>* pw, bool act)
 {
     using C = vec2_t<T>;
-    constexpr int E = fft_e(L);
     constexpr int TPF = L / E;
     constexpr int NB = E / R;
+    constexpr int LG = ilog2c(R);
     C v[NB][R];
     if (act) {
 #pragma unroll
@@ -307,18 +375,16 @@ __device__ __forceinline__ void fft_stage(vec2_t<T>* buf, int t,
     }
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-        const int j = t + TPF * b;
-        const int k = j % NS;
         if constexpr (NS > 1) {
-            // W^(r k S) for r < R: the power-of-two exponents come from the
-            // table, the others are products of at most three of them
-            constexpr int S = L / (NS * R);
+            // W^(r k S) for r < R (k = j mod NS, S = L / (NS R)): the
+            // power-of-two exponents come from the table, the others are
+            // products of at most three of them
             C w[R];
 #pragma unroll
             for (int r = 1; r < R; ++r) {
                 const int hi = 1 << (31 - __builtin_clz(r));
                 if (hi == r) {
-                    w[r] = tw[r * k * S];
+                    w[r] = pw[b * LG + ilog2c(r)];
                     if (INV) w[r].y = -w[r].y;
                 } else {
                     w[r] = cmul(w[hi], w[r - hi]);
@@ -344,28 +410,49 @@ __device__ __forceinline__ void fft_stage(vec2_t<T>* buf, int t,
     __syncthreads();
 }
 
-template <typename T, int L, int NS, bool INV>
+template <typename T, int L, int E, int NS, int OFF, bool INV>
 __device__ __forceinline__ void fft_stages(vec2_t<T>* buf, int t,
-                                           const vec2_t<T>* __restrict__ tw,
-                                           bool act)
+                                           const FftTw<T, L, E>& p, bool act)
 {
     if constexpr (NS < L) {
-        constexpr int REM = L / NS;
-        constexpr int R = REM >= fft_e(L) ? fft_e(L) : REM;
-        fft_stage<T, L, R, NS, INV>(buf, t, tw, act);
-        fft_stages<T, L, NS * R, INV>(buf, t, tw, act);
+        constexpr int R = fft_radix<L, NS, E>();
+        fft_stage<T, L, E, R, NS, INV>(buf, t, p.w + OFF, act);
+        fft_stages<T, L, E, NS * R, fft_tw_next<L, NS, E>(OFF), INV>(buf, t, p, act);
     }
 }
 
-// Full in-place FFT; caller must __syncthreads() before (data in LDS).  Every
-// thread of the workgroup calls it (the stages hold barriers); threads with
-// act = false hold no FFT.
-template <typename T, int L, bool INV>
+// Stages that read their own twiddles from the table as they start (fewer
+// registers held than a full FftTw; each stage waits on its reads).
+template <typename T, int L, int E, int NS, int OFF, bool INV>
+__device__ __forceinline__ void fft_stages_tw(vec2_t<T>* buf, int t,
+                                              const vec2_t<T>* __restrict__ tw, bool act)
+{
+    if constexpr (NS < L) {
+        constexpr int R = fft_radix<L, NS, E>();
+        FftTw<T, L, E> p;
+        fft_tw_stage<T, L, E, NS, OFF>(p, t, tw);
+        fft_stage<T, L, E, R, NS, INV>(buf, t, p.w + OFF, act);
+        fft_stages_tw<T, L, E, NS * R, fft_tw_next<L, NS, E>(OFF), INV>(buf, t, tw, act);
+    }
+}
+
+// Full in-place FFT with the thread's twiddles already in registers; caller
+// must __syncthreads() before (data in LDS).  Every thread of the workgroup
+// calls it (the stages hold barriers); threads with act = false hold no FFT.
+template <typename T, int L, bool INV, int E>
+__device__ __forceinline__ void fft_lds(vec2_t<T>* buf, int t, const FftTw<T, L, E>& p,
+                                        bool act = true)
+{
+    fft_stages<T, L, E, 1, 0, INV>(buf, t, p, act);
+}
+
+// The same, each stage reading its twiddles from tw (exp(-2 pi i m / L)).
+template <typename T, int L, bool INV, int E = fft_e(L)>
 __device__ __forceinline__ void fft_lds(vec2_t<T>* buf, int t,
                                         const vec2_t<T>* __restrict__ tw,
                                         bool act = true)
 {
-    fft_stages<T, L, 1, INV>(buf, t, tw, act);
+    fft_stages_tw<T, L, E, 1, 0, INV>(buf, t, tw, act);
 }
 
 }  // namespace dpep

@@ -56,6 +56,34 @@ __host__ __device__ constexpr int fpw(int L)
     return sizeof(T) == 4 ? (L <= 1024 ? 4 : 2) : 2;
 }
 
+// Elements per thread of the FFTs of the column pass (P2) and of the row
+// pass (P3).  A column-pass workgroup holds only F = fpw FFTs and there are
+// N / 2F of them, so fewer elements per thread (more threads per FFT) is
+// how the pass gets more waves in flight.
+template <typename T>
+__host__ __device__ constexpr int col_e(int L)
+{
+    return fft_e(L);
+}
+
+template <typename T>
+__host__ __device__ constexpr int row_e(int L)
+{
+    return fft_e(L);
+}
+
+template <typename T>
+__host__ __device__ constexpr int col_threads(int L)
+{
+    return fpw<T>(L) * (L / col_e<T>(L));
+}
+
+template <typename T>
+__host__ __device__ constexpr int row_threads(int L)
+{
+    return fpw<T>(L) * (L / row_e<T>(L));
+}
+
 template <typename T>
 __device__ __forceinline__ T& comp(vec2_t<T>& c, int which)
 {
@@ -83,19 +111,26 @@ __device__ __forceinline__ T inv_d(int u, int v, const SpectralArgs& a)
     return fast_rcp(wu * wu + wv * wv);
 }
 
+// The post-processing twiddle of slot s: post[s], or post[L/2] for s = 0
+// (the slot that owns {0, L/2}).  post[k] = exp(-i pi k / 2L).
+template <typename T, int L>
+__device__ __forceinline__ vec2_t<T> post_of(const vec2_t<T>* __restrict__ post, int s)
+{
+    return post[s == 0 ? L / 2 : s];
+}
+
 // Forward post-processing of slot s for two packed rows: returns X at k and m
 // (x component = first row, y = second row).
 template <typename T, int L>
 __device__ __forceinline__ void dct_post(const vec2_t<T>* buf, int s,
-                                         const vec2_t<T>* __restrict__ post,
-                                         T scale, vec2_t<T>& Xk,
+                                         vec2_t<T> pc, T scale, vec2_t<T>& Xk,
                                          vec2_t<T>& Xm)
 {
     using C = vec2_t<T>;
     if (s == 0) {
         const C z0 = buf[0];
         const C zh = buf[lds_pad(L / 2)];
-        const T c45 = post[L / 2].x;
+        const T c45 = pc.x;
         Xk = C{z0.x * scale, z0.y * scale};
         Xm = C{zh.x * c45 * scale, zh.y * c45 * scale};
     } else {
@@ -103,9 +138,8 @@ __device__ __forceinline__ void dct_post(const vec2_t<T>* buf, int s,
         const C zb = buf[lds_pad(L - s)];
         const C v1 = C{(T)0.5 * (za.x + zb.x), (T)0.5 * (za.y - zb.y)};
         const C v2 = C{(T)0.5 * (za.y + zb.y), (T)-0.5 * (za.x - zb.x)};
-        const C tw = post[s];
-        const C w1 = cmul(tw, v1);
-        const C w2 = cmul(tw, v2);
+        const C w1 = cmul(pc, v1);
+        const C w2 = cmul(pc, v2);
         Xk = C{w1.x * scale, w2.x * scale};
         Xm = C{-w1.y * scale, -w2.y * scale};
     }
@@ -114,20 +148,17 @@ __device__ __forceinline__ void dct_post(const vec2_t<T>* buf, int s,
 // Inverse pre-processing of slot s for one real spectrum given X[k], X[m]
 // (k = s, m = L - s; for s = 0: k = 0, m = L/2).  rev selects X'[k] = X[L-k].
 template <typename T, int L>
-__device__ __forceinline__ void inv_pre(int s, T xk, T xm, bool rev,
-                                        const vec2_t<T>* __restrict__ post,
+__device__ __forceinline__ void inv_pre(int s, T xk, T xm, bool rev, vec2_t<T> c,
                                         vec2_t<T>& Vk, vec2_t<T>& Vm)
 {
     using C = vec2_t<T>;
     if (s == 0) {
         Vk = C{rev ? (T)0 : xk, (T)0};
-        const C c = post[L / 2];
         // conj(c) * (xm - i xm)
         Vm = C{c.x * xm - c.y * xm, -c.x * xm - c.y * xm};
     } else {
         const T a = rev ? xm : xk;
         const T b = rev ? xk : xm;
-        const C c = post[s];
         // conj(c) * (a - i b)
         Vk = C{c.x * a - c.y * b, -c.x * b - c.y * a};
         // i * c * (b - i a) = i*(c.x b + c.y a) + ... expand:
@@ -148,12 +179,12 @@ __device__ __forceinline__ vec2_t<T> pack2(vec2_t<T> v1, vec2_t<T> v2)
 // three inverse transforms along x; writes Ux, Uy and Up (Up over T) tiled.
 // ---------------------------------------------------------------------------
 template <typename T, int L, int F>
-__global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
+__global__ __launch_bounds__(col_threads<T>(L)) void k_col_pass(
     SpectralArgs a, const T* __restrict__ Tt, T* __restrict__ Ux,
     T* __restrict__ Uy)
 {
     using C = vec2_t<T>;
-    constexpr int E = fft_e(L), TPF = L / E, NT = F * TPF, LP = lds_len(L);
+    constexpr int E = col_e<T>(L), TPF = L / E, NT = F * TPF, LP = lds_len(L);
     constexpr int TV = 2 * F;
     extern __shared__ __align__(16) unsigned char smem[];
     C* sb = reinterpret_cast<C*>(smem);
@@ -175,6 +206,9 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
     // FFT) of one x
     constexpr int V = kVec<T>, NV = L * TV / (NT * V);
     static_assert(NV * NT * V == L * TV && V % 2 == 0 && TV % V == 0, "P2 vector split");
+    const C* post = reinterpret_cast<const C*>(a.postM);
+    C pst[E / 2];           // post-processing twiddles of the thread's slots
+    FftTw<T, L, E> twp;     // and its FFT twiddles (forward; inverse conjugates)
     {
         const int tile_t = TXT * TV;
         const int lgTET = lgTXT + lgTV;
@@ -187,6 +221,9 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
             r[i] = *reinterpret_cast<const pack<T>*>(
                 Tt + ((size_t)bx * NBV + b2) * tile_t + w);
         }
+#pragma unroll
+        for (int i = 0; i < E / 2; ++i) pst[i] = post_of<T, L>(post, t + TPF * i);
+        fft_tw_fetch<T, L, E>(twp, t, reinterpret_cast<const C*>(a.twM));
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int e0 = (tid + i * NT) * V;
@@ -201,14 +238,13 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
         }
     }
     __syncthreads();
-    fft_lds<T, L, false>(buf, t, reinterpret_cast<const C*>(a.twM));
+    fft_lds<T, L, false>(buf, t, twp);
 
-    const C* post = reinterpret_cast<const C*>(a.postM);
     const T scale = (T)2 / (T)L;
     C Ak[E / 2], Am[E / 2];
 #pragma unroll
     for (int i = 0; i < E / 2; ++i)
-        dct_post<T, L>(buf, t + TPF * i, post, scale, Ak[i], Am[i]);
+        dct_post<T, L>(buf, t + TPF * i, pst[i], scale, Ak[i], Am[i]);
 
     // A / D once (zero at (0,0)); the rounds then only scale by w_u / 2
     // (a function of the row k), w_v / 2 (of the column) or 1, so nothing
@@ -247,8 +283,8 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
             const T b2k = Ak[i].y * w2k;
             const T b2m = Am[i].y * w2m;
             C p1k, p1m, p2k, p2m;
-            inv_pre<T, L>(s, b1k, b1m, rev, post, p1k, p1m);
-            inv_pre<T, L>(s, b2k, b2m, rev, post, p2k, p2m);
+            inv_pre<T, L>(s, b1k, b1m, rev, pst[i], p1k, p1m);
+            inv_pre<T, L>(s, b2k, b2m, rev, pst[i], p2k, p2m);
             Vk[i] = pack2<T>(p1k, p2k);
             Vm[i] = pack2<T>(p1m, p2m);
         }
@@ -260,7 +296,7 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
             buf[lds_pad(s == 0 ? L / 2 : L - s)] = Vm[i];
         }
         __syncthreads();
-        fft_lds<T, L, true>(buf, t, reinterpret_cast<const C*>(a.twM));
+        fft_lds<T, L, true>(buf, t, twp);
 
         T* dst = round == 0 ? Ux : Uy;
         const T rscale = round == 1 ? (T)2 : (T)1;
@@ -294,12 +330,12 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_col_pass(
 // type-B block re-reads are still in that XCD's L2.
 // ---------------------------------------------------------------------------
 template <typename T, int L, int F>
-__global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_inv(
+__global__ __launch_bounds__(row_threads<T>(L)) void k_row_inv(
     SpectralArgs a, const T* __restrict__ Ux, const T* __restrict__ Uy,
     T* __restrict__ fx, T* __restrict__ fy, T* __restrict__ phi)
 {
     using C = vec2_t<T>;
-    constexpr int E = fft_e(L), TPF = L / E, NT = F * TPF, LP = lds_len(L);
+    constexpr int E = row_e<T>(L), TPF = L / E, NT = F * TPF, LP = lds_len(L);
     constexpr int TX = 2 * F;
     extern __shared__ __align__(16) unsigned char smem[];
     C* sb = reinterpret_cast<C*>(smem);
@@ -313,6 +349,13 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_inv(
     const int per_group = a.potential ? 3 : 2;
     const int lb = (int)xcd_logical_block(blockIdx.x, gridDim.x);
     const int grp = lb / per_group, role = lb % per_group;
+    // every twiddle the thread needs, loaded before the rows so the latency
+    // of these small (cache-resident) tables overlaps theirs
+    C pst[E / 2];
+#pragma unroll
+    for (int i = 0; i < E / 2; ++i) pst[i] = post_of<T, L>(post, t + TPF * i);
+    FftTw<T, L, E> twp;
+    fft_tw_fetch<T, L, E>(twp, t, tw);
 
     if (role < 2) {
         const int ab = 2 * grp + role;
@@ -353,8 +396,8 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_inv(
             const C zk = buf[lds_pad(s)];
             const C zm = buf[lds_pad(s == 0 ? L / 2 : L - s)];
             C pxk, pxm, pyk, pym;
-            inv_pre<T, L>(s, zk.x, zm.x, false, post, pxk, pxm);
-            inv_pre<T, L>(s, zk.y, zm.y, true, post, pyk, pym);
+            inv_pre<T, L>(s, zk.x, zm.x, false, pst[i], pxk, pxm);
+            inv_pre<T, L>(s, zk.y, zm.y, true, pst[i], pyk, pym);
             Vk[i] = pack2<T>(pxk, pyk);
             Vm[i] = pack2<T>(pxm, pym);
         }
@@ -366,7 +409,7 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_inv(
             buf[lds_pad(s == 0 ? L / 2 : L - s)] = Vm[i];
         }
         __syncthreads();
-        fft_lds<T, L, true>(buf, t, tw);
+        fft_lds<T, L, true>(buf, t, twp);
         const size_t base = (size_t)x0 * L;
 #pragma unroll
         for (int i = 0; i < NVA; ++i) {
@@ -419,8 +462,8 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_inv(
             const C zk = buf[lds_pad(s)];
             const C zm = buf[lds_pad(s == 0 ? L / 2 : L - s)];
             C pak, pam, pbk, pbm;
-            inv_pre<T, L>(s, zk.x, zm.x, false, post, pak, pam);
-            inv_pre<T, L>(s, zk.y, zm.y, false, post, pbk, pbm);
+            inv_pre<T, L>(s, zk.x, zm.x, false, pst[i], pak, pam);
+            inv_pre<T, L>(s, zk.y, zm.y, false, pst[i], pbk, pbm);
             Vk[i] = pack2<T>(pak, pbk);
             Vm[i] = pack2<T>(pam, pbm);
         }
@@ -432,7 +475,7 @@ __global__ __launch_bounds__(F * (L / fft_e(L))) void k_row_inv(
             buf[lds_pad(s == 0 ? L / 2 : L - s)] = Vm[i];
         }
         __syncthreads();
-        fft_lds<T, L, true>(buf, t, tw);
+        fft_lds<T, L, true>(buf, t, twp);
         pack<T>* dst = reinterpret_cast<pack<T>*>(phi + base);
 #pragma unroll
         for (int i = 0; i < NVB; ++i) {

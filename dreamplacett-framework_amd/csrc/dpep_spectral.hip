@@ -18,12 +18,6 @@ constexpr size_t lds_bytes()
     return (size_t)fpw<T>(L) * lds_len(L) * sizeof(vec2_t<T>);
 }
 
-template <typename T, int L>
-constexpr int threads_of()
-{
-    return fpw<T>(L) * (L / fft_e(L));
-}
-
 template <typename T, typename Fn>
 static hipError_t dispatch_len(int L, Fn&& fn)
 {
@@ -52,7 +46,7 @@ hipError_t launch_col_pass(const SpectralArgs& a, const T* Tt, T* Ux, T* Uy,
     return dispatch_len<T>(a.M, [&](auto lc) -> hipError_t {
         constexpr int L = decltype(lc)::value;
         constexpr int F = fpw<T>(L);
-        const dim3 grid(a.N / (2 * F)), block(threads_of<T, L>());
+        const dim3 grid(a.N / (2 * F)), block(col_threads<T>(L));
         k_col_pass<T, L, F><<<grid, block, lds_bytes<T, L>(), s>>>(a, Tt, Ux, Uy);
         return hipGetLastError();
     });
@@ -66,7 +60,7 @@ hipError_t launch_row_inv(const SpectralArgs& a, const T* Ux, const T* Uy,
         constexpr int L = decltype(lc)::value;
         constexpr int F = fpw<T>(L);
         const int groups = a.M / (2 * F);
-        const dim3 grid(groups * (a.potential ? 3 : 2)), block(threads_of<T, L>());
+        const dim3 grid(groups * (a.potential ? 3 : 2)), block(row_threads<T>(L));
         k_row_inv<T, L, F><<<grid, block, lds_bytes<T, L>(), s>>>(a, Ux, Uy, fx, fy, phi);
         return hipGetLastError();
     });

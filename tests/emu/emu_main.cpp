@@ -175,13 +175,13 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     {
         constexpr int F = fpw<T>(LM);
         const size_t shm = (size_t)F * lds_len(LM) * sizeof(vec2_t<T>);
-        launch(N / (2 * F), F * (LM / fft_e(LM)), shm, [&] { k_col_pass<T, LM, F>(a, Tt, Ux, Uy); });
+        launch(N / (2 * F), col_threads<T>(LM), shm, [&] { k_col_pass<T, LM, F>(a, Tt, Ux, Uy); });
     }
     {
         constexpr int F = fpw<T>(LN);
         const size_t shm = (size_t)F * lds_len(LN) * sizeof(vec2_t<T>);
         const unsigned grid = (M / (2 * F)) * (pot ? 3 : 2);
-        launch(grid, F * (LN / fft_e(LN)), shm, [&] { k_row_inv<T, LN, F>(a, Ux, Uy, fx, fy, phi); });
+        launch(grid, row_threads<T>(LN), shm, [&] { k_row_inv<T, LN, F>(a, Ux, Uy, fx, fy, phi); });
     }
     if (nc > 0) {
         const size_t glds = (size_t)gather_rows<T>(p.R, N) * N * 2 * sizeof(T);

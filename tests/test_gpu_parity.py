@@ -203,6 +203,12 @@ def test_timings_and_kernel_times():
     assert all(v > 0 for v in kt.values())
     assert kt["step"] >= kt["strip_acc"] + kt["col_pass"]
     assert set(t) == set(dpep.TIMING_KEYS) and t["total"] > 0
+    # without DPEP_FLAG_STEP_TIMINGS (and without profiling) no step event is
+    # recorded: the compute slot reads 0, the results are the same
+    with dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh) as ctx:
+        out = ctx.step(*w.cells(np.float32))
+        t0 = ctx.timings()
+    assert t0["compute"] == 0.0 and np.isfinite(out["density"]).all()
 
 
 def test_step_device_matches_host_step():
