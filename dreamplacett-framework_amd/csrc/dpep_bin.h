@@ -462,9 +462,6 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     const unsigned n = b.nch[s];
     const unsigned CH = b.chunk[0];
     unsigned* last_flag = reinterpret_cast<unsigned*>(tile + RN);   // LDS word
-    for (int e = tid; e < RN; e += kAccThreads) tile[e] = 0ull;
-    __syncthreads();
-
     const unsigned e0 = b.strip_off[s] + (unsigned)chunk * CH;
     const unsigned eend = b.strip_off[s + 1];
     const unsigned e1 = min(e0 + CH, eend);
@@ -472,7 +469,7 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     const T fs = (T)g.fix_scale;
     // one record per thread per pass, the next one's loads in flight while
     // it is added (measured faster here than 2, 4 or 8 records per pass, or
-    // than two ahead)
+    // than two ahead); the first ones are issued before the tile is zeroed
     constexpr int kBatch = 1;
     vec4_t<T> rgn{};
     unsigned rmn = 0u;
@@ -480,6 +477,8 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
         rgn = recg[e0 + tid];
         rmn = b.recm[e0 + tid];
     }
+    for (int e = tid; e < RN; e += kAccThreads) tile[e] = 0ull;
+    __syncthreads();
     for (unsigned eb = e0 + tid; eb < e1; eb += kBatch * kAccThreads) {
         vec4_t<T> rg[kBatch];
         unsigned rm[kBatch];

@@ -432,9 +432,9 @@ __global__ __launch_bounds__(row_threads<T>(L)) void k_row_inv(
         const int lgTE = __builtin_ctz(TX) + lgTV;
         constexpr int V = kVec<T>, NVB = TX * L / (NT * V);
         static_assert(NVB * NT * V == TX * L, "P3 vector split");
+        const T wv = (T)a.wv_step;
         {
             const pack<T>* src = reinterpret_cast<const pack<T>*>(Uy + base);
-            const T wv = (T)a.wv_step;
             pack<T> r[NVB];
 #pragma unroll
             for (int i = 0; i < NVB; ++i) r[i] = src[tid + i * NT];
@@ -447,11 +447,7 @@ __global__ __launch_bounds__(row_threads<T>(L)) void k_row_inv(
                 const int v = (bv << lgTV) + (w & (TV - 1));
                 C* rowp = sb + (x_in >> 1) * LP;
 #pragma unroll
-                for (int q = 0; q < V; ++q) {
-                    const int vq = v + q;
-                    const T up = r[i].v[q] * fast_rcp((T)(vq > 0 ? vq : 1) * wv);
-                    comp<T>(rowp[lds_pad(vq)], x_in & 1) = up;
-                }
+                for (int q = 0; q < V; ++q) comp<T>(rowp[lds_pad(v + q)], x_in & 1) = r[i].v[q];
             }
         }
         __syncthreads();
@@ -459,11 +455,14 @@ __global__ __launch_bounds__(row_threads<T>(L)) void k_row_inv(
 #pragma unroll
         for (int i = 0; i < E / 2; ++i) {
             const int s = t + TPF * i;
+            const int m = s == 0 ? L / 2 : L - s;
             const C zk = buf[lds_pad(s)];
-            const C zm = buf[lds_pad(s == 0 ? L / 2 : L - s)];
+            const C zm = buf[lds_pad(m)];
+            // Up = Uy / w_v at the slot's two columns (column 0: / w_v(1))
+            const T rk = fast_rcp((T)(s > 0 ? s : 1) * wv), rm = fast_rcp((T)m * wv);
             C pak, pam, pbk, pbm;
-            inv_pre<T, L>(s, zk.x, zm.x, false, pst[i], pak, pam);
-            inv_pre<T, L>(s, zk.y, zm.y, false, pst[i], pbk, pbm);
+            inv_pre<T, L>(s, zk.x * rk, zm.x * rm, false, pst[i], pak, pam);
+            inv_pre<T, L>(s, zk.y * rk, zm.y * rm, false, pst[i], pbk, pbm);
             Vk[i] = pack2<T>(pak, pbk);
             Vm[i] = pack2<T>(pam, pbm);
         }
