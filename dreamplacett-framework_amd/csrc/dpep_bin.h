@@ -648,7 +648,7 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
         constexpr int V = kVec<T>;
         const int TX = a.tiles.TXT, TV = a.tiles.TV;
         const int lgTV = __builtin_ctz(TV);
-        const int TE = TX * TV, NBV = L / TV;
+        const int lgTX = __builtin_ctz(TX), lgNBV = __builtin_ctz(L) - lgTV;
         const int TXe = R < TX ? R : TX;
         const int lgTXe = __builtin_ctz(TXe);
         constexpr int lgL = __builtin_ctz(L);
@@ -664,8 +664,10 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
             pack<T> o;
 #pragma unroll
             for (int q = 0; q < V; ++q) o.v[q] = comp_of<T>(rowp[lds_pad(v + q)], r & 1);
-            const size_t gi = ((size_t)(x / TX) * NBV + bv) * TE + (size_t)(x % TX) * TV +
-                              (wv & (TV - 1));
+            // tile (x / TX, bv), row x % TX within it (powers of two: shifts)
+            const unsigned gi =
+                (((((unsigned)x >> lgTX) << lgNBV) + (unsigned)bv) << (lgTX + lgTV)) +
+                (((unsigned)x & (TX - 1)) << lgTV) + (unsigned)(wv & (TV - 1));
             *reinterpret_cast<pack<T>*>(Tt + gi) = o;
         }
     }

@@ -194,7 +194,8 @@ __global__ __launch_bounds__(col_threads<T>(L)) void k_col_pass(
     const int lgTX = __builtin_ctz(TX);
     const int TXT = a.tiles.TXT;          // T tiles (loads)
     const int lgTXT = __builtin_ctz(TXT);
-    const int NBV = a.N / TV;
+    // tile offsets by shifts: every tile extent and N are powers of two
+    const int lgNBV = __builtin_ctz(a.N) - __builtin_ctz(TV);
     const int b2 = blockIdx.x;
     const int v0 = b2 * TV;
     constexpr int lgTV = __builtin_ctz(TV);
@@ -219,7 +220,7 @@ __global__ __launch_bounds__(col_threads<T>(L)) void k_col_pass(
             const int bx = e0 >> lgTET;
             const int w = e0 & (tile_t - 1);
             r[i] = *reinterpret_cast<const pack<T>*>(
-                Tt + ((size_t)bx * NBV + b2) * tile_t + w);
+                Tt + (((((unsigned)bx << lgNBV) + (unsigned)b2) << lgTET) + (unsigned)w));
         }
 #pragma unroll
         for (int i = 0; i < E / 2; ++i) pst[i] = post_of<T, L>(post, t + TPF * i);
@@ -316,7 +317,8 @@ __global__ __launch_bounds__(col_threads<T>(L)) void k_col_pass(
                 o.v[q] = z.x * sc;
                 o.v[q + 1] = z.y * sc;
             }
-            *reinterpret_cast<pack<T>*>(dst + ((size_t)bx * NBV + b2) * tile_elems + w) = o;
+            *reinterpret_cast<pack<T>*>(
+                dst + (((((unsigned)bx << lgNBV) + (unsigned)b2) << lgTE) + (unsigned)w)) = o;
         }
     }
 }
@@ -343,7 +345,7 @@ __global__ __launch_bounds__(row_threads<T>(L)) void k_row_inv(
     C* buf = sb + f * LP;
     const int TV = a.tiles.TV;
     const int lgTV = __builtin_ctz(TV);
-    const int NBV = L / TV;
+    const int lgNBV = __builtin_ctz(L) - lgTV;
     const C* post = reinterpret_cast<const C*>(a.postN);
     const C* tw = reinterpret_cast<const C*>(a.twN);
     const int per_group = a.potential ? 3 : 2;
@@ -372,7 +374,9 @@ __global__ __launch_bounds__(row_threads<T>(L)) void k_row_inv(
                 const int e0 = (tid + i * NT) * V;
                 const int bv = e0 >> lgCH;
                 const int w = e0 & (chunk - 1);
-                const size_t g = ((size_t)bx * NBV + bv) * (TX * TV) + half * chunk + w;
+                const unsigned g =
+                    ((((unsigned)bx << lgNBV) + (unsigned)bv) << (__builtin_ctz(TX) + lgTV)) +
+                    (unsigned)(half * chunk + w);
                 rx[i] = *reinterpret_cast<const pack<T>*>(Ux + g);
                 ry[i] = *reinterpret_cast<const pack<T>*>(Uy + g);
             }
