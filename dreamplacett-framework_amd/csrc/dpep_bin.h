@@ -128,6 +128,37 @@ __device__ __forceinline__ bool load_span(const T* px, const T* py,
                      (double)sy[i], g, c);
 }
 
+// The kCellsPerThread cells of thread tid in the workgroup's block starting
+// at c0 (zero past nc).  A full block loads unconditionally: with a branch per
+// cell the compiler moves each float32 -> float64 conversion into the branch
+// and waits there for the load, so the four cells' loads no longer overlap.
+template <typename T>
+__device__ __forceinline__ void load_cells(const T* __restrict__ px, const T* __restrict__ py,
+                                           const T* __restrict__ sx, const T* __restrict__ sy,
+                                           int nc, int c0, int tid, T* cx, T* cy, T* cw, T* ch)
+{
+    if (c0 + kCellsPerGroup <= nc) {
+#pragma unroll
+        for (int j = 0; j < kCellsPerThread; ++j) {
+            const int i = c0 + tid + j * kBinThreads;
+            cx[j] = px[i];
+            cy[j] = py[i];
+            cw[j] = sx[i];
+            ch[j] = sy[i];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < kCellsPerThread; ++j) {
+            const int i = c0 + tid + j * kBinThreads;
+            const bool ok = i < nc;
+            cx[j] = ok ? px[i] : (T)0;
+            cy[j] = ok ? py[i] : (T)0;
+            cw[j] = ok ? sx[i] : (T)0;
+            ch[j] = ok ? sy[i] : (T)0;
+        }
+    }
+}
+
 __device__ __forceinline__ unsigned long long to_fixed(double v, double scale)
 {
     return (unsigned long long)__double2ull_rn(v * scale);
@@ -293,15 +324,7 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_count(
     const int c0 = blockIdx.x * kCellsPerGroup;
     // all loads of this thread's cells first (independent, in flight together)
     T cx[kCellsPerThread], cy[kCellsPerThread], cw[kCellsPerThread], ch[kCellsPerThread];
-#pragma unroll
-    for (int j = 0; j < kCellsPerThread; ++j) {
-        const int i = c0 + tid + j * kBinThreads;
-        const bool ok = i < nc;
-        cx[j] = ok ? px[i] : (T)0;
-        cy[j] = ok ? py[i] : (T)0;
-        cw[j] = ok ? sx[i] : (T)0;
-        ch[j] = ok ? sy[i] : (T)0;
-    }
+    load_cells(px, py, sx, sy, nc, c0, tid, cx, cy, cw, ch);
 #pragma unroll
     for (int j = 0; j < kCellsPerThread; ++j) {
         CellSpan c;
@@ -338,21 +361,14 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill(
     extern __shared__ __align__(16) unsigned char smem[];
     unsigned* cur = reinterpret_cast<unsigned*>(smem);
     const int tid = threadIdx.x;
+    // the cells' loads are issued first: their latency overlaps the offsets
+    const int c0 = blockIdx.x * kCellsPerGroup;
+    T cx[kCellsPerThread], cy[kCellsPerThread], cw[kCellsPerThread], chh[kCellsPerThread];
+    load_cells(px, py, sx, sy, nc, c0, tid, cx, cy, cw, chh);
     strip_offsets(b, cur, cur + b.S, cur + 2 * b.S);
     __syncthreads();
     vec4_t<T>* recg = reinterpret_cast<vec4_t<T>*>(b.recg);
     unsigned long long* Bm = reinterpret_cast<unsigned long long*>(b.B);
-    const int c0 = blockIdx.x * kCellsPerGroup;
-    T cx[kCellsPerThread], cy[kCellsPerThread], cw[kCellsPerThread], chh[kCellsPerThread];
-#pragma unroll
-    for (int j = 0; j < kCellsPerThread; ++j) {
-        const int i = c0 + tid + j * kBinThreads;
-        const bool ok = i < nc;
-        cx[j] = ok ? px[i] : (T)0;
-        cy[j] = ok ? py[i] : (T)0;
-        cw[j] = ok ? sx[i] : (T)0;
-        chh[j] = ok ? sy[i] : (T)0;
-    }
     for (int j = 0; j < kCellsPerThread; ++j) {
         const int i = c0 + tid + j * kBinThreads;
         if (i >= nc) break;
