@@ -445,6 +445,15 @@ __host__ __device__ constexpr int strip_rows(int N)
     return R;
 }
 
+// Elements per thread of K4's row DCT: the fewest (8 or more) that keep the
+// strip's R / 2 FFTs within the workgroup, so every thread takes part.
+__host__ __device__ constexpr int acc_e(int L, int R)
+{
+    int e = 8;
+    while (e < fft_e(L) && (R / 2) * (L / e) > kAccThreads) e <<= 1;
+    return e < L ? e : L;
+}
+
 template <typename T, int L>
 __host__ __device__ constexpr size_t acc_lds_bytes()
 {
@@ -608,7 +617,7 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     }
 
     // ---- row DCT-II of the strip's R rows: rows (2p, 2p+1) -> FFT slot p --
-    constexpr int LP = lds_len(L), E = fft_e(L), TPF = L / E;
+    constexpr int LP = lds_len(L), E = acc_e(L, R), TPF = L / E;
     const bool act = tid < (R / 2) * TPF;
     const int f = act ? tid / TPF : 0, t = tid % TPF;
     // the transform's twiddles, loaded before the rows go to LDS (float32;
@@ -636,7 +645,7 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     if constexpr (sizeof(T) == 4)
         fft_lds<T, L, false>(buf, t, twp, act);
     else
-        fft_lds<T, L, false>(buf, t, reinterpret_cast<const C*>(a.twN), act);
+        fft_lds<T, L, false, E>(buf, t, reinterpret_cast<const C*>(a.twN), act);
     {
         const T scale = (T)2 / (T)L;
         C Xk[E / 2], Xm[E / 2];
