@@ -34,7 +34,7 @@ PMC_SUMMARY = os.path.join(ROOT, "profiles", "kernels_c3_1.1M_2048.md")
 PMC_NAMES = {"bin_count": "k_bin_count", "bin_fill": "k_bin_fill",
              "strip_acc": "k_strip_acc",
              "col_pass": "k_col_pass", "row_inv": "k_row_inv",
-             "gather": ("k_gather_bin", "k_gather_out")}
+             "gather_bin": "k_gather_bin", "gather_out": "k_gather_out"}
 METRIC = ("ms per potential step (scatter+DCT+field), 1.1M cells @2048^2; "
           "% HBM peak")
 
@@ -50,7 +50,8 @@ def kernel_bytes(nc, M, N, esz, potential=True):
         "strip_acc": 3 * esz * mn,                     # read D0, write rho and T (row DCT fused)
         "col_pass": 3 * esz * mn,                      # read T, write Ux, Uy
         "row_inv": (2 + nmaps) * esz * mn,             # read Ux, Uy, write maps
-        "gather": 6 * esz * nc + 2 * esz * mn,         # cells, fields, forces
+        "gather_bin": 2 * esz * mn,                    # read fx, fy (records: scratch)
+        "gather_out": 6 * esz * nc,                    # the cells' 4 arrays in, forces out
     }
 
 
@@ -85,7 +86,7 @@ def step_bytes(nc, M, N, esz, potential=True):
     return 10 * esz * nc + (13 if potential else 12) * esz * M * N
 
 
-def cpu_baseline(w, seconds, max_steps=20):
+def cpu_baseline(w, seconds, max_steps=400):
     import pyoracle
     cb = pyoracle.CpuBaseline(w.M, w.N, w.xl, w.yl, w.xh, w.yh)
     px, py, sx, sy = w.cells(np.float32)
@@ -123,7 +124,7 @@ def main():
     ap.add_argument("--dtype", choices=["f32", "f64"], default="f32")
     ap.add_argument("--deterministic", action="store_true")
     ap.add_argument("--no-potential", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="wall-clock budget of the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true",

@@ -51,7 +51,7 @@ int fail(int code, const char* fmt, ...)
 
 // strip count (+ table), strip fill, strip accumulate (+ row DCT), column
 // pass, row inverse, gather
-constexpr int kNumStages = 6;
+constexpr int kNumStages = 7;
 
 bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
@@ -205,7 +205,9 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
     if (prof) HIP_TRY(hipEventRecord(pe[5], s));
     if (gather)
         HIP_TRY(launch_bin_gather<T>(px, py, sx, sy, nc, c->grid, c->bins, fx, fy,
-                                     gx, gy, s));
+                                     gx, gy, s, prof ? pe[6] : nullptr));
+    else if (prof)
+        HIP_TRY(hipEventRecord(pe[6], s));
     if (prof) HIP_TRY(hipEventRecord(pe[kNumStages], s));
     if (timed) HIP_TRY(hipEventRecord(c->ev[kNumStages], s));
     if (prof) c->prof_steps++;

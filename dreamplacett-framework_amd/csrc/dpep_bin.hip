@@ -68,13 +68,14 @@ template <typename T>
 hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
                              const T* sy, int nc, const Grid& g,
                              const BinArgs& b, const T* fx, const T* fy,
-                             T* gx, T* gy, hipStream_t s)
+                             T* gx, T* gy, hipStream_t s, hipEvent_t ev)
 {
-    if (nc <= 0) return hipSuccess;
+    if (nc <= 0) return ev ? hipEventRecord(ev, s) : hipSuccess;
     const size_t lds = (size_t)gather_rows<T>(b.R, g.N) * g.N * 2 * sizeof(T);
     k_gather_bin<T><<<b.Wgat, kAccThreads, lds, s>>>(g, b, fx, fy);
     hipError_t e = hipGetLastError();
     if (e) return e;
+    if (ev && (e = hipEventRecord(ev, s))) return e;
     k_gather_out<T><<<g1_of(nc), kBinThreads, kGatherOutLds, s>>>(px, py, sx, sy, nc, g, b, fx, fy, gx,
                                                       gy);
     return hipGetLastError();
@@ -162,11 +163,11 @@ template hipError_t launch_fixed_density<double>(const double*, const double*,
 template hipError_t launch_bin_gather<float>(const float*, const float*, const float*,
                                              const float*, int, const Grid&,
                                              const BinArgs&, const float*, const float*,
-                                             float*, float*, hipStream_t);
+                                             float*, float*, hipStream_t, hipEvent_t);
 template hipError_t launch_bin_gather<double>(const double*, const double*,
                                               const double*, const double*, int,
                                               const Grid&, const BinArgs&, const double*,
                                               const double*, double*, double*,
-                                              hipStream_t);
+                                              hipStream_t, hipEvent_t);
 
 }  // namespace dpep

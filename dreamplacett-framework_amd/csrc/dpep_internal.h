@@ -121,7 +121,8 @@ inline void set_item_grids(BinArgs& b, int acc_per_cu, int gat_per_cu, int cus)
 }
 
 // Strip-binned scatter (K1, K3, K4; K4 also runs the row DCT, writing T)
-// and gather (G1, G2); ev (nullable) receives 3 events: after K1, K3, K4.
+// and gather (G1, G2); the scatter's ev (nullable) receives 3 events: after
+// K1, K3, K4; the gather's ev (nullable) is recorded between G1 and G2.
 template <typename T>
 hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
                               const T* sy, int nc, const Grid& g, BinArgs b,
@@ -131,7 +132,7 @@ template <typename T>
 hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
                              const T* sy, int nc, const Grid& g,
                              const BinArgs& b, const T* fx, const T* fy,
-                             T* gx, T* gy, hipStream_t s);
+                             T* gx, T* gy, hipStream_t s, hipEvent_t ev);
 
 // D0n = target_density * exact overlap of n fixed cells / bin area, through
 // the side map B (left at zero).

@@ -35,7 +35,7 @@ NUM_TIMINGS = 9
 TIMING_KEYS = ("h2d", "scatter", "gather", "d2h_den", "upload", "compute",
                "download", "fw", "total")
 KERNEL_KEYS = ("bin_count", "bin_fill", "strip_acc", "col_pass", "row_inv",
-               "gather", "step")
+               "gather_bin", "gather_out", "step")
 
 # Every symbol include/dpep.h declares, with (restype, argtypes).
 _vp = ctypes.c_void_p

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define DPEP_ABI_VERSION 1
+#define DPEP_ABI_VERSION 2
 
 /* status codes */
 #define DPEP_OK 0
@@ -163,8 +163,10 @@ int dpep_get_timings(dpep_ctx* ctx, float* out);
  * events around each launch on the stream the kernels run on:
  * [0] strip count (with the strip table), [1] strip fill, [2] strip
  * accumulate with the row DCT (and the reduction of split strips),
- * [3] column DCT + inverse, [4] row inverse, [5] gather, [6] whole step.
- * n = floats in out. */
+ * [3] column DCT + inverse, [4] row inverse, [5] gather of the partial
+ * forces per strip record, [6] forces in cell order, [7] whole step.
+ * n = floats in out.  (ABI version 1 had one gather slot at [5] and the
+ * step at [6].) */
 int dpep_get_kernel_times(dpep_ctx* ctx, float* out, int n);
 
 /* slots > 0 enables per-kernel event timing for a ring of `slots` steps

@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_info():
     import dpep
     lib = dpep.load_library()
-    assert lib.dpep_abi_version() == 1
+    assert lib.dpep_abi_version() == 2
     assert b"gfx950" in lib.dpep_build_info()
 
 
