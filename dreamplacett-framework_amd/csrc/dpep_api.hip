@@ -365,11 +365,11 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
         HIP_TRY(hipMalloc((void**)&b.recm, p.cap * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.pos, (size_t)(nc_max > 0 ? nc_max : 1) * sizeof(unsigned long long)));
         HIP_TRY(hipMalloc(&b.gtmp, p.cap * 2 * c->esz));
-        HIP_TRY(hipMalloc((void**)&b.bigflag, (size_t)2 * p.S * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.bigflag, (size_t)kSideWords * p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc(&b.B, (size_t)M * N * accb));
         // B and the strip flags must start at zero; each step leaves them so.
         HIP_TRY(hipMemset(b.B, 0, (size_t)M * N * accb));
-        HIP_TRY(hipMemset(b.bigflag, 0, (size_t)2 * p.S * sizeof(unsigned)));
+        HIP_TRY(hipMemset(b.bigflag, 0, (size_t)kSideWords * p.S * sizeof(unsigned)));
         HIP_TRY(hipDeviceSynchronize());
         return dtype == DPEP_DTYPE_F32 ? upload_tables<float>(c)
                                        : upload_tables<double>(c);

@@ -104,6 +104,26 @@ __device__ __forceinline__ void stretch_of(const vec4_t<T>& r, int stretch, T& x
 constexpr unsigned kPosTall = 0xFFFFFFFFu;     // record slot: tall cell (side map)
 constexpr unsigned kPosNone = 0xFFFFFFFEu;     // record slot: none
 
+// Columns of the side map B that hold a strip's tall-cell sums: a bitmap of
+// kSideBits column blocks of side_block(N) columns (kSideWords words per
+// strip), so K4 folds and re-zeroes only the blocks its tall cells touch.
+__host__ __device__ constexpr int side_block(int N)
+{
+    return N / kSideBits > 16 ? N / kSideBits : 16;
+}
+
+// Sets the bits of column blocks [c0 / CB, c1 / CB] in one strip's words:
+// one atomicOr per word the range overlaps.
+__device__ __forceinline__ void side_mark(unsigned* __restrict__ words, int c0, int c1, int CB)
+{
+    const int b0 = c0 / CB, b1 = c1 / CB;
+    for (int w = b0 >> 5; w <= (b1 >> 5); ++w) {
+        const int lo = max(b0 - (w << 5), 0), hi = min(b1 - (w << 5), 31);
+        const unsigned m = (hi == 31 ? 0xFFFFFFFFu : ((1u << (hi + 1)) - 1u)) & ~((1u << lo) - 1u);
+        atomicOr(&words[w], m);
+    }
+}
+
 // pos[i]: the records of cell i in its first and second strip, one word
 __device__ __forceinline__ unsigned long long pos_pair(unsigned p0, unsigned p1)
 {
@@ -393,11 +413,10 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill(
                     atomicAdd(&Bm[rowi + q], to_fixed(stx * ty, g.fix_scale));
                 }
             }
-            // the strips' column range in B: highest + 1, N - lowest
-            for (int s = s0; s <= s1; ++s) {
-                atomicMax(&b.bigflag[s], (unsigned)(c.byh + 1));
-                atomicMax(&b.bigflag[b.S + s], (unsigned)(g.N - c.byl));
-            }
+            // the column blocks of B this cell touches, in each of its strips
+            const int CB = side_block(g.N);
+            for (int s = s0; s <= s1; ++s)
+                side_mark(b.bigflag + (size_t)s * kSideWords, c.byl, c.byh, CB);
             b.pos[i] = pos_pair(kPosTall, kPosNone);
             continue;
         }
@@ -569,13 +588,18 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
 
     // ---- flush: rho = D0 + tile (+B), kept in registers ------------------
     constexpr int PER = (RN + kAccThreads - 1) / kAccThreads;
-    // columns [blo, bhi) of the strip's rows hold sums in B: the tall cells'
-    // range, or all of them for a split strip (read at device scope: the
-    // other chunks added them in this launch)
+    // the column blocks of the strip's rows that hold sums in B: those its
+    // tall cells marked, or all of them for a split strip (read at device
+    // scope: the other chunks added them in this launch)
     const bool split = n > 1u;
-    const int bhi = split ? N : (int)b.bigflag[s];
-    const int blo = split ? 0 : N - (int)b.bigflag[b.S + s];
-    const bool bf = bhi != 0;
+    constexpr int CB = side_block(N);
+    unsigned side[kSideWords];
+    bool bf = split;
+#pragma unroll
+    for (int q = 0; q < kSideWords; ++q) {
+        side[q] = split ? 0xFFFFFFFFu : b.bigflag[(size_t)s * kSideWords + q];
+        bf = bf || side[q] != 0u;
+    }
     T rv[PER];
     {
         A v[PER];
@@ -592,8 +616,8 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
 #pragma unroll
             for (int j = 0; j < PER; ++j) {
                 const int e = tid + j * kAccThreads;
-                const int col = e & (N - 1);
-                if (e < RN && col >= blo && col < bhi) {
+                const int cb = (e & (N - 1)) / CB;
+                if (e < RN && ((side[cb >> 5] >> (cb & 31)) & 1u)) {
                     v[j] += split ? __hip_atomic_load(&Bm[gbase + e], __ATOMIC_RELAXED,
                                                       __HIP_MEMORY_SCOPE_AGENT)
                                   : Bm[gbase + e];
@@ -610,11 +634,9 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
             }
         }
     }
-    __syncthreads();   // the tile is dead (the FFT buffers alias it); bigflag read
-    if (tid == 0 && (split || b.bigflag[s] != 0u)) {
-        b.bigflag[s] = 0u;
-        b.bigflag[b.S + s] = 0u;
-    }
+    __syncthreads();   // the tile is dead (the FFT buffers alias it); bitmap read
+    if (tid < kSideWords && (split || side[tid] != 0u))
+        b.bigflag[(size_t)s * kSideWords + tid] = 0u;
 
     // ---- row DCT-II of the strip's R rows: rows (2p, 2p+1) -> FFT slot p --
     constexpr int LP = lds_len(L), E = acc_e(L, R), TPF = L / E;
@@ -892,8 +914,11 @@ __global__ __launch_bounds__(256) void k_fixed_flush(unsigned long long* __restr
 // costs one round of loads instead of a serial walk over its bins.
 // LDS: ntall | list[kCellsPerGroup] | red[2][kBinThreads] (doubles).
 // ---------------------------------------------------------------------------
+// LDS of G2: the tall-cell count and list, one bit per list entry marking
+// the cells too large for a team, and the workgroup-wide reduction buffer
 constexpr size_t kGatherOutLds =
-    ((1 + kCellsPerGroup) * sizeof(unsigned) + 15) / 16 * 16 + 2 * kBinThreads * sizeof(double);
+    ((1 + kCellsPerGroup + kCellsPerGroup / 32) * sizeof(unsigned) + 15) / 16 * 16 +
+    2 * kBinThreads * sizeof(double);
 
 template <typename T>
 __device__ __forceinline__ void gather_tall(int i, const T* __restrict__ px,
@@ -941,9 +966,61 @@ __device__ __forceinline__ void gather_tall(int i, const T* __restrict__ px,
     __syncthreads();                      // red is reused by the next cell
 }
 
+// A tall cell of at most kTallTeamBins bins, gathered by the kTallTeam
+// threads of one team (lane: index in the team; every lane calls it for the
+// same cell): the bins strided over the team, float64 partial sums reduced
+// by shuffles within the team in a fixed order.  Returns false (nothing
+// written) for a larger cell, which the whole workgroup then gathers.
+constexpr int kTallTeam = 16;
+constexpr long long kTallTeamBins = 256;
+
+template <typename T>
+__device__ __forceinline__ bool gather_tall_team(int i, int lane, const T* __restrict__ px,
+                                                 const T* __restrict__ py,
+                                                 const T* __restrict__ sx,
+                                                 const T* __restrict__ sy, const Grid& g,
+                                                 const T* __restrict__ fx,
+                                                 const T* __restrict__ fy,
+                                                 T* __restrict__ gx, T* __restrict__ gy)
+{
+    CellSpan c;
+    const bool ok = load_span(px, py, sx, sy, i, g, c);     // same for the team
+    if (ok && (long long)(c.bxh - c.bxl + 1) * (c.byh - c.byl + 1) > kTallTeamBins)
+        return false;
+    double ax = 0.0, ay = 0.0;
+    if (ok) {
+        const int ny1 = c.byh - c.byl + 1;
+        const int nb = (c.bxh - c.bxl + 1) * ny1;
+        for (int e = lane; e < nb; e += kTallTeam) {
+            const int k = c.bxl + e / ny1, q = c.byl + e % ny1;
+            const double tx = overlap_1d(c.x, c.w, g.xl, g.bsx, k);
+            const double ty = overlap_1d(c.y, c.h, g.yl, g.bsy, q);
+            const double a = tx * ty;
+            if (a > 0.0) {
+                const size_t gi = (size_t)k * g.N + q;
+                ax += a * (double)fx[gi];
+                ay += a * (double)fy[gi];
+            }
+        }
+    }
+#pragma unroll
+    for (int m = kTallTeam / 2; m > 0; m >>= 1) {
+        ax += __shfl_xor(ax, m, kTallTeam);
+        ay += __shfl_xor(ay, m, kTallTeam);
+    }
+    if (lane == 0) {
+        const double rat = ok ? c.ratio() : 0.0;
+        gx[i] = ok ? (T)(ax * rat) : (T)0;
+        gy[i] = ok ? (T)(ay * rat) : (T)0;
+    }
+    return true;
+}
+
 // One workgroup per K3 block of kCellsPerGroup cells (same cell-to-thread
 // map): the records of a block sit in one short run per strip, so the
 // block's partials are read by one CU while they are still in its caches.
+// Tall cells: a team of kTallTeam threads per cell of at most kTallTeamBins
+// bins, larger ones one at a time by the whole workgroup.
 template <typename T>
 __global__ __launch_bounds__(kBinThreads) void k_gather_out(
     const T* __restrict__ px, const T* __restrict__ py,
@@ -954,9 +1031,11 @@ __global__ __launch_bounds__(kBinThreads) void k_gather_out(
     extern __shared__ __align__(16) unsigned char smem[];
     unsigned* ntall = reinterpret_cast<unsigned*>(smem);
     unsigned* list = ntall + 1;
+    unsigned* large = list + kCellsPerGroup;
     double* red = reinterpret_cast<double*>(
-        smem + ((1 + kCellsPerGroup) * sizeof(unsigned) + 15) / 16 * 16);
+        smem + ((1 + kCellsPerGroup + kCellsPerGroup / 32) * sizeof(unsigned) + 15) / 16 * 16);
     if (threadIdx.x == 0) *ntall = 0u;
+    if (threadIdx.x < kCellsPerGroup / 32) large[threadIdx.x] = 0u;
     __syncthreads();
     const int c0 = blockIdx.x * kCellsPerGroup + threadIdx.x;
     const vec2_t<T>* res = reinterpret_cast<const vec2_t<T>*>(b.gtmp);
@@ -987,8 +1066,19 @@ __global__ __launch_bounds__(kBinThreads) void k_gather_out(
     }
     __syncthreads();
     const unsigned n = *ntall;                // uniform across the group
-    for (unsigned t = 0; t < n; ++t)
-        gather_tall<T>((int)list[t], px, py, sx, sy, g, fx, fy, red, gx, gy);
+    if (n == 0u) return;
+    // one team per tall cell; a team's lane 0 marks the cells too large for
+    // it, which the whole workgroup gathers afterwards
+    constexpr int kTeams = kBinThreads / kTallTeam;
+    const int team = threadIdx.x / kTallTeam, lane = threadIdx.x % kTallTeam;
+    for (unsigned t = team; t < n; t += kTeams)
+        if (!gather_tall_team<T>((int)list[t], lane, px, py, sx, sy, g, fx, fy, gx, gy) &&
+            lane == 0)
+            atomicOr(&large[t >> 5], 1u << (t & 31u));
+    __syncthreads();
+    for (unsigned t = 0; t < n; ++t)          // uniform across the group
+        if ((large[t >> 5] >> (t & 31u)) & 1u)
+            gather_tall<T>((int)list[t], px, py, sx, sy, g, fx, fy, red, gx, gy);
 }
 
 }  // namespace dpep

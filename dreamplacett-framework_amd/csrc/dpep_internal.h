@@ -50,6 +50,8 @@ constexpr int kCellsPerGroup = kBinThreads * kCellsPerThread;
 constexpr int kAccThreads = 1024;      // K4 workgroup size
 constexpr int kCountSlots = 8;         // strip-total counters per strip
 constexpr int kMaxSpanY = 4095;        // larger y spans take the tall path
+constexpr int kSideBits = 128;         // column blocks tracked per strip in B
+constexpr int kSideWords = kSideBits / 32;
 
 // Chunk sizes a step may choose for K4 / G1 work items: kChunkMin << k.
 constexpr int kChunkMin = 1024;
@@ -78,8 +80,9 @@ struct BinArgs {
     unsigned long long* pos;   // [nc_max] records of cell i: first strip (or
                                // kPosTall / kPosNone) | second strip << 32
     void* gtmp;             // [2 nc_max] vec2 forces in record order
-    unsigned* bigflag;      // [2S] per strip: 1 + highest, N - lowest column
-                            // of its rows in B (0: none; zero between steps)
+    unsigned* bigflag;      // [kSideWords S] per strip: bitmap of the column
+                            // blocks of its rows that hold tall-cell sums in B
+                            // (zero between steps)
     void* B;                // [M*N] uint64, zero between steps: tall cells and
                             // the chunks of split strips add into it
 };

@@ -11,6 +11,7 @@
 #include <functional>
 #include <random>
 #include <thread>
+#include <memory>
 #include <vector>
 
 #include "dpep_bin.h"
@@ -33,10 +34,26 @@ int oracle_gather(const double*, const double*, const double*, const double*, lo
                   double*);
 }
 
+// shuffle groups of the current launch (the only width the kernels use)
+static constexpr int kEmuShflWidth = 16;
+static std::vector<std::unique_ptr<std::barrier<>>> emu_groups;
+double emu_shfl_slot[1024];
+std::barrier<>* emu_group_barrier(unsigned group, int width)
+{
+    if (width != kEmuShflWidth || group >= emu_groups.size()) {
+        fprintf(stderr, "shuffle width %d / group %u not emulated\n", width, group);
+        abort();
+    }
+    return emu_groups[group].get();
+}
+
 static void launch(unsigned grid, unsigned block, size_t shm, const std::function<void()>& body)
 {
     blockDim = dim3(block);
     gridDim = dim3(grid);
+    emu_groups.clear();
+    for (unsigned q = 0; q < block / kEmuShflWidth; ++q)
+        emu_groups.push_back(std::make_unique<std::barrier<>>(kEmuShflWidth));
     if (shm > sizeof(dpep::smem)) { fprintf(stderr, "LDS %zu too big\n", shm); abort(); }
     // One OS thread per GPU thread of a block, created once per launch; the
     // blocks run one after another, fenced by barriers, with the LDS
@@ -153,10 +170,10 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     memset(b.done, 0, p.S * sizeof(unsigned));
     b.pos = exact<unsigned long long>(nc > 0 ? nc : 1);
     b.gtmp = exact<vec2_t<T>>(p.cap);
-    b.bigflag = exact<unsigned>(2 * p.S);
+    b.bigflag = exact<unsigned>(kSideWords * p.S);
     b.B = malloc(mn * 8);
     memset(b.B, 0, mn * 8);
-    memset(b.bigflag, 0, 2 * p.S * sizeof(unsigned));
+    memset(b.bigflag, 0, kSideWords * p.S * sizeof(unsigned));
     const size_t hist = (size_t)p.S * sizeof(unsigned);
     for (int rep = 0; rep < 2; ++rep) {   // two steps: B / flags must be clean again
         launch(b.G1, kBinThreads, hist, [&] { k_bin_count<T>(px, py, sx, sy, nc, g, b); });
@@ -167,7 +184,7 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
                [&] { k_strip_acc<T, LN>(g, b, a, d0n, dens, Tt); });
         for (int s2 = 0; s2 < p.S; ++s2)
             if (b.done[s2]) { fprintf(stderr, "strip chunk counter left set\n"); return 4; }
-        for (int s2 = 0; s2 < 2 * p.S; ++s2)
+        for (int s2 = 0; s2 < kSideWords * p.S; ++s2)
             if (b.bigflag[s2]) { fprintf(stderr, "bigflag left set\n"); return 4; }
         for (int s2 = 0; s2 < kCountSlots * p.S; ++s2)
             if (b.xtot[s2]) { fprintf(stderr, "slot totals left set\n"); return 4; }

@@ -44,6 +44,21 @@ extern dim3 blockDim, gridDim;
 extern std::barrier<>* emu_barrier;
 inline void __syncthreads() { emu_barrier->arrive_and_wait(); }
 inline void __threadfence() { std::atomic_thread_fence(std::memory_order_seq_cst); }
+// __shfl_xor within groups of `width` lanes.  Every lane of a group calls it
+// together (on the GPU the group runs in lockstep); here the lanes exchange
+// values through one slot each, between two waits on the group's barrier.
+extern std::barrier<>* emu_group_barrier(unsigned group, int width);
+extern double emu_shfl_slot[1024];
+inline double __shfl_xor(double v, int mask, int width)
+{
+    const unsigned t = threadIdx.x, first = t - t % (unsigned)width;
+    std::barrier<>& b = *emu_group_barrier(first / (unsigned)width, width);
+    emu_shfl_slot[t] = v;
+    b.arrive_and_wait();
+    const double r = emu_shfl_slot[first + ((t - first) ^ (unsigned)mask) % (unsigned)width];
+    b.arrive_and_wait();
+    return r;
+}
 // __hip_atomic_load is a clang builtin, available to host code as well
 #ifndef __HIP_MEMORY_SCOPE_AGENT
 #define __HIP_MEMORY_SCOPE_AGENT 3
@@ -91,6 +106,10 @@ inline unsigned atomicMax(unsigned* p, unsigned v)
     while (o < v && !r.compare_exchange_weak(o, v)) {
     }
     return o;
+}
+inline unsigned atomicOr(unsigned* p, unsigned v)
+{
+    return std::atomic_ref<unsigned>(*p).fetch_or(v);
 }
 inline float atomicAdd(float* p, float v) { return unsafeAtomicAdd(p, v); }
 inline double atomicAdd(double* p, double v) { return unsafeAtomicAdd(p, v); }

@@ -167,6 +167,34 @@ def test_edge_cells(oracle):
     assert out["grad_x"][0] == 0 and out["grad_x"][1] == 0 and out["grad_x"][2] == 0
 
 
+@pytest.mark.parametrize("grid", [512, 4096])
+def test_tall_cells(oracle, grid):
+    """Cells wider than a strip take the side map B: small ones (<= 256 bins)
+    are gathered by one thread, larger ones by the whole workgroup, and each
+    strip folds only the column blocks its tall cells marked.  Two steps on
+    one context: the marks must be cleared by the first."""
+    import dpep
+    from dpep import workloads
+    w = workloads.small(4, seed=12, cells=20000, grid=grid)
+    px, py, sx, sy = [a.copy() for a in w.cells(np.float32)]
+    rng = np.random.default_rng(12)
+    sel = rng.choice(w.nc, w.nc // 10, replace=False)
+    sx[sel] = (w.bsx * rng.uniform(4.5, 40.0, sel.size)).astype(np.float32)     # small tall
+    big = sel[:8]
+    sx[big] = np.float32(300 * w.bsx)                                         # > 256 bins
+    sy[big] = np.float32(3 * w.bsy)
+    px[sel] = np.minimum(px[sel], np.float32(w.xh - sx[sel]))
+    cells = (px, py, sx, sy)
+    ref = run_oracle(oracle, w, cells=cells)
+    with dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh) as ctx:
+        ctx.set_initial_density(w.d0n.astype(np.float32))
+        first = ctx.step(*cells)
+        check(first, ref, np.float32, f"tall {grid} step 1")
+        second = ctx.step(*cells)
+    for k in first:
+        assert np.array_equal(first[k], second[k]), k
+
+
 def test_no_cells_and_shrinking_cell_count(oracle):
     import dpep
     from dpep import workloads
