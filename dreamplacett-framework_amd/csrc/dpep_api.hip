@@ -313,7 +313,7 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
     {
         int R = 8;   // rows per strip, as the binning plan sizes them
         while (R > 1 && (size_t)R * N * 8 > kTileBytes) R >>= 1;
-        a.tiles.TXT = R > a.tiles.TX ? R : a.tiles.TX;
+        a.tiles.TXT = t_tile_rows(R, a.tiles.TX, a.tiles.TV, c->esz, M);
     }
     a.wu_step = 2.0 * M_PI / M;
     a.wv_step = 2.0 * M_PI / N * (g.bsx / g.bsy);

@@ -18,9 +18,19 @@ int spectral_fpw(int L, int dtype);
 struct Tiles {
     int TX;   // tile extent along x of Ux, Uy (= 2 * F of the length-N passes)
     int TV;   // tile extent along v of T, Ux, Uy (= 2 * F of the length-M pass)
-    int TXT;  // tile extent along x of T: max(TX, rows per strip), so that
-              // the column pass reads whole >= 128-byte tiles
+    int TXT;  // tile extent along x of T: t_tile_rows()
 };
+
+// Rows of one T tile: at least the rows of a strip (the rows P1 writes at
+// once) and TX, doubled until a tile fills a 128-byte cache line (P2 reads
+// whole tiles: a half-line tile costs a second line fetch; at 4096 x 4096
+// float32, 4-row tiles doubled P2's fetched bytes).  At most M.
+inline int t_tile_rows(int R, int TX, int TV, size_t esz, int M)
+{
+    int t = R > TX ? R : TX;
+    while ((size_t)t * TV * esz < 128 && t < M) t *= 2;
+    return t;
+}
 
 struct SpectralArgs {
     int M, N;

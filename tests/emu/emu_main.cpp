@@ -136,7 +136,7 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     SpectralArgs a{};
     a.M = M; a.N = N;
     a.tiles.TX = 2 * fpw<T>(N); a.tiles.TV = 2 * fpw<T>(M);
-    a.tiles.TXT = strip_rows(N) > a.tiles.TX ? strip_rows(N) : a.tiles.TX;
+    a.tiles.TXT = t_tile_rows(strip_rows(N), a.tiles.TX, a.tiles.TV, sizeof(T), M);
     a.wu_step = 2 * M_PI / M; a.wv_step = 2 * M_PI / N * (g.bsx / g.bsy);
     a.potential = pot; a.twM = d_twM; a.postM = d_poM; a.twN = d_twN; a.postN = d_poN;
 
