@@ -355,8 +355,8 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
         HIP_TRY(hipMalloc((void**)&b.strip_off, (size_t)(p.S + 1) * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.nch, (size_t)p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.item_start, (size_t)p.S * sizeof(unsigned)));
-        HIP_TRY(hipMalloc((void**)&b.items, (size_t)b.Wacc * sizeof(unsigned)));
-        HIP_TRY(hipMalloc((void**)&b.items_g, (size_t)b.Wgat * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.items, (size_t)b.Wacc * sizeof(uint4)));
+        HIP_TRY(hipMalloc((void**)&b.items_g, (size_t)b.Wgat * sizeof(uint4)));
         HIP_TRY(hipMalloc((void**)&b.nitems, 2 * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.chunk, 2 * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.done, (size_t)p.S * sizeof(unsigned)));

@@ -249,6 +249,7 @@ __device__ __forceinline__ void strip_offsets(const BinArgs& b, unsigned* cur,
     for (int s = r0; s < r1; ++s) run += tot[s];
     unsigned total;
     unsigned base = block_exclusive_scan(run, tmp, total);
+    const unsigned base0 = base;              // offset of strip r0
     const bool pub = blockIdx.x == 0;         // uniform across the group
     for (int s = r0; s < r1; ++s) {
         const unsigned t = tot[s];
@@ -299,10 +300,12 @@ __device__ __forceinline__ void strip_offsets(const BinArgs& b, unsigned* cur,
         b.chunk[0] = cha;
         b.chunk[1] = chg;
     }
-    // work items (strip, chunk) of K4, then of G1
+    // work items (strip, chunk) of K4, then of G1: {strip | chunk << 16,
+    // first record, end record, chunks of the strip}, so a workgroup has its
+    // record range from one load
     for (int list = 0; list < 2; ++list) {
         const unsigned ch = list == 0 ? cha : chg;
-        unsigned* items = list == 0 ? b.items : b.items_g;
+        uint4* items = list == 0 ? b.items : b.items_g;
         const unsigned W = (unsigned)(list == 0 ? b.Wacc : b.Wgat);
         unsigned nrun = 0u;
         for (int s = r0; s < r1; ++s) {
@@ -311,16 +314,21 @@ __device__ __forceinline__ void strip_offsets(const BinArgs& b, unsigned* cur,
         }
         unsigned ntotal;
         unsigned ibase = block_exclusive_scan(nrun, tmp, ntotal);
+        unsigned off = base0;
         for (int s = r0; s < r1; ++s) {
-            unsigned n = (tot[s] + ch - 1u) / ch;
+            const unsigned t = tot[s];
+            unsigned n = (t + ch - 1u) / ch;
             n = n > 1u ? n : 1u;
             if (list == 0) {
                 b.nch[s] = n;
                 b.item_start[s] = ibase;
             }
             for (unsigned c = 0; c < n; ++c)
-                if (ibase + c < W) items[ibase + c] = (unsigned)s | (c << 16);
+                if (ibase + c < W)
+                    items[ibase + c] = uint4{(unsigned)s | (c << 16), off + c * ch,
+                                             off + min((c + 1u) * ch, t), n};
             ibase += n;
+            off += t;
         }
         if (tid == 0) b.nitems[list] = ntotal < W ? ntotal : W;
     }
@@ -498,17 +506,13 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     if (w == 0)   // K3 has read the slot totals: zero them for the next step
         for (int e = threadIdx.x; e < kCountSlots * b.S; e += kAccThreads) b.xtot[e] = 0u;
     if (w >= (int)b.nitems[0]) return;          // uniform across the group
-    const unsigned item = b.items[w];
-    const int s = (int)(item & 0xFFFFu);
-    const int chunk = (int)(item >> 16);
+    const uint4 item = b.items[w];
+    const int s = (int)(item.x & 0xFFFFu);
     const int tid = threadIdx.x;
     const int k0 = s * R, k1 = k0 + R - 1;
-    const unsigned n = b.nch[s];
-    const unsigned CH = b.chunk[0];
+    const unsigned n = item.w;                  // chunks of this strip
     unsigned* last_flag = reinterpret_cast<unsigned*>(tile + RN);   // LDS word
-    const unsigned e0 = b.strip_off[s] + (unsigned)chunk * CH;
-    const unsigned eend = b.strip_off[s + 1];
-    const unsigned e1 = min(e0 + CH, eend);
+    const unsigned e0 = item.y, e1 = item.z;    // this chunk's records
     const vec4_t<T>* recg = reinterpret_cast<const vec4_t<T>*>(b.recg);
     const T fs = (T)g.fix_scale;
     // one record per thread per pass, the next one's loads in flight while
@@ -741,18 +745,15 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
     extern __shared__ __align__(16) unsigned char smem[];
     const int w = blockIdx.x;
     if (w >= (int)b.nitems[1]) return;          // uniform across the group
-    const unsigned item = b.items_g[w];
-    const int s = (int)(item & 0xFFFFu);
-    const int chunk = (int)(item >> 16);
+    const uint4 item = b.items_g[w];
+    const int s = (int)(item.x & 0xFFFFu);
     const int tid = threadIdx.x;
     const int R = b.R, N = g.N;
-    const unsigned CH = b.chunk[1];
     const int RG = gather_rows<T>(R, N);
     const int k0 = s * R;
     // both fields of a bin side by side: one 2-element LDS read per bin
     vec2_t<T>* lf = reinterpret_cast<vec2_t<T>*>(smem);
-    const unsigned e0 = b.strip_off[s] + (unsigned)chunk * CH;
-    const unsigned e1 = min(e0 + CH, b.strip_off[s + 1]);
+    const unsigned e0 = item.y, e1 = item.z;    // this item's records
     const vec4_t<T>* recg = reinterpret_cast<const vec4_t<T>*>(b.recg);
     vec2_t<T>* out = reinterpret_cast<vec2_t<T>*>(b.gtmp);
     const T ba = (T)(g.bsx * g.bsy);

@@ -81,9 +81,10 @@ struct BinArgs {
     unsigned* chunk;        // [2] records per K4 / G1 item, chosen per step
     unsigned* nch;          // [S] K4 chunks per strip
     unsigned* item_start;   // [S] first K4 work item of each strip
-    unsigned* items;        // [Wacc] K4 items: strip | chunk << 16
+    uint4* items;           // [Wacc] K4 items: {strip | chunk << 16, first
+                            // record, end record, chunks of the strip}
     unsigned* nitems;       // [2] K4, G1 item counts
-    unsigned* items_g;      // [Wgat] G1 items
+    uint4* items_g;         // [Wgat] G1 items (same layout)
     unsigned* done;         // [S] K4 chunks done per strip (zero between steps)
     void* recg;             // [2 nc_max] record geometry, vec4 of T
     unsigned* recm;         // [2 nc_max] record span word

@@ -159,8 +159,8 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     b.strip_off = exact<unsigned>(p.S + 1);
     b.nch = exact<unsigned>(p.S);
     b.item_start = exact<unsigned>(p.S);
-    b.items = exact<unsigned>(b.Wacc);
-    b.items_g = exact<unsigned>(b.Wgat);
+    b.items = exact<uint4>(b.Wacc);
+    b.items_g = exact<uint4>(b.Wgat);
     b.nitems = exact<unsigned>(2);
     b.chunk = exact<unsigned>(2);
     if (sizeof(vec4_t<T>) != p.geo_bytes) { fprintf(stderr, "record size mismatch\n"); return 4; }
