@@ -65,11 +65,15 @@ def pmc_traffic(key):
     names = (names,) if isinstance(names, str) else names
     total = 0.0
     found = 0
+    col = None                       # index of the "HBM traffic MB" column
     with open(PMC_SUMMARY) as f:
         for line in f:
             cols = [c.strip() for c in line.strip().strip("|").split("|")]
-            if len(cols) >= 9 and any(cols[0].startswith(n + "<") for n in names):
-                total += float(cols[8]) * 1e6
+            if col is None and "HBM traffic MB" in cols:
+                col = cols.index("HBM traffic MB")
+            elif (col is not None and len(cols) > col and
+                  any(cols[0].startswith(n + "<") for n in names)):
+                total += float(cols[col]) * 1e6
                 found += 1
     return round(total) if found == len(names) else None
 
@@ -84,6 +88,16 @@ def step_bytes(nc, M, N, esz, potential=True):
     (Up = Uy / w_v) and the density is not re-read, so the 3-pass model's
     64 MN is not what this step has to move."""
     return 10 * esz * nc + (13 if potential else 12) * esz * M * N
+
+
+def step_bytes_3pass(nc, M, N, esz, potential=True):
+    """The 3-pass row-column byte model of the step: 10 e Nc + 16 e MN
+    (40 Nc + 64 MN at float32; 3 e MN less without the potential).
+    Beyond step_bytes() it counts a separate row pass that re-reads rho and
+    a round trip of the potential's pre-image Up, which this step does not
+    make; reported beside it because the step's % of HBM peak is quoted on
+    this model."""
+    return 10 * esz * nc + (16 if potential else 13) * esz * M * N
 
 
 def cpu_baseline(w, seconds, max_steps=400):
@@ -228,6 +242,8 @@ def main():
         },
         "hbm_fraction_step": round(bstep / (ms * 1e-3) / HBM_PEAK, 4),
         "step_bytes": bstep,
+        "hbm_fraction_3pass_model": round(
+            step_bytes_3pass(w.nc, w.M, w.N, esz, potential) / (ms * 1e-3) / HBM_PEAK, 4),
         "roofline": roof,
         "kernel_us": {k: round(v, 2) for k, v in kt.items()} if kt else None,
         "host_step_ms": round(host_ms, 3) if host_ms else None,

@@ -19,3 +19,19 @@ def test_cpu_baseline_matches_oracle(oracle):
         assert rel_l2(got[k], ref[k]) < 1e-3, k
     assert set(got["stage_ms"]) == {"scatter", "solve", "gather"}
     cb.close()
+
+
+def test_bench_reads_every_kernel_from_the_committed_profile():
+    """bench.py's roofline takes each kernel's HBM traffic from the committed
+    rocprofv3 summary of the headline workload and its algorithmic bytes from
+    the byte model: both must cover every kernel the events time."""
+    import bench
+    import dpep
+    kb = bench.kernel_bytes(1100000, 2048, 2048, 4)
+    keys = [k for k in dpep.KERNEL_KEYS if k != "step"]
+    assert set(kb) == set(keys) == set(bench.PMC_NAMES)
+    for k in keys:
+        t = bench.pmc_traffic(k)
+        assert t is not None and t >= 0.9 * kb[k], k   # HBM traffic covers the algorithmic bytes
+    # the step's byte model: 40 Nc + 52 MN at float32 with the potential
+    assert bench.step_bytes(1100000, 2048, 2048, 4) == 40 * 1100000 + 52 * 2048 * 2048
