@@ -41,9 +41,10 @@
 //
 // A cell whose span covers more than R rows or more than kMaxSpanY + 1
 // columns ("tall") skips the sort: K3 adds it with global atomics into the
-// side map B (zero between steps), records the column range it touches in
-// each of its strips, and K4 folds and re-zeroes those columns of B.  Every other cell touches at most two
-// strips, so the record arrays hold 2*nc_max.
+// side map B (zero between steps) and marks the column blocks it touches in
+// each of its strips; K4 folds and re-zeroes those blocks of B, and G2
+// gathers the cell with a team of threads.  Every other cell touches at most
+// two strips, so the record arrays hold 2*nc_max.
 #pragma once
 
 #include <type_traits>
