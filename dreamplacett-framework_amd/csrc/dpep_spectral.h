@@ -49,11 +49,21 @@ namespace dpep {
 
 // FFTs held by one workgroup of the length-L passes.  Two at L = 2048 (not
 // four): twice the workgroups, two of them per CU, measured 2-3 us faster
-// per pass at 2048 x 2048.
+// per pass at 2048 x 2048.  Two at L <= 512 as well (with 8 elements per
+// thread, below): a 512-point pass has only N / 2F workgroups to spread
+// over the CUs.
 template <typename T>
 __host__ __device__ constexpr int fpw(int L)
 {
-    return sizeof(T) == 4 ? (L <= 1024 ? 4 : 2) : 2;
+    return sizeof(T) == 4 ? ((L <= 1024 && L > 512) ? 4 : 2) : 2;
+}
+
+// Elements per thread of the float32 passes at L <= 512: 8, so each FFT has
+// twice the threads (the passes are latency-bound at these sizes).
+template <typename T>
+__host__ __device__ constexpr int small_e(int L)
+{
+    return (sizeof(T) == 4 && L <= 512 && L >= 8) ? 8 : fft_e(L);
 }
 
 // Elements per thread of the FFTs of the column pass (P2) and of the row
@@ -63,13 +73,13 @@ __host__ __device__ constexpr int fpw(int L)
 template <typename T>
 __host__ __device__ constexpr int col_e(int L)
 {
-    return fft_e(L);
+    return small_e<T>(L);
 }
 
 template <typename T>
 __host__ __device__ constexpr int row_e(int L)
 {
-    return fft_e(L);
+    return small_e<T>(L);
 }
 
 template <typename T>
