@@ -58,12 +58,12 @@ __host__ __device__ constexpr int fpw(int L)
     return sizeof(T) == 4 ? ((L <= 1024 && L > 512) ? 4 : 2) : 2;
 }
 
-// Elements per thread of the float32 passes at L <= 512: 8, so each FFT has
-// twice the threads (the passes are latency-bound at these sizes).
+// Elements per thread of the passes at L <= 512: 8, so each FFT has twice
+// the threads (the passes are latency-bound at these sizes).
 template <typename T>
 __host__ __device__ constexpr int small_e(int L)
 {
-    return (sizeof(T) == 4 && L <= 512 && L >= 8) ? 8 : fft_e(L);
+    return (L <= 512 && L >= 8) ? 8 : fft_e(L);
 }
 
 // Elements per thread of the FFTs of the column pass (P2) and of the row
