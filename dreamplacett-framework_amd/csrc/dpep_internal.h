@@ -66,7 +66,7 @@ constexpr int kSideWords = kSideBits / 32;
 // Chunk sizes a step may choose for K4 / G1 work items: kChunkMin << k.
 constexpr int kChunkMin = 1024;
 constexpr int kChunkCands = 21;        // up to 2^30 records: never splits
-constexpr int kAccChunkMin = 16384;    // smallest K4 chunk a step chooses
+constexpr int kAccChunkMin = 8192;     // smallest K4 chunk a step chooses
 
 // Shared between host (sizing) and device.
 struct BinArgs {
