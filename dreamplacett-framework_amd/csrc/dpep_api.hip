@@ -53,6 +53,10 @@ int fail(int code, const char* fmt, ...)
 // pass, row inverse, gather
 constexpr int kNumStages = 7;
 
+// the context's output buffers, for the validity mask
+constexpr unsigned kOutDensity = 1u, kOutPotential = 2u, kOutFx = 4u, kOutFy = 8u,
+                   kOutGx = 16u, kOutGy = 32u, kOutRaw = 64u;
+
 bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
 }  // namespace
@@ -68,6 +72,7 @@ struct dpep_ctx {
     void *d_d0n = nullptr, *d_density = nullptr, *d_potential = nullptr;
     void *d_fx = nullptr, *d_fy = nullptr, *d_gx = nullptr, *d_gy = nullptr;
     void *d_T = nullptr, *d_Ux = nullptr, *d_Uy = nullptr;
+    void* d_raw = nullptr;       // scatter density without D0 (DPEP_FLAG_SCATTER_DENSITY)
     BinPlan plan{};
     BinArgs bins{};
     void *d_twM = nullptr, *d_postM = nullptr, *d_twN = nullptr,
@@ -83,6 +88,10 @@ struct dpep_ctx {
     int nc = -1;                 // resident cells (-1: none uploaded)
     int last_nc = 0;             // cells of the last computed step
     int stepped = 0;
+    // which of the context's own output buffers hold the last step's results
+    // (kOut* bits): a step on caller-owned outputs leaves the others stale,
+    // and new cells uploaded after the step make every output stale
+    unsigned valid = 0;
     float h2d_ms = 0.f, d2h_den_ms = 0.f, d2h_out_ms = 0.f;
 };
 
@@ -95,43 +104,18 @@ static int check_ctx(const dpep_ctx* c)
     return DPEP_OK;
 }
 
+// Twiddle tables on the device (the kernel the no-alloc entry point runs
+// too, so both paths use bitwise the same tables).
 template <typename T>
-static std::vector<T> twiddles(int L)
+static int make_tables(dpep_ctx* c)
 {
-    std::vector<T> v(2 * (size_t)L);
-    for (int m = 0; m < L; ++m) {
-        const double a = 2.0 * M_PI * (double)m / (double)L;
-        v[2 * m] = (T)cos(a);
-        v[2 * m + 1] = (T)-sin(a);
-    }
-    return v;
-}
-
-template <typename T>
-static std::vector<T> post_twiddles(int L)
-{
-    std::vector<T> v(2 * (size_t)(L / 2 + 1));
-    for (int k = 0; k <= L / 2; ++k) {
-        const double a = M_PI * (double)k / (2.0 * (double)L);
-        v[2 * k] = (T)cos(a);
-        v[2 * k + 1] = (T)-sin(a);
-    }
-    return v;
-}
-
-template <typename T>
-static int upload_tables(dpep_ctx* c)
-{
-    auto twM = twiddles<T>(c->M), twN = twiddles<T>(c->N);
-    auto poM = post_twiddles<T>(c->M), poN = post_twiddles<T>(c->N);
-    HIP_TRY(hipMalloc(&c->d_twM, twM.size() * sizeof(T)));
-    HIP_TRY(hipMalloc(&c->d_twN, twN.size() * sizeof(T)));
-    HIP_TRY(hipMalloc(&c->d_postM, poM.size() * sizeof(T)));
-    HIP_TRY(hipMalloc(&c->d_postN, poN.size() * sizeof(T)));
-    HIP_TRY(hipMemcpy(c->d_twM, twM.data(), twM.size() * sizeof(T), hipMemcpyHostToDevice));
-    HIP_TRY(hipMemcpy(c->d_twN, twN.data(), twN.size() * sizeof(T), hipMemcpyHostToDevice));
-    HIP_TRY(hipMemcpy(c->d_postM, poM.data(), poM.size() * sizeof(T), hipMemcpyHostToDevice));
-    HIP_TRY(hipMemcpy(c->d_postN, poN.data(), poN.size() * sizeof(T), hipMemcpyHostToDevice));
+    HIP_TRY(hipMalloc(&c->d_twM, twiddle_elems(c->M) * sizeof(T)));
+    HIP_TRY(hipMalloc(&c->d_twN, twiddle_elems(c->N) * sizeof(T)));
+    HIP_TRY(hipMalloc(&c->d_postM, post_elems(c->M) * sizeof(T)));
+    HIP_TRY(hipMalloc(&c->d_postN, post_elems(c->N) * sizeof(T)));
+    HIP_TRY(launch_tables<T>(c->M, (T*)c->d_twM, (T*)c->d_postM, c->stream));
+    HIP_TRY(launch_tables<T>(c->N, (T*)c->d_twN, (T*)c->d_postN, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
     c->sargs.twM = c->d_twM;
     c->sargs.postM = c->d_postM;
     c->sargs.twN = c->d_twN;
@@ -148,7 +132,7 @@ static void release(dpep_ctx* c)
                     c->d_postM, c->d_twN, c->d_postN, b.cnt, b.xtot, b.strip_off,
                     b.nch, b.item_start, b.items, b.nitems, b.done, b.recg,
                     b.recm, b.pos, b.gtmp,
-                    b.bigflag, b.B, b.chunk, b.items_g};
+                    b.bigflag, b.B, b.chunk, b.items_g, c->d_raw};
     for (void* p : bufs)
         if (p) (void)hipFree(p);
     for (auto& e : c->ev)
@@ -221,21 +205,27 @@ static int step_dispatch(dpep_ctx* c, const void* px, const void* py,
                          void* fy, void* dens, void* phi, void* gx, void* gy,
                          hipStream_t s)
 {
-    if (!fx) fx = c->d_fx;
-    if (!fy) fy = c->d_fy;
-    if (!dens) dens = c->d_density;
-    if (!phi) phi = c->d_potential;
-    if (!gx) gx = c->d_gx;
-    if (!gy) gy = c->d_gy;
+    // outputs the caller does not supply land in the context's buffers
+    unsigned valid = kOutRaw;
+    if (!fx) { fx = c->d_fx; valid |= kOutFx; }
+    if (!fy) { fy = c->d_fy; valid |= kOutFy; }
+    if (!dens) { dens = c->d_density; valid |= kOutDensity; }
+    if (!phi) { phi = c->d_potential; valid |= kOutPotential; }
+    if (!gx) { gx = c->d_gx; valid |= kOutGx; }
+    if (!gy) { gy = c->d_gy; valid |= kOutGy; }
+    int rc;
     if (c->dtype == DPEP_DTYPE_F32)
-        return run_step<float>(c, (const float*)px, (const float*)py,
-                               (const float*)sx, (const float*)sy, nc,
-                               (float*)fx, (float*)fy, (float*)dens,
-                               (float*)phi, (float*)gx, (float*)gy, s);
-    return run_step<double>(c, (const double*)px, (const double*)py,
-                            (const double*)sx, (const double*)sy, nc,
-                            (double*)fx, (double*)fy, (double*)dens,
-                            (double*)phi, (double*)gx, (double*)gy, s);
+        rc = run_step<float>(c, (const float*)px, (const float*)py,
+                             (const float*)sx, (const float*)sy, nc,
+                             (float*)fx, (float*)fy, (float*)dens,
+                             (float*)phi, (float*)gx, (float*)gy, s);
+    else
+        rc = run_step<double>(c, (const double*)px, (const double*)py,
+                              (const double*)sx, (const double*)sy, nc,
+                              (double*)fx, (double*)fy, (double*)dens,
+                              (double*)phi, (double*)gx, (double*)gy, s);
+    c->valid = rc == DPEP_OK ? valid : 0u;
+    return rc;
 }
 
 static float elapsed(hipEvent_t a, hipEvent_t b)
@@ -243,6 +233,23 @@ static float elapsed(hipEvent_t a, hipEvent_t b)
     float ms = 0.f;
     if (hipEventElapsedTime(&ms, a, b) != hipSuccess) return 0.f;
     return ms;
+}
+
+int dpep::report_error(int code, const char* msg)
+{
+    g_last_error = msg;
+    return code;
+}
+
+hipError_t dpep::prepare_kernels()
+{
+    static std::once_flag once;
+    static hipError_t err = hipSuccess;
+    std::call_once(once, [] {
+        err = spectral_prepare();
+        if (err == hipSuccess) err = bin_prepare();
+    });
+    return err;
 }
 
 // ---------------------------------------------------------------------------
@@ -254,7 +261,7 @@ int dpep_abi_version(void) { return DPEP_ABI_VERSION; }
 
 const char* dpep_build_info(void)
 {
-    return "dpep abi 1; HIP kernels for gfx950; scatter/P1/P2/P3/gather";
+    return "dpep abi 3; HIP kernels for gfx950; scatter/P1/P2/P3/gather";
 }
 
 const char* dpep_last_error(void) { return g_last_error.c_str(); }
@@ -277,47 +284,21 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
         return fail(DPEP_ERR_ARG, "die [%g,%g]x[%g,%g] is empty or not finite",
                     xl, xh, yl, yh);
     if (flags & ~(DPEP_FLAG_DETERMINISTIC | DPEP_FLAG_NO_POTENTIAL |
-                  DPEP_FLAG_NO_STRETCH | DPEP_FLAG_NO_GATHER | DPEP_FLAG_STEP_TIMINGS))
+                  DPEP_FLAG_NO_STRETCH | DPEP_FLAG_NO_GATHER | DPEP_FLAG_STEP_TIMINGS |
+                  DPEP_FLAG_SCATTER_DENSITY))
         return fail(DPEP_ERR_ARG, "unknown flag bits 0x%x", flags);
 
-    static std::once_flag once;
-    static hipError_t prep_err = hipSuccess;
-    std::call_once(once, [] {
-        prep_err = spectral_prepare();
-        if (prep_err == hipSuccess) prep_err = bin_prepare();
-    });
-    if (prep_err != hipSuccess)
-        return fail(DPEP_ERR_HIP, "kernel attribute set-up failed: %s",
-                    hipGetErrorString(prep_err));
+    if (const hipError_t e = prepare_kernels())
+        return fail(DPEP_ERR_HIP, "kernel attribute set-up failed: %s", hipGetErrorString(e));
 
     dpep_ctx* c = new (std::nothrow) dpep_ctx();
     if (!c) return fail(DPEP_ERR_NOMEM, "host allocation failed");
     c->M = M; c->N = N; c->nc_max = nc_max; c->dtype = dtype; c->flags = flags;
     c->esz = dtype == DPEP_DTYPE_F32 ? 4 : 8;
-    Grid& g = c->grid;
-    g.M = M; g.N = N; g.xl = xl; g.yl = yl; g.xh = xh; g.yh = yh;
-    g.bsx = (xh - xl) / M;
-    g.bsy = (yh - yl) / N;
-    g.inv_ba = 1.0 / (g.bsx * g.bsy);
-    g.inv_bsx = 1.0 / g.bsx;
-    g.inv_bsy = 1.0 / g.bsy;
-    g.minw = M_SQRT2 * g.bsx;
-    g.minh = M_SQRT2 * g.bsy;
-    g.stretch = (flags & DPEP_FLAG_NO_STRETCH) ? 0 : 1;
-    g.fix_scale = ldexp(1.0, fix_exponent_of(nc_max, (int)c->esz));
-
-    SpectralArgs& a = c->sargs;
-    a.M = M; a.N = N;
-    a.tiles.TX = 2 * spectral_fpw(N, dtype);
-    a.tiles.TV = 2 * spectral_fpw(M, dtype);
-    {
-        int R = 8;   // rows per strip, as the binning plan sizes them
-        while (R > 1 && (size_t)R * N * 8 > kTileBytes) R >>= 1;
-        a.tiles.TXT = t_tile_rows(R, a.tiles.TX, a.tiles.TV, c->esz, M);
-    }
-    a.wu_step = 2.0 * M_PI / M;
-    a.wv_step = 2.0 * M_PI / N * (g.bsx / g.bsy);
-    a.potential = (flags & DPEP_FLAG_NO_POTENTIAL) ? 0 : 1;
+    make_grid(c->grid, M, N, xl, yl, xh, yh, !(flags & DPEP_FLAG_NO_STRETCH), nc_max,
+              (int)c->esz);
+    make_spectral_args(c->sargs, c->grid, dtype, !(flags & DPEP_FLAG_NO_POTENTIAL));
+    const SpectralArgs& a = c->sargs;
 
     int rc = DPEP_OK;
     auto step = [&]() -> int {
@@ -334,6 +315,7 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
                             &c->d_T, &c->d_Ux, &c->d_Uy};
         for (void** p : mapbufs) HIP_TRY(hipMalloc(p, mnb));
         if (a.potential) HIP_TRY(hipMalloc(&c->d_potential, mnb));
+        if (flags & DPEP_FLAG_SCATTER_DENSITY) HIP_TRY(hipMalloc(&c->d_raw, mnb));
         HIP_TRY(hipMemset(c->d_d0n, 0, mnb));
         // strip binning
         const size_t accb = sizeof(unsigned long long);
@@ -341,6 +323,7 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
         p = make_bin_plan(M, N, nc_max, c->esz);
         BinArgs& b = c->bins;
         b.S = p.S; b.R = p.R; b.lgR = p.lgR; b.G1 = 1; b.ch_force = 0;
+        b.raw = c->d_raw;
         {
             int acc = 0, gat = 0, cus = 0;
             HIP_TRY(dtype == DPEP_DTYPE_F32 ? bin_occupancy<float>(N, p.R, acc, gat)
@@ -371,8 +354,7 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
         HIP_TRY(hipMemset(b.B, 0, (size_t)M * N * accb));
         HIP_TRY(hipMemset(b.bigflag, 0, (size_t)kSideWords * p.S * sizeof(unsigned)));
         HIP_TRY(hipDeviceSynchronize());
-        return dtype == DPEP_DTYPE_F32 ? upload_tables<float>(c)
-                                       : upload_tables<double>(c);
+        return dtype == DPEP_DTYPE_F32 ? make_tables<float>(c) : make_tables<double>(c);
     };
     rc = step();
     if (rc != DPEP_OK) {
@@ -471,6 +453,7 @@ int dpep_set_cells(dpep_ctx* c, const void* px, const void* py,
     HIP_TRY(hipEventSynchronize(c->ev_x1));
     c->h2d_ms = elapsed(c->ev_x0, c->ev_x1);
     c->nc = nc;
+    c->valid = 0u;          // the outputs no longer describe the resident cells
     return DPEP_OK;
 }
 
@@ -498,6 +481,16 @@ int dpep_get_outputs(dpep_ctx* c, void* density, void* potential,
         return fail(DPEP_ERR_STATE, "context was created with DPEP_FLAG_NO_POTENTIAL");
     if ((grad_x || grad_y) && (c->flags & DPEP_FLAG_NO_GATHER))
         return fail(DPEP_ERR_STATE, "context was created with DPEP_FLAG_NO_GATHER");
+    {
+        const unsigned want = (density ? kOutDensity : 0u) | (potential ? kOutPotential : 0u) |
+                              (field_x ? kOutFx : 0u) | (field_y ? kOutFy : 0u) |
+                              (grad_x ? kOutGx : 0u) | (grad_y ? kOutGy : 0u);
+        if (want & ~c->valid)
+            return fail(DPEP_ERR_STATE,
+                        "the context's outputs are stale: cells were uploaded after the "
+                        "last step, or the last step wrote to caller-owned device buffers "
+                        "(requested mask 0x%x, valid 0x%x)", want, c->valid);
+    }
     const size_t mnb = (size_t)c->M * c->N * c->esz;
     const size_t ncb = (size_t)c->last_nc * c->esz;
     hipStream_t s = c->stream;
@@ -515,6 +508,40 @@ int dpep_get_outputs(dpep_ctx* c, void* density, void* potential,
     HIP_TRY(hipEventRecord(c->ev_x1, s));
     HIP_TRY(hipEventSynchronize(c->ev_x1));
     c->d2h_out_ms = elapsed(c->ev_x0, c->ev_x1);
+    return DPEP_OK;
+}
+
+int dpep_get_scatter_density(dpep_ctx* c, void* out)
+{
+    if (int rc = check_ctx(c)) return rc;
+    if (!out) return fail(DPEP_ERR_ARG, "out is NULL");
+    if (!c->d_raw)
+        return fail(DPEP_ERR_STATE, "context was created without DPEP_FLAG_SCATTER_DENSITY");
+    if (!c->stepped || !(c->valid & kOutRaw))
+        return fail(DPEP_ERR_STATE, "no step has been computed on the resident cells");
+    HIP_TRY(hipMemcpyAsync(out, c->d_raw, (size_t)c->M * c->N * c->esz,
+                           hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return DPEP_OK;
+}
+
+int dpep_host_alloc(size_t bytes, void** out)
+{
+    if (!out) return fail(DPEP_ERR_ARG, "out is NULL");
+    *out = nullptr;
+    if (bytes == 0) bytes = 1;
+    const hipError_t e = hipHostMalloc(out, bytes, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        *out = nullptr;
+        return fail(DPEP_ERR_NOMEM, "hipHostMalloc(%zu) failed: %s", bytes,
+                    hipGetErrorString(e));
+    }
+    return DPEP_OK;
+}
+
+int dpep_host_free(void* p)
+{
+    if (p) HIP_TRY(hipHostFree(p));
     return DPEP_OK;
 }
 

@@ -574,9 +574,13 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     A* Bm = reinterpret_cast<A*>(b.B);
     if (n > 1u) {
         // A strip split into n chunks: every chunk but the last to finish
-        // adds its tile into the strip's rows of B (device-scope atomics
-        // whose results are awaited, so they are performed before the
-        // ticket is taken; no fence); the last one folds B in its flush.
+        // adds its tile into the strip's rows of B with device-scope atomics;
+        // the last one folds B in its flush.  Ordering: each wave awaits the
+        // results of its own atomics (so they are performed before the
+        // barrier), the barrier orders the waves before thread 0, and thread
+        // 0 takes the strip's ticket with an acquire-release RMW at agent
+        // scope: every chunk's sums happen-before the ticket that follows
+        // them, and the chunk that draws the last ticket reads B after it.
         unsigned long long got = 0ull;
         for (int e = tid; e < RN; e += kAccThreads) {
             const A v = tile[e];
@@ -585,7 +589,10 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
         // never true (sums stay below 2^63); it makes the results live
         if (got >> 63) *last_flag = 0u;
         __syncthreads();
-        if (tid == 0) *last_flag = atomicAdd(&b.done[s], 1u) == n - 1u ? 1u : 0u;
+        if (tid == 0)
+            *last_flag = __hip_atomic_fetch_add(&b.done[s], 1u, __ATOMIC_ACQ_REL,
+                                                __HIP_MEMORY_SCOPE_AGENT) == n - 1u
+                             ? 1u : 0u;
         __syncthreads();
         if (*last_flag == 0u) return;           // uniform across the group
         if (tid == 0) b.done[s] = 0u;
@@ -636,6 +643,17 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
             if (e < RN) {
                 rv[j] = (T)((double)d[j] + (double)v[j] * inv);
                 dens[gbase + e] = rv[j];
+            }
+        }
+        // the cells' own density, before the initial density is added (the
+        // reference server's density read-back, kept for its dump and its
+        // CPU-solve mode); a uniform branch, off unless the context asks
+        if (b.raw) {
+            T* raw = reinterpret_cast<T*>(b.raw);
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const int e = tid + j * kAccThreads;
+                if (e < RN) raw[gbase + e] = (T)((double)v[j] * inv);
             }
         }
     }

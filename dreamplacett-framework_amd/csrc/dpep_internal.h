@@ -3,6 +3,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stdint.h>
 
 #include "dpep_device.h"
@@ -43,6 +44,14 @@ struct SpectralArgs {
     const void* twN;
     const void* postN;
 };
+
+// Twiddle tables of a length-L transform on the device: tw[m] =
+// exp(-2 pi i m / L) for m < L and post[k] = exp(-i pi k / 2L) for k <= L/2,
+// interleaved (re, im) in T, evaluated in float64 (sincospi) and rounded once.
+inline size_t twiddle_elems(int L) { return 2 * (size_t)L; }
+inline size_t post_elems(int L) { return 2 * (size_t)(L / 2 + 1); }
+template <typename T>
+hipError_t launch_tables(int L, T* tw, T* post, hipStream_t s);
 
 // Launchers (return hipError_t of the launch).  T = float or double.
 template <typename T>
@@ -96,7 +105,28 @@ struct BinArgs {
                             // (zero between steps)
     void* B;                // [M*N] uint64, zero between steps: tall cells and
                             // the chunks of split strips add into it
+    void* raw;              // [M*N] of T or null: the scattered cells' density
+                            // alone (no initial density), written by K4's flush
 };
+
+// Geometry of one problem (bins, die, stretch, fixed-point scale) and the
+// spectral passes' arguments (everything but the table pointers), shared by
+// dpep_create and the no-alloc entry point so both compute identically.
+inline void make_grid(Grid& g, int M, int N, double xl, double yl, double xh, double yh,
+                      bool stretch, int nc_max, int esz)
+{
+    g = Grid{};
+    g.M = M; g.N = N; g.xl = xl; g.yl = yl; g.xh = xh; g.yh = yh;
+    g.bsx = (xh - xl) / M;
+    g.bsy = (yh - yl) / N;
+    g.inv_ba = 1.0 / (g.bsx * g.bsy);
+    g.inv_bsx = 1.0 / g.bsx;
+    g.inv_bsy = 1.0 / g.bsy;
+    g.minw = M_SQRT2 * g.bsx;
+    g.minh = M_SQRT2 * g.bsy;
+    g.stretch = stretch ? 1 : 0;
+    g.fix_scale = ldexp(1.0, fix_exponent_of(nc_max, esz));
+}
 
 // Host-side sizing of the binning buffers (shared with the CPU emulator).
 constexpr size_t kTileBytes = 131072;  // LDS tile of K4 (uint64 words) and G1
@@ -122,6 +152,21 @@ inline BinPlan make_bin_plan(int M, int N, int nc_max, size_t elem_bytes)
     p.G1max = (int)((nc + kCellsPerGroup - 1) / kCellsPerGroup);
     p.cap = (size_t)(2 * nc);
     return p;
+}
+
+inline void make_spectral_args(SpectralArgs& a, const Grid& g, int dtype, bool potential)
+{
+    const size_t esz = dtype == 0 ? 4 : 8;
+    a = SpectralArgs{};
+    a.M = g.M; a.N = g.N;
+    a.tiles.TX = 2 * spectral_fpw(g.N, dtype);
+    a.tiles.TV = 2 * spectral_fpw(g.M, dtype);
+    int R = 8;   // rows per strip, as make_bin_plan sizes them
+    while (R > 1 && (size_t)R * g.N * 8 > kTileBytes) R >>= 1;
+    a.tiles.TXT = t_tile_rows(R, a.tiles.TX, a.tiles.TV, esz, g.M);
+    a.wu_step = 2.0 * M_PI / g.M;
+    a.wv_step = 2.0 * M_PI / g.N * (g.bsx / g.bsy);
+    a.potential = potential ? 1 : 0;
 }
 
 // The work-item grids of K4 and G1 from the per-CU occupancy of each (both
@@ -159,8 +204,14 @@ hipError_t launch_fixed_density(const T* px, const T* py, const T* sx, const T* 
 template <typename T>
 hipError_t bin_occupancy(int N, int R, int& acc_per_cu, int& gat_per_cu);
 
-// Sets the dynamic-LDS limits of every spectral / binning kernel (once).
+// Sets the dynamic-LDS limits of every spectral / binning kernel;
+// prepare_kernels() does both once per process (later calls return the
+// first one's status).
 hipError_t spectral_prepare();
 hipError_t bin_prepare();
+hipError_t prepare_kernels();
+
+// Records msg as the calling thread's dpep_last_error() text; returns code.
+int report_error(int code, const char* msg);
 
 }  // namespace dpep

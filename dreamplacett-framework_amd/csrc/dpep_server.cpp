@@ -10,12 +10,22 @@
 // the fields and the 9 timing slots, set DONE; QUIT ends the server.  The
 // device work goes through libdpep.so's C ABI (include/dpep.h).  Version-2
 // shm files (magic in the header padding, see dpep/shm.py) also receive the
-// density, the potential and the per-cell forces.
+// density, the potential and the per-cell forces, as the header's output
+// word asks, and may ask for no fields at all.
 //
-// Environment honoured as in the reference: EXPORT_DENSITY_PATH (density
-// every step, float[M*N]), EXPORT_POS_PATH (positions at steps 1, 50, 100,
-// :1686-1726 format), CPU_DCT=1 (density in the field_x slot, field_y zero,
-// :1785-1788), GATHER_MODE (accepted, no effect).
+// Transfers: the positions are copied from the shm file into page-locked
+// staging buffers (dpep_host_alloc) by a few threads, uploaded from there,
+// and the requested outputs come back the same way; only the slots a step
+// needs cross the link.
+//
+// Environment honoured as in the reference: EXPORT_DENSITY_PATH (the
+// scattered cells' density every step, float[M*N], before the initial
+// density is added, :1676-1695), EXPORT_POS_PATH (positions at steps 1, 50,
+// 100, :1696-1726 format), CPU_DCT=1 (that same density, without the
+// initial density, in the field_x slot and field_y zero, :1757-1788; the
+// client adds the initial density back and solves on the CPU), GATHER_MODE
+// (accepted, no effect).
+#include <errno.h>
 #include <fcntl.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -25,8 +35,13 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
+#include <atomic>
 #include <chrono>
+#include <condition_variable>
+#include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "dpep.h"
@@ -36,7 +51,7 @@ namespace {
 constexpr uint32_t kIdle = 0, kGo = 1, kDone = 2, kQuit = 3;
 constexpr size_t kHeader = 64;
 constexpr uint32_t kMagicV2 = 0x32504544u;
-constexpr uint32_t kOutDensity = 1u, kOutPotential = 2u, kOutGrads = 4u;
+constexpr uint32_t kOutDensity = 1u, kOutPotential = 2u, kOutGrads = 4u, kOutNoFields = 8u;
 constexpr uint32_t kGatherModeHip = 16u;
 
 double now_ms()
@@ -45,17 +60,108 @@ double now_ms()
     return duration<double, std::milli>(steady_clock::now().time_since_epoch()).count();
 }
 
-void flag_write(const std::string& path, const char* content)
+// Publishes `content` at `path` atomically: written to a sibling file first,
+// then renamed over the target, so a poller never reads a partial flag.
+void publish_flag(const std::string& path, const char* content)
 {
-    const std::string tmp = path + ".tmp";
-    FILE* f = fopen(tmp.c_str(), "w");
+    const std::string part = path + ".tmp";
+    FILE* f = fopen(part.c_str(), "w");
     if (!f) {
-        perror(("fopen " + tmp).c_str());
+        fprintf(stderr, "[server] cannot write %s\n", part.c_str());
         return;
     }
     fputs(content, f);
     fclose(f);
-    rename(tmp.c_str(), path.c_str());
+    if (rename(part.c_str(), path.c_str()) != 0)
+        fprintf(stderr, "[server] cannot rename %s\n", part.c_str());
+}
+
+// A fixed set of worker threads that copy lists of (dst, src, bytes) pieces
+// between the shm file and the page-locked staging buffers; the calling
+// thread takes part.  One memcpy thread moves ~10 GB/s, below the link.
+class CopyPool {
+  public:
+    explicit CopyPool(int workers)
+    {
+        for (int i = 0; i < workers; ++i) threads_.emplace_back([this] { run(); });
+    }
+    ~CopyPool()
+    {
+        {
+            std::lock_guard<std::mutex> g(mu_);
+            quit_ = true;
+        }
+        cv_.notify_all();
+        for (auto& t : threads_) t.join();
+    }
+    struct Job {
+        void* dst;
+        const void* src;
+        size_t bytes;
+    };
+    // Copies every job, split into pieces of about 1 MiB, and returns when
+    // all are done.
+    void copy(const std::vector<Job>& jobs)
+    {
+        constexpr size_t kPiece = 1u << 20;
+        pieces_.clear();
+        for (const Job& j : jobs)
+            for (size_t o = 0; o < j.bytes; o += kPiece)
+                pieces_.push_back({(char*)j.dst + o, (const char*)j.src + o,
+                                   std::min(kPiece, j.bytes - o)});
+        if (pieces_.empty()) return;
+        {
+            std::lock_guard<std::mutex> g(mu_);
+            next_.store(0);
+            left_.store(pieces_.size());
+            ++round_;
+        }
+        cv_.notify_all();
+        work();
+        std::unique_lock<std::mutex> g(mu_);
+        done_cv_.wait(g, [this] { return left_.load() == 0; });
+    }
+
+  private:
+    void work()
+    {
+        for (;;) {
+            const size_t i = next_.fetch_add(1);
+            if (i >= pieces_.size()) return;
+            memcpy(pieces_[i].dst, pieces_[i].src, pieces_[i].bytes);
+            if (left_.fetch_sub(1) == 1) {
+                std::lock_guard<std::mutex> g(mu_);
+                done_cv_.notify_all();
+            }
+        }
+    }
+    void run()
+    {
+        unsigned long seen = 0;
+        for (;;) {
+            {
+                std::unique_lock<std::mutex> g(mu_);
+                cv_.wait(g, [&] { return quit_ || round_ != seen; });
+                if (quit_) return;
+                seen = round_;
+            }
+            work();
+        }
+    }
+    std::vector<std::thread> threads_;
+    std::vector<Job> pieces_;
+    std::mutex mu_;
+    std::condition_variable cv_, done_cv_;
+    std::atomic<size_t> next_{0}, left_{0};
+    unsigned long round_ = 0;
+    bool quit_ = false;
+};
+
+float* host_floats(size_t n)
+{
+    void* p = nullptr;
+    if (dpep_host_alloc(n * sizeof(float), &p) != DPEP_OK) return nullptr;
+    return (float*)p;
 }
 
 [[noreturn]] void fatal(const char* what)
@@ -115,29 +221,37 @@ int main(int argc, char** argv)
            xl, xh, yl, yh, dpep_build_info());
     fflush(stdout);
 
+    const char* dump_dens = getenv("EXPORT_DENSITY_PATH");
+    const bool dump_density = dump_dens && dump_dens[0];
+    const char* dump_pos = getenv("EXPORT_POS_PATH");
+
+    // the shm header reports every step's timings; the reference's dump and
+    // CPU-solve mode need the scattered cells' density before the fold
+    unsigned flags = DPEP_FLAG_STEP_TIMINGS;
+    if (cpu_dct || dump_density) flags |= DPEP_FLAG_SCATTER_DENSITY;
     dpep_ctx* ctx = nullptr;
-    // the shm header reports every step's timings
-    if (dpep_create(M, N, NC_max, xl, yl, xh, yh, DPEP_DTYPE_F32, DPEP_FLAG_STEP_TIMINGS,
-                    &ctx) != DPEP_OK)
+    if (dpep_create(M, N, NC_max, xl, yl, xh, yh, DPEP_DTYPE_F32, flags, &ctx) != DPEP_OK)
         fatal("dpep_create");
 
-    // Open the shm file the client created (poll briefly, :1258-1267).
+    // The client creates the shm file before it launches the server; allow
+    // it up to ten seconds to appear (:1258-1267 polls the same way).
     int fd = -1;
-    for (int i = 0; i < 100 && fd < 0; ++i) {
-        fd = open(shm_path.c_str(), O_RDWR);
-        if (fd < 0) usleep(100000);
-    }
+    const double open_deadline = now_ms() + 10000.0;
+    while ((fd = open(shm_path.c_str(), O_RDWR)) < 0 && now_ms() < open_deadline)
+        usleep(50000);
     if (fd < 0) {
-        perror(("[server] open shm: " + shm_path).c_str());
+        fprintf(stderr, "[server] FATAL cannot open %s: %s\n", shm_path.c_str(),
+                strerror(errno));
         return 1;
     }
     struct stat st;
     if (fstat(fd, &st) != 0) {
-        perror("[server] fstat shm");
+        fprintf(stderr, "[server] FATAL fstat %s: %s\n", shm_path.c_str(), strerror(errno));
         return 1;
     }
     const size_t soa = ((size_t)NC_max + 1023) / 1024 * 1024;
-    const size_t pos_bytes = soa * 4, map_bytes = (size_t)M * N * 4;
+    const size_t MN = (size_t)M * N;
+    const size_t pos_bytes = soa * 4, map_bytes = MN * 4;
     const size_t v1_size = kHeader + 4 * pos_bytes + 3 * map_bytes;
     const size_t v2_size = v1_size + 2 * map_bytes + 2 * pos_bytes;
     if ((size_t)st.st_size < v1_size) {
@@ -149,7 +263,7 @@ int main(int argc, char** argv)
     void* base = mmap(nullptr, shm_size, PROT_READ | PROT_WRITE, MAP_SHARED, fd, 0);
     close(fd);
     if (base == MAP_FAILED) {
-        perror("[server] mmap shm");
+        fprintf(stderr, "[server] FATAL mmap %s: %s\n", shm_path.c_str(), strerror(errno));
         return 1;
     }
     char* p = (char*)base;
@@ -157,35 +271,52 @@ int main(int argc, char** argv)
     volatile int32_t* shm_nc = (volatile int32_t*)(p + 4);
     float* timing = (float*)(p + 8);
     uint32_t* gmode = (uint32_t*)(p + 44);
-    const uint32_t* hdr_v2 = (const uint32_t*)(p + 48);
-    const float* px = (const float*)(p + kHeader);
-    const float* py = px + soa;
-    const float* sx = py + soa;
-    const float* sy = sx + soa;
-    float* fx = (float*)(p + kHeader + 4 * pos_bytes);
-    float* fy = fx + (size_t)M * N;
-    const float* init_density = fy + (size_t)M * N;
-    float* density = nullptr;
-    float* potential = nullptr;
-    float* gx = nullptr;
-    float* gy = nullptr;
-    if (hdr_v2[0] == kMagicV2 && shm_size >= v2_size) {
-        float* d = (float*)(p + v1_size);
-        density = d;
-        potential = d + (size_t)M * N;
-        gx = (float*)(p + v1_size + 2 * map_bytes);
-        gy = gx + soa;
+    const volatile uint32_t* hdr_v2 = (const volatile uint32_t*)(p + 48);
+    const float* shm_px = (const float*)(p + kHeader);
+    const float* shm_py = shm_px + soa;
+    const float* shm_sx = shm_py + soa;
+    const float* shm_sy = shm_sx + soa;
+    float* shm_fx = (float*)(p + kHeader + 4 * pos_bytes);
+    float* shm_fy = shm_fx + MN;
+    const float* shm_d0 = shm_fy + MN;
+    float* shm_density = nullptr;
+    float* shm_potential = nullptr;
+    float* shm_gx = nullptr;
+    float* shm_gy = nullptr;
+    const bool v2 = hdr_v2[0] == kMagicV2 && shm_size >= v2_size;
+    if (v2) {
+        shm_density = (float*)(p + v1_size);
+        shm_potential = shm_density + MN;
+        shm_gx = (float*)(p + v1_size + 2 * map_bytes);
+        shm_gy = shm_gx + soa;
         printf("[server] shm version 2 (density, potential, per-cell forces)\n");
     } else {
         printf("[server] shm version 1 (fields only)\n");
     }
     fflush(stdout);
 
-    flag_write(ready_flag, "READY\n");
+    // page-locked staging: cells in, every output a step can ask for out
+    float* h_cells = host_floats(4 * soa);
+    float* h_fx = host_floats(MN);
+    float* h_fy = host_floats(MN);
+    float* h_raw = (flags & DPEP_FLAG_SCATTER_DENSITY) ? host_floats(MN) : nullptr;
+    float* h_dens = v2 ? host_floats(MN) : nullptr;
+    float* h_phi = v2 ? host_floats(MN) : nullptr;
+    float* h_g = v2 ? host_floats(2 * soa) : nullptr;
+    if (!h_cells || !h_fx || !h_fy || ((flags & DPEP_FLAG_SCATTER_DENSITY) && !h_raw) ||
+        (v2 && (!h_dens || !h_phi || !h_g)))
+        fatal("dpep_host_alloc");
+    float* h_px = h_cells;
+    float* h_py = h_px + soa;
+    float* h_sx = h_py + soa;
+    float* h_sy = h_sx + soa;
+    const unsigned hw = std::thread::hardware_concurrency();
+    CopyPool pool((int)std::min(7u, hw > 1 ? hw - 1 : 1u));
+
+    publish_flag(ready_flag, "READY\n");
     printf("[server] READY -- polling shm state\n");
     fflush(stdout);
 
-    std::vector<float> dens_host;       // density for CPU_DCT / export
     bool d0_uploaded = false;
     uint32_t iter = 0;
     while (true) {
@@ -207,49 +338,58 @@ int main(int argc, char** argv)
         const double t0 = now_ms();
         if (!d0_uploaded) {
             // the client writes slot 3 once before its first GO (:1770-1773)
-            if (dpep_set_initial_density(ctx, init_density) != DPEP_OK)
+            if (dpep_set_initial_density(ctx, shm_d0) != DPEP_OK)
                 fatal("dpep_set_initial_density");
             d0_uploaded = true;
         }
-        const uint32_t outs = density ? hdr_v2[2] : 0u;
-        const char* dump_dens = getenv("EXPORT_DENSITY_PATH");
-        const bool want_dens_host = cpu_dct || (dump_dens && dump_dens[0]);
-        float* dens_out = (outs & kOutDensity) ? density : nullptr;
-        if (want_dens_host && !dens_out) {
-            dens_host.resize((size_t)M * N);
-            dens_out = dens_host.data();
-        }
-        const double tf0 = now_ms();
-        int rc;
-        if (cpu_dct) {
-            rc = dpep_step(ctx, px, py, sx, sy, nc, nullptr, nullptr, dens_out, nullptr,
-                           nullptr, nullptr);
-        } else {
-            rc = dpep_step(ctx, px, py, sx, sy, nc, fx, fy, dens_out,
-                           (outs & kOutPotential) ? potential : nullptr,
-                           (outs & kOutGrads) ? gx : nullptr,
-                           (outs & kOutGrads) ? gy : nullptr);
-        }
-        if (rc != DPEP_OK) fatal("dpep_step");
+        // outputs this step: the fields (v1 always; v2 unless the client
+        // opts out, and never in the CPU-solve mode, where the fx slot
+        // carries the density), and the v2 extras the header asks for
+        const uint32_t outs = v2 ? hdr_v2[2] : 0u;
+        const bool want_fields = !cpu_dct && !(outs & kOutNoFields);
+        const bool want_dens = (outs & kOutDensity) != 0;
+        const bool want_phi = (outs & kOutPotential) != 0;
+        const bool want_grads = (outs & kOutGrads) != 0;
+        const size_t ncb = (size_t)nc * sizeof(float);
+        pool.copy({{h_px, shm_px, ncb}, {h_py, shm_py, ncb}, {h_sx, shm_sx, ncb},
+                   {h_sy, shm_sy, ncb}});
+        if (dpep_set_cells(ctx, h_px, h_py, h_sx, h_sy, nc) != DPEP_OK) fatal("dpep_set_cells");
+        if (dpep_compute(ctx) != DPEP_OK) fatal("dpep_compute");
+        if (dpep_get_outputs(ctx, want_dens ? h_dens : nullptr, want_phi ? h_phi : nullptr,
+                             want_fields ? h_fx : nullptr, want_fields ? h_fy : nullptr,
+                             want_grads ? h_g : nullptr, want_grads ? h_g + soa : nullptr) !=
+            DPEP_OK)
+            fatal("dpep_get_outputs");
+        if (h_raw && dpep_get_scatter_density(ctx, h_raw) != DPEP_OK)
+            fatal("dpep_get_scatter_density");
         float t[DPEP_NUM_TIMINGS] = {0};
         dpep_get_timings(ctx, t);
         const double tw0 = now_ms();
+        std::vector<CopyPool::Job> out;
         if (cpu_dct) {
-            memcpy(fx, dens_out, map_bytes);
-            memset(fy, 0, map_bytes);
+            out.push_back({shm_fx, h_raw, map_bytes});
+            memset(shm_fy, 0, map_bytes);
+        } else if (want_fields) {
+            out.push_back({shm_fx, h_fx, map_bytes});
+            out.push_back({shm_fy, h_fy, map_bytes});
         }
-        if (dump_dens && dump_dens[0]) {
+        if (want_dens) out.push_back({shm_density, h_dens, map_bytes});
+        if (want_phi) out.push_back({shm_potential, h_phi, map_bytes});
+        if (want_grads) {
+            out.push_back({shm_gx, h_g, ncb});
+            out.push_back({shm_gy, h_g + soa, ncb});
+        }
+        pool.copy(out);
+        if (dump_density) {
             FILE* f = fopen(dump_dens, "wb");
             if (f) {
-                fwrite(dens_out, 4, (size_t)M * N, f);
+                fwrite(h_raw, sizeof(float), MN, f);
                 fclose(f);
             }
         }
-        const char* dump_pos = getenv("EXPORT_POS_PATH");
         if (dump_pos && dump_pos[0] && (iter == 1 || iter == 50 || iter == 100))
-            dump_positions(dump_pos, iter, M, N, xl, yl, xh, yh, nc, px, py, sx, sy);
+            dump_positions(dump_pos, iter, M, N, xl, yl, xh, yh, nc, h_px, h_py, h_sx, h_sy);
         const double t1 = now_ms();
-        (void)tf0;
         timing[0] = t[0];                      // h2d
         timing[1] = t[1];                      // scatter
         timing[2] = t[2];                      // gather
@@ -262,11 +402,12 @@ int main(int argc, char** argv)
         *gmode = kGatherModeHip;
         __atomic_thread_fence(__ATOMIC_RELEASE);
         *state = kDone;
-        printf("[server] done nc=%d h2d=%.3f compute=%.3f download=%.3f total=%.3f\n", nc,
-               t[0], t[5], t[6], t1 - t0);
+        printf("[server] done nc=%d h2d=%.3f compute=%.3f download=%.3f fw=%.3f total=%.3f\n",
+               nc, t[0], t[5], t[6], t1 - tw0, t1 - t0);
         fflush(stdout);
     }
     munmap(base, shm_size);
     dpep_destroy(ctx);
+    for (float* h : {h_cells, h_fx, h_fy, h_raw, h_dens, h_phi, h_g}) dpep_host_free(h);
     return 0;
 }

@@ -40,6 +40,32 @@ static hipError_t dispatch_len(int L, Fn&& fn)
 }
 
 template <typename T>
+__global__ __launch_bounds__(256) void k_tables(int L, T* __restrict__ tw,
+                                                T* __restrict__ post)
+{
+    const int i = (int)(blockIdx.x * 256 + threadIdx.x);
+    double s, c;
+    if (i < L) {
+        sincospi(2.0 * (double)i / (double)L, &s, &c);
+        tw[2 * i] = (T)c;
+        tw[2 * i + 1] = (T)-s;
+    }
+    if (i <= L / 2) {
+        sincospi((double)i / (2.0 * (double)L), &s, &c);
+        post[2 * i] = (T)c;
+        post[2 * i + 1] = (T)-s;
+    }
+}
+
+template <typename T>
+hipError_t launch_tables(int L, T* tw, T* post, hipStream_t s)
+{
+    if (L < 1 || !tw || !post) return hipErrorInvalidValue;
+    k_tables<T><<<(unsigned)((L + 255) / 256), 256, 0, s>>>(L, tw, post);
+    return hipGetLastError();
+}
+
+template <typename T>
 hipError_t launch_col_pass(const SpectralArgs& a, const T* Tt, T* Ux, T* Uy,
                            hipStream_t s)
 {
@@ -105,6 +131,8 @@ hipError_t spectral_prepare()
     return prepare_type<double>();
 }
 
+template hipError_t launch_tables<float>(int, float*, float*, hipStream_t);
+template hipError_t launch_tables<double>(int, double*, double*, hipStream_t);
 template hipError_t launch_col_pass<float>(const SpectralArgs&, const float*,
                                            float*, float*, hipStream_t);
 template hipError_t launch_col_pass<double>(const SpectralArgs&, const double*,

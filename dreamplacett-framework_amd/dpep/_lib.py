@@ -30,6 +30,9 @@ DPEP_FLAG_NO_POTENTIAL = 0x2
 DPEP_FLAG_NO_STRETCH = 0x4
 DPEP_FLAG_NO_GATHER = 0x8
 DPEP_FLAG_STEP_TIMINGS = 0x10
+DPEP_FLAG_SCATTER_DENSITY = 0x20
+
+OUTPUT_NAMES = ("density", "potential", "field_x", "field_y", "grad_x", "grad_y")
 
 NUM_TIMINGS = 9
 TIMING_KEYS = ("h2d", "scatter", "gather", "d2h_den", "upload", "compute",
@@ -65,6 +68,9 @@ _SIGNATURES = {
                                              ctypes.POINTER(ctypes.c_float),
                                              ctypes.c_int]),
     "dpep_set_profiling": (ctypes.c_int, [_vp, ctypes.c_int]),
+    "dpep_get_scatter_density": (ctypes.c_int, [_vp, _vp]),
+    "dpep_host_alloc": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(_vp)]),
+    "dpep_host_free": (ctypes.c_int, [_vp]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
@@ -123,20 +129,53 @@ def _ptr(a: Optional[np.ndarray]):
     return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
 
 
+class _Pinned:
+    """Page-locked host memory from dpep_host_alloc, viewed as numpy arrays.
+    Transfers from and to it run at the link rate; the views die with it."""
+
+    def __init__(self, lib: ctypes.CDLL):
+        self._lib = lib
+        self._ptrs = []
+
+    def array(self, n: int, dtype) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        p = ctypes.c_void_p()
+        _check(self._lib.dpep_host_alloc(max(1, n) * dtype.itemsize, ctypes.byref(p)),
+               "dpep_host_alloc", self._lib)
+        self._ptrs.append(p)
+        buf = (ctypes.c_char * (max(1, n) * dtype.itemsize)).from_address(p.value)
+        return np.frombuffer(buf, dtype=dtype, count=n)
+
+    def free(self) -> None:
+        for p in self._ptrs:
+            self._lib.dpep_host_free(p)
+        self._ptrs = []
+
+
 class Context:
     """One electric-potential problem (grid, die, capacity, dtype) on the GPU.
 
     Mirrors the life cycle of the reference server
     (host/density_scatter_ttnn_server_host.cpp: start-up :324-1294, per-step
     loop :1326-1824) as in-process calls.
+
+    pinned=True stages cells and outputs through page-locked buffers owned by
+    the context: host_cells() exposes the input buffers (write positions there
+    to skip a copy), and get_outputs(copy=False) returns views of the output
+    buffers, valid until the next get_outputs or close().
+    scatter_density=True keeps the scattered cells' density without the
+    initial density (scatter_density()), as the reference's read-back.
     """
 
     def __init__(self, num_bins_x: int, num_bins_y: int, nc_max: int,
                  xl: float, yl: float, xh: float, yh: float,
                  dtype=np.float32, deterministic: bool = False,
                  potential: bool = True, stretch: bool = True,
-                 gather: bool = True, step_timings: bool = False):
+                 gather: bool = True, step_timings: bool = False,
+                 pinned: bool = False, scatter_density: bool = False):
         self._lib = load_library()
+        self._h = None
+        self._pin: Optional[_Pinned] = None
         self.M, self.N, self.nc_max = int(num_bins_x), int(num_bins_y), int(nc_max)
         self.dtype = np.dtype(dtype)
         if self.dtype not in (np.dtype(np.float32), np.dtype(np.float64)):
@@ -153,6 +192,8 @@ class Context:
             flags |= DPEP_FLAG_NO_GATHER
         if step_timings:
             flags |= DPEP_FLAG_STEP_TIMINGS
+        if scatter_density:
+            flags |= DPEP_FLAG_SCATTER_DENSITY
         self.flags = flags
         self.potential = potential
         self.gather = gather
@@ -162,7 +203,15 @@ class Context:
                                      dt, flags, ctypes.byref(h)),
                "dpep_create", self._lib)
         self._h = h
-        self._nc = None
+        self._nc = None            # cells resident on the device
+        self._last_nc = None       # cells of the last computed step
+        self._in: Dict[str, np.ndarray] = {}
+        self._out: Dict[str, np.ndarray] = {}
+        if pinned:
+            self._pin = _Pinned(self._lib)
+            n = max(1, self.nc_max)
+            for name in ("px", "py", "sx", "sy"):
+                self._in[name] = self._pin.array(n, self.dtype)
 
     # -- helpers -----------------------------------------------------------
     def _arr(self, a, n: int, name: str) -> np.ndarray:
@@ -174,11 +223,23 @@ class Context:
             raise ValueError(f"{name} has {a.size} elements, expected {n}")
         return a
 
+    def _out_buf(self, name: str, n: int) -> np.ndarray:
+        """Pinned output buffer `name` with room for n elements."""
+        buf = self._out.get(name)
+        if buf is None:
+            cap = max(1, self.nc_max) if name.startswith("grad") else self.M * self.N
+            buf = self._out[name] = self._pin.array(cap, self.dtype)
+        return buf[:n]
+
     @property
     def handle(self) -> ctypes.c_void_p:
         if self._h is None:
             raise RuntimeError("context is closed")
         return self._h
+
+    @property
+    def pinned(self) -> bool:
+        return self._pin is not None
 
     # -- API -----------------------------------------------------------------
     def set_initial_density(self, d0n) -> None:
@@ -199,48 +260,93 @@ class Context:
                                               float(target_density)),
                "dpep_set_fixed_cells", self._lib)
 
+    def host_cells(self) -> Dict[str, np.ndarray]:
+        """The pinned input buffers px, py, sx, sy (nc_max elements each) of
+        a pinned context: positions written there upload without a copy."""
+        if self._pin is None:
+            raise RuntimeError("context was created without pinned=True")
+        return dict(self._in)
+
     def set_cells(self, px, py, sx, sy) -> None:
         n = int(np.asarray(px).size)
+        if n > self.nc_max:
+            raise ValueError(f"nc={n} exceeds nc_max={self.nc_max}")
         arrs = [self._arr(a, n, nm) for a, nm in ((px, "px"), (py, "py"),
                                                     (sx, "sx"), (sy, "sy"))]
+        if self._pin is not None:
+            staged = []
+            for a, name in zip(arrs, ("px", "py", "sx", "sy")):
+                dst = self._in[name]
+                if a.ctypes.data != dst.ctypes.data:     # not already staged
+                    dst[:n] = a
+                staged.append(dst)
+            arrs = staged
         _check(self._lib.dpep_set_cells(self.handle, *[_ptr(a) for a in arrs], n),
                "dpep_set_cells", self._lib)
         self._nc = n
 
     def compute(self) -> None:
         _check(self._lib.dpep_compute(self.handle), "dpep_compute", self._lib)
+        self._last_nc = self._nc
 
     def sync(self) -> None:
         _check(self._lib.dpep_sync(self.handle), "dpep_sync", self._lib)
 
     def get_outputs(self, density=True, potential=None, fields=True,
-                    grads=None) -> Dict[str, np.ndarray]:
+                    grads=None, copy=True) -> Dict[str, np.ndarray]:
+        """The last step's outputs.  grad_x/grad_y have one entry per cell of
+        that step.  On a pinned context copy=False returns views of the
+        pinned buffers (overwritten by the next get_outputs)."""
         potential = self.potential if potential is None else potential
         grads = self.gather if grads is None else grads
         mn = (self.M, self.N)
+        want = {"density": density, "potential": potential, "field_x": fields,
+                "field_y": fields, "grad_x": grads, "grad_y": grads}
+        n = self._last_nc or 0
         out: Dict[str, np.ndarray] = {}
-        if density:
-            out["density"] = np.empty(mn, self.dtype)
-        if potential:
-            out["potential"] = np.empty(mn, self.dtype)
-        if fields:
-            out["field_x"] = np.empty(mn, self.dtype)
-            out["field_y"] = np.empty(mn, self.dtype)
-        if grads:
-            n = self._nc or 0
-            out["grad_x"] = np.empty(n, self.dtype)
-            out["grad_y"] = np.empty(n, self.dtype)
+        for name in OUTPUT_NAMES:
+            if not want[name]:
+                continue
+            size = n if name.startswith("grad") else self.M * self.N
+            if self._pin is not None:
+                out[name] = self._out_buf(name, size)
+            else:
+                out[name] = np.empty(size, self.dtype)
         _check(self._lib.dpep_get_outputs(
             self.handle, _ptr(out.get("density")), _ptr(out.get("potential")),
             _ptr(out.get("field_x")), _ptr(out.get("field_y")),
             _ptr(out.get("grad_x")), _ptr(out.get("grad_y"))),
             "dpep_get_outputs", self._lib)
+        for name in list(out):
+            a = out[name]
+            if self._pin is not None and copy:
+                a = a.copy()
+            out[name] = a if name.startswith("grad") else a.reshape(mn)
         return out
 
-    def step(self, px, py, sx, sy) -> Dict[str, np.ndarray]:
+    def scatter_density(self) -> np.ndarray:
+        """The last step's scattered-cell density without the initial
+        density (M x N); needs scatter_density=True."""
+        d = np.empty((self.M, self.N), self.dtype)
+        _check(self._lib.dpep_get_scatter_density(self.handle, _ptr(d)),
+               "dpep_get_scatter_density", self._lib)
+        return d
+
+    def step(self, px, py, sx, sy, outputs=None, copy=True) -> Dict[str, np.ndarray]:
+        """set_cells + compute + get_outputs.  outputs: names from
+        OUTPUT_NAMES to fetch (default: all this context computes)."""
         self.set_cells(px, py, sx, sy)
         self.compute()
-        return self.get_outputs()
+        if outputs is None:
+            return self.get_outputs(copy=copy)
+        outputs = set(outputs)
+        unknown = outputs - set(OUTPUT_NAMES)
+        if unknown:
+            raise ValueError(f"unknown outputs {sorted(unknown)}")
+        return self.get_outputs(density="density" in outputs,
+                                potential="potential" in outputs,
+                                fields=bool(outputs & {"field_x", "field_y"}),
+                                grads=bool(outputs & {"grad_x", "grad_y"}), copy=copy)
 
     def set_profiling(self, slots: int) -> None:
         """slots > 0: record per-kernel HIP events for up to `slots` steps."""
@@ -263,6 +369,10 @@ class Context:
         if self._h is not None:
             self._lib.dpep_destroy(self._h)
             self._h = None
+        if self._pin is not None:
+            self._in, self._out = {}, {}
+            self._pin.free()
+            self._pin = None
 
     def __enter__(self):
         return self

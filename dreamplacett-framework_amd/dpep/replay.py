@@ -78,9 +78,12 @@ def read_density(path: str, M: int, N: int) -> np.ndarray:
 def replay(d: PositionDump, d0n: Optional[np.ndarray] = None, dtype=np.float32,
            steps: int = 1) -> Dict[str, object]:
     """One step (the last of `steps` identical ones, for timing) of the dump's
-    cells on the GPU; returns the outputs and the per-step milliseconds."""
+    cells on the GPU; returns the outputs, the cells' density without the
+    initial density ("scatter_density", what EXPORT_DENSITY_PATH dumps) and
+    the per-step milliseconds."""
     from ._lib import Context
-    with Context(d.M, d.N, max(d.nc, 1), d.xl, d.yl, d.xh, d.yh, dtype=dtype) as ctx:
+    with Context(d.M, d.N, max(d.nc, 1), d.xl, d.yl, d.xh, d.yh, dtype=dtype,
+                 scatter_density=True) as ctx:
         if d0n is not None:
             ctx.set_initial_density(np.asarray(d0n, dtype).reshape(d.M, d.N))
         ctx.set_cells(d.px, d.py, d.sx, d.sy)
@@ -92,6 +95,7 @@ def replay(d: PositionDump, d0n: Optional[np.ndarray] = None, dtype=np.float32,
         ctx.sync()
         ms = (time.perf_counter() - t0) * 1e3 / max(steps, 1)
         out = ctx.get_outputs()
+        out["scatter_density"] = ctx.scatter_density()
     out["ms_per_step"] = ms
     return out
 
@@ -100,7 +104,8 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__,
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("dump")
-    ap.add_argument("--density", help="float32[M*N] density to compare with")
+    ap.add_argument("--density", help="float32[M*N] density dump (EXPORT_DENSITY_PATH: "
+                    "the cells' density without the initial density) to compare with")
     ap.add_argument("--d0", help="float32[M*N] initial density / bin area")
     ap.add_argument("--steps", type=int, default=10)
     args = ap.parse_args(argv)
@@ -116,7 +121,8 @@ def main(argv=None) -> int:
     if args.density:
         ref = read_density(args.density, d.M, d.N).astype(np.float64)
         den = np.abs(ref).max() or 1.0
-        print(f"  vs {args.density}: rel Linf {np.abs(rho - ref).max() / den:.3e}")
+        raw = out["scatter_density"].astype(np.float64)
+        print(f"  vs {args.density}: rel Linf {np.abs(raw - ref).max() / den:.3e}")
     return 0
 
 

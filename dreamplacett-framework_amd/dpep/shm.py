@@ -26,7 +26,8 @@ Version 2 = version 1 plus, after init_density:
 and, in the header padding:
         [48:52] magic        u32  0x32504544 ("DEP2")
         [52:56] version      u32  2
-        [56:60] outputs      u32  bit 0 density, bit 1 potential, bit 2 grads
+        [56:60] outputs      u32  bit 0 density, bit 1 potential, bit 2 grads,
+                                  bit 3 no fields (field_x/field_y not written)
 A version-1 server ignores bytes 48..64; a version-1 client never writes the
 magic, so the server falls back to the version-1 layout.
 """
@@ -53,6 +54,7 @@ MAGIC_V2 = 0x32504544
 OUT_DENSITY = 0x1
 OUT_POTENTIAL = 0x2
 OUT_GRADS = 0x4
+OUT_NO_FIELDS = 0x8
 
 # state nc h2d scatter gather d2h_den upload compute download fw total gm
 HDR_TIMING_FMT = "<IifffffffffI"
@@ -114,6 +116,25 @@ class Layout:
 
 def write_v2_header(buf, outputs: int = OUT_DENSITY | OUT_POTENTIAL | OUT_GRADS) -> None:
     struct.pack_into("<III", buf, OFF_MAGIC, MAGIC_V2, 2, outputs)
+
+
+def set_outputs(buf, outputs: int) -> None:
+    """The outputs word a version-2 server reads before every step."""
+    struct.pack_into("<I", buf, OFF_OUTPUTS, outputs)
+
+
+def outputs_of(names) -> int:
+    """Outputs word for a set of output names (density, potential, field_x,
+    field_y, grad_x, grad_y)."""
+    names = set(names)
+    word = 0 if names & {"field_x", "field_y"} else OUT_NO_FIELDS
+    if "density" in names:
+        word |= OUT_DENSITY
+    if "potential" in names:
+        word |= OUT_POTENTIAL
+    if names & {"grad_x", "grad_y"}:
+        word |= OUT_GRADS
+    return word
 
 
 def read_timings(buf):

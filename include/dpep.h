@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define DPEP_ABI_VERSION 2
+#define DPEP_ABI_VERSION 3
 
 /* status codes */
 #define DPEP_OK 0
@@ -65,6 +65,10 @@ extern "C" {
                                         costs a few microseconds of GPU time
                                         per step; without the flag the slot
                                         reads 0 unless profiling is on)    */
+#define DPEP_FLAG_SCATTER_DENSITY 0x20u /* also keep the scattered cells'
+                                        density without the initial density
+                                        (one more M*N map written per step),
+                                        for dpep_get_scatter_density       */
 
 /* timing slots, the reference's 9-float shm header order
  * (integration/scatter_ttnn_client.py:151-163): h2d, scatter, gather,
@@ -131,11 +135,31 @@ int dpep_sync(dpep_ctx* ctx);
 
 /* Copies the last step's outputs to host memory (waits first).  Any pointer
  * may be NULL.  density, potential, field_x, field_y: M*N; grad_x, grad_y:
- * nc (the per-cell gather ratio * sum tx*ty*field, sign left to the caller).
+ * nc of the last computed step (the per-cell gather ratio * sum
+ * tx*ty*field, sign left to the caller).  Fails with DPEP_ERR_STATE when a
+ * requested output is stale: cells were uploaded after the last step, or the
+ * last step was a dpep_step_device that wrote that output to a caller-owned
+ * buffer.  Host memory from dpep_host_alloc copies at the full link rate.
  * Replaces the server's D2H and field write (:1678, :1785-1789). */
 int dpep_get_outputs(dpep_ctx* ctx, void* density, void* potential,
                      void* field_x, void* field_y, void* grad_x,
                      void* grad_y);
+
+/* The last step's scattered-cell density alone, M*N elements, without the
+ * initial density: the reference server's density read-back
+ * (host/density_scatter_ttnn_server_host.cpp:1676-1678), which it dumps to
+ * EXPORT_DENSITY_PATH (:1686-1695) and, with CPU_DCT=1, writes to the
+ * field_x slot unfolded (:1759, :1786-1788).  Needs a context created with
+ * DPEP_FLAG_SCATTER_DENSITY.  Waits for the step. */
+int dpep_get_scatter_density(dpep_ctx* ctx, void* out);
+
+/* Page-locked host memory (hipHostMalloc): transfers from and to it run at
+ * the link rate, where pageable memory is staged by the runtime.  The
+ * reference's server copies through pageable std::vectors
+ * (:1335-1349, :1676-1678); the shm server of this library stages through
+ * these buffers instead.  Free with dpep_host_free. */
+int dpep_host_alloc(size_t bytes, void** out);
+int dpep_host_free(void* p);
 
 /* set_cells + compute + get_outputs: one whole step on host buffers, the
  * server loop body (:1326-1815). */

@@ -1,4 +1,7 @@
-"""Shared test set-up: import paths, the `gpu` marker, tolerance helpers."""
+"""Shared test set-up: import paths, the `gpu` marker, tolerance helpers, and
+the HIP runtime libdpep.so is linked against (for tests that hand it device
+buffers)."""
+import ctypes
 import os
 import sys
 
@@ -38,3 +41,64 @@ def oracle():
     import pyoracle
     pyoracle.build()
     return pyoracle
+
+
+def hip_runtime():
+    """The HIP runtime library libdpep.so loaded (found in this process's
+    memory map after loading it, so caller-owned device buffers come from
+    the same runtime), with the few entry points the tests call declared."""
+    import dpep
+    dpep.load_library()
+    path = None
+    with open("/proc/self/maps") as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) >= 6 and "libamdhip64" in os.path.basename(parts[-1]):
+                path = parts[-1]
+                break
+    if path is None:
+        raise RuntimeError("libdpep.so loaded no libamdhip64")
+    hip = ctypes.CDLL(path)
+    hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    hip.hipFree.argtypes = [ctypes.c_void_p]
+    hip.hipDeviceSynchronize.argtypes = []
+    return hip
+
+
+class DeviceBuffers:
+    """hipMalloc'd buffers through the runtime libdpep uses, freed on exit."""
+    H2D, D2H = 1, 2
+
+    def __init__(self):
+        self.hip = hip_runtime()
+        self.bufs = []
+
+    def alloc(self, nbytes):
+        p = ctypes.c_void_p()
+        rc = self.hip.hipMalloc(ctypes.byref(p), max(1, int(nbytes)))
+        assert rc == 0, f"hipMalloc({nbytes}) = {rc}"
+        self.bufs.append(p)
+        return p
+
+    def upload(self, a):
+        a = np.ascontiguousarray(a)
+        p = self.alloc(a.nbytes)
+        assert self.hip.hipMemcpy(p, a.ctypes.data, a.nbytes, self.H2D) == 0
+        return p
+
+    def download(self, p, n, dtype):
+        h = np.empty(n, dtype)
+        assert self.hip.hipMemcpy(h.ctypes.data, p, h.nbytes, self.D2H) == 0
+        return h
+
+    def sync(self):
+        assert self.hip.hipDeviceSynchronize() == 0
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        for p in self.bufs:
+            self.hip.hipFree(p)
+        self.bufs = []

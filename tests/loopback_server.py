@@ -6,7 +6,9 @@ the shared-memory client.
 Speaks the server side of the protocol in dpep/shm.py: writes ready.flag
 (tmp + rename), polls the state word, answers GO with the float64 oracle's
 step cast to float32 (fields always; density, potential and per-cell forces
-when the file is version 2), QUIT ends it.  LOOPBACK_MODE selects a failure
+when the file is version 2, as its outputs word asks, fields omitted when
+it says so), QUIT ends it.  CPU_DCT=1 as the real server: the cells' density
+without the initial density in the field_x slot, field_y zero.  LOOPBACK_MODE selects a failure
 for the client's error paths: "exit" (exit 3 before ready), "noready" (never
 write ready.flag), "hang" (never answer GO; QUIT still ends it).  The
 arguments received are written to <ipc_dir>/args.txt.
@@ -36,6 +38,7 @@ def main():
     xl, yl, xh, yh = (float(v) for v in sys.argv[5:9]) if len(sys.argv) >= 9 else (
         0.0, 0.0, 1e6, 1e6)
     mode = os.environ.get("LOOPBACK_MODE", "ok")
+    cpu_dct = os.environ.get("CPU_DCT") == "1"
     with open(os.path.join(ipc, "args.txt"), "w") as f:
         f.write(" ".join(sys.argv[1:]))
     if mode == "exit":
@@ -80,10 +83,14 @@ def main():
         d0n = grid("init_density").astype(np.float64)
         r = pyoracle.step(*cells, M, N, xl, yl, xh, yh, d0n=d0n,
                           gather_forces=lay.version >= 2)
-        grid("field_x")[...] = r["field_x"]
-        grid("field_y")[...] = r["field_y"]
+        outs = struct.unpack_from("<I", mm, S.OFF_OUTPUTS)[0] if lay.version >= 2 else 0
+        if cpu_dct:
+            grid("field_x")[...] = pyoracle.density(*cells, M, N, xl, yl, xh, yh)
+            grid("field_y")[...] = 0.0
+        elif not outs & S.OUT_NO_FIELDS:
+            grid("field_x")[...] = r["field_x"]
+            grid("field_y")[...] = r["field_y"]
         if lay.version >= 2:
-            outs = struct.unpack_from("<I", mm, S.OFF_OUTPUTS)[0]
             if outs & S.OUT_DENSITY:
                 grid("density")[...] = r["density"]
             if outs & S.OUT_POTENTIAL:

@@ -162,46 +162,177 @@ def test_returns_torch_when_asked(tmp_path):
         c.stop()
 
 
-def test_dreamplace_adapter_selects_movable_and_filler(tmp_path, oracle):
+def _adapter_case(rng, M=16, die=160.0):
+    """40 movable cells, 5 terminals (macros), 15 fillers on a 16 x 16 grid."""
+    def cells(n, lo, hi):
+        return (rng.uniform(0, 150, n), rng.uniform(0, 150, n),
+                rng.uniform(lo, hi, n), rng.uniform(lo, hi, n))
+    return cells(40, 1, 20), cells(5, 30, 60), cells(15, 2, 8)
+
+
+def test_dreamplace_adapter_forward_and_backward(tmp_path, oracle):
     """The patched forward passes [movable | filler] cells with their
     original sizes (clamped + 2*offset) and the die, grid and initial density
-    taken from the call (reference :611-640, :786-795)."""
+    taken from the call (reference :611-640, :786-795); the patched backward
+    returns -grad_pos times the per-cell forces the step gathered, in pos
+    layout, zero for the terminals."""
     torch = pytest.importorskip("torch")
     from dpep import scatter_ttnn_client as stc
+    import dreamplace_fakes as F
 
     rng = np.random.default_rng(11)
-    n_mov, n_fix, n_fil = 40, 5, 15
-    n = n_mov + n_fix + n_fil
+    mov, term, fil = _adapter_case(rng)
     M = N = 16
-    die = 160.0
-    pos = torch.from_numpy(np.concatenate([rng.uniform(0, 150, n), rng.uniform(0, 150, n)]))
-    sx = rng.uniform(1, 20, n)
-    sy = rng.uniform(1, 20, n)
-    # DREAMPlace clamps to sqrt2*bin and keeps offset = (size - clamped)/2
-    bs = die / M
-    csx, csy = np.maximum(sx, np.sqrt(2) * bs), np.maximum(sy, np.sqrt(2) * bs)
-    t = lambda a: torch.from_numpy(np.asarray(a, np.float64))
-    init = rng.uniform(0, 5, (M, N))
-
-    class Ctx:
-        pass
-
-    client = _client(tmp_path, _w(0, n, M), nc_max=n)
+    die = (0.0, 0.0, 160.0, 160.0)
+    d0n = rng.uniform(0, 0.5, (M, N))
+    args, sel = F.forward_args(mov, term, fil, M, N, die, d0n)
+    client = _client(tmp_path, _w(0, len(sel), M), nc_max=len(sel))
     client.M = client.N = 0                       # taken from the call
-    fwd = stc.make_forward(client).__func__
+    fwd = stc.make_forward(client, keep_field_maps=True).__func__
+    bwd = stc.make_backward().__func__
     try:
-        fwd(Ctx(), pos, t(csx), t(csy), t((sx - csx) / 2), t((sy - csy) / 2), None,
-            None, None, t(init), 1.0, 0.0, 0.0, die, die, bs, bs, n_mov, n_fil,
-            0, None, M, N, 0, 0, 0, 0, False, None)
-        sel = np.r_[0:n_mov, n - n_fil:n]
-        p = pos.numpy()
-        ref = oracle.step(p[:n][sel], p[n:][sel], sx[sel], sy[sel], M, N, 0.0, 0.0,
-                          die, die, d0n=init / (bs * bs))
-        out = client.last_outputs
-        assert rel_linf(out["density"], ref["density"]) < 1e-5
-        assert rel_l2(out["field_x"], ref["field_x"]) < 1e-5
+        ctx = F.Ctx()
+        energy = fwd(ctx, *args)
+        assert float(energy.sum()) == 0.0
+        pos = args[0].numpy()
+        n = pos.size // 2
+        sx, sy = (args[1] + 2 * args[3]).numpy(), (args[2] + 2 * args[4]).numpy()
+        ref = oracle.step(pos[:n][sel], pos[n:][sel], sx[sel], sy[sel], M, N, *die,
+                          d0n=d0n)
+        assert set(client.last_outputs) == {"field_x", "field_y", "grad_x", "grad_y"}
+        assert rel_l2(ctx.field_map_x.numpy(), ref["field_x"]) < 1e-5
+        assert rel_l2(ctx.field_map_y.numpy(), ref["field_y"]) < 1e-5
+        grads = bwd(ctx, torch.tensor([0.5], dtype=torch.float64))
+        assert len(grads) == 38 and all(g is None for g in grads[1:])
+        g = grads[0].numpy()
+        assert g.shape == pos.shape
+        assert rel_l2(g[:n][sel], -0.5 * ref["grad_x"]) < 1e-5
+        assert rel_l2(g[n:][sel], -0.5 * ref["grad_y"]) < 1e-5
+        term_idx = np.setdiff1d(np.arange(n), sel)
+        assert np.all(g[:n][term_idx] == 0) and np.all(g[n:][term_idx] == 0)
     finally:
         client.stop()
+
+
+def test_dreamplace_adapter_fetches_only_the_forces(tmp_path, oracle):
+    """Without keep_field_maps the step fetches the per-cell forces alone:
+    the server is told to skip the fields, ctx.field_map_x/y stay None."""
+    pytest.importorskip("torch")
+    from dpep import scatter_ttnn_client as stc
+    import dreamplace_fakes as F
+
+    rng = np.random.default_rng(12)
+    mov, term, fil = _adapter_case(rng)
+    args, sel = F.forward_args(mov, term, fil, 16, 16, (0.0, 0.0, 160.0, 160.0),
+                               np.zeros((16, 16)))
+    client = _client(tmp_path, _w(0, len(sel), 16), nc_max=len(sel))
+    fwd = stc.make_forward(client).__func__
+    try:
+        ctx = F.Ctx()
+        fwd(ctx, *args)
+        assert set(client.last_outputs) == {"grad_x", "grad_y"}
+        assert ctx.field_map_x is None and ctx.dpep_forces
+        outs = struct.unpack_from("<I", client._mm, S.OFF_OUTPUTS)[0]
+        assert outs == S.OUT_GRADS | S.OUT_NO_FIELDS
+        assert not client._views["field_x"].any()      # never written
+        with pytest.raises(RuntimeError, match="needs the fields"):
+            client.call(*(np.zeros(4, np.float32),) * 4)
+    finally:
+        client.stop()
+
+
+def test_cpu_dct_mode(tmp_path, oracle, monkeypatch):
+    """CPU_DCT=1 as in the reference (:804-829 client, :1757-1788 server):
+    call() returns the cells' density without the initial density in
+    field_x and zero field_y; the adapter adds the initial density back and
+    runs DREAMPlace's transforms (stand-ins in the server's conventions), and
+    its backward is DREAMPlace's own."""
+    torch = pytest.importorskip("torch")
+    from dpep import scatter_ttnn_client as stc
+    import dreamplace_fakes as F
+
+    monkeypatch.setenv("CPU_DCT", "1")
+    rng = np.random.default_rng(13)
+    mov, term, fil = _adapter_case(rng)
+    M = N = 16
+    die = (0.0, 0.0, 160.0, 160.0)
+    d0n = rng.uniform(0, 0.5, (M, N))
+    tf = F.Transforms(M, N, 10.0, 10.0)
+    args, sel = F.forward_args(mov, term, fil, M, N, die, d0n, transforms=tf)
+    calls = []
+    client = _client(tmp_path, _w(0, len(sel), M), nc_max=len(sel))
+    fwd = stc.make_forward(client).__func__
+    bwd = stc.make_backward(lambda ctx, g: calls.append(g) or ("cpu",)).__func__
+    try:
+        ctx = F.Ctx()
+        fwd(ctx, *args)
+        pos = args[0].numpy()
+        n = pos.size // 2
+        sx, sy = (args[1] + 2 * args[3]).numpy(), (args[2] + 2 * args[4]).numpy()
+        cells = (pos[:n][sel], pos[n:][sel], sx[sel], sy[sel])
+        raw = oracle.density(*cells, M, N, *die)
+        assert rel_linf(client.last_outputs["field_x"], raw) < 1e-6
+        assert not client.last_outputs["field_y"].any()
+        ref = oracle.step(*cells, M, N, *die, d0n=d0n)
+        assert rel_l2(ctx.field_map_x.numpy(), ref["field_x"]) < 1e-5
+        assert rel_l2(ctx.field_map_y.numpy(), ref["field_y"]) < 1e-5
+        assert bwd(ctx, torch.ones(1)) == ("cpu",) and len(calls) == 1
+        fx, fy, _ = client.call(*(c.astype(np.float32) for c in cells))
+        assert rel_linf(fx, raw) < 1e-6 and not np.asarray(fy).any()
+        # DREAMPlace's operators are required
+        args2 = args[:31] + (None,) * 6
+        with pytest.raises(ValueError, match="CPU_DCT"):
+            fwd(F.Ctx(), *args2)
+    finally:
+        client.stop()
+
+
+def test_cpu_cut_over_after_n_iterations(tmp_path, monkeypatch):
+    """V13_USE_CPU_AFTER_ITER=n (reference :540-604): iterations after the
+    n-th run DREAMPlace's original forward, and the backward follows."""
+    torch = pytest.importorskip("torch")
+    from dpep import scatter_ttnn_client as stc
+    import dreamplace_fakes as F
+
+    monkeypatch.setenv("V13_USE_CPU_AFTER_ITER", "2")
+    rng = np.random.default_rng(14)
+    mov, term, fil = _adapter_case(rng)
+    args, sel = F.forward_args(mov, term, fil, 16, 16, (0.0, 0.0, 160.0, 160.0),
+                               np.zeros((16, 16)))
+    seen = []
+
+    def orig_forward(ctx, *a):
+        seen.append("fwd")
+        return torch.ones(1)
+
+    client = _client(tmp_path, _w(0, len(sel), 16), nc_max=len(sel))
+    fwd = stc.make_forward(client, original_forward=orig_forward).__func__
+    bwd = stc.make_backward(lambda ctx, g: ("orig",)).__func__
+    try:
+        for it in range(4):
+            ctx = F.Ctx()
+            e = fwd(ctx, *args)
+            if it < 2:
+                assert float(e.sum()) == 0.0 and ctx.dpep_forces
+                assert bwd(ctx, torch.ones(1))[0].shape == args[0].shape
+            else:
+                assert float(e.sum()) == 1.0 and not ctx.dpep_forces
+                assert bwd(ctx, torch.ones(1)) == ("orig",)
+        assert seen == ["fwd", "fwd"] and len(client._timings) == 2
+    finally:
+        client.stop()
+
+
+def test_timing_summary():
+    c = ScatterTTNNClient()
+    assert c.timing_summary() == {}
+    c._timings = [{"a": 1.0, "mode": "v11"}, {"a": 3.0, "mode": "hip"},
+                  {"a": 5.0, "mode": "hip"}, {"a": 10.0, "mode": "hip", "b": 2}]
+    s = c.timing_summary(n_warmup=1)
+    assert s["a_mean"] == 6.0 and s["a_median"] == 5.0 and s["mode"] == "hip"
+    assert s["b_mean"] == 2.0 and s["n_iters"] == 4 and s["n_timed"] == 3
+    s = c.timing_summary(n_warmup=10)           # too few steps: all of them
+    assert s["n_timed"] == 4 and s["a_mean"] == 4.75
 
 
 def test_patch_dreamplace_needs_dreamplace(tmp_path):

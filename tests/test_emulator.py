@@ -45,6 +45,7 @@ CASES = [
     "f32 32 2048 500",
     "f32 16 4096 2000 tall", "f64 16 4096 100",
     "f32 16 128 9000 tall",  # chunks chosen per step: both strips split
+    "f32 8 8192 3000 tall",  # 2-row strips, the largest LDS tile and row FFT
 ]
 
 

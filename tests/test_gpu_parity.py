@@ -53,7 +53,8 @@ def run_oracle(oracle, w, dtype=np.float32, cells=None, stretch=True):
 # --------------------------------------------------------------------------
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("M,N", [(8, 8), (16, 64), (64, 16), (512, 512),
-                                 (2048, 2048), (4096, 4096), (8192, 8)])
+                                 (2048, 2048), (4096, 4096), (8192, 8), (8, 8192),
+                                 (64, 8192)])
 def test_solve_random_density(oracle, dtype, M, N):
     import dpep
     if dtype == np.float64 and max(M, N) > 4096:
@@ -239,60 +240,111 @@ def test_timings_and_kernel_times():
     assert t0["compute"] == 0.0 and np.isfinite(out["density"]).all()
 
 
+def test_full_step_8192_columns(oracle):
+    """float32 rows of 8192 bins: 2-row strips (the largest LDS tile, 128 KiB
+    + 16 B), the 8192-point row DCT inside the accumulation, two gather rows
+    at a time; cells of all sizes, some spanning more than a strip."""
+    import dpep
+    M, N = 64, 8192
+    rng = np.random.default_rng(8192)
+    nc = 40000
+    xh, yh = 640.0, 81920.0
+    sx = rng.uniform(0.5, 30.0, nc)
+    sy = rng.uniform(2.0, 40.0, nc)
+    px = rng.uniform(-5.0, xh, nc)
+    py = rng.uniform(-5.0, yh, nc)
+    cells = [a.astype(np.float32) for a in (px, py, sx, sy)]
+    d0 = (0.3 * rng.random((M, N))).astype(np.float32)
+    with dpep.Context(M, N, nc, 0.0, 0.0, xh, yh) as ctx:
+        ctx.set_initial_density(d0)
+        for k in range(2):       # twice: the side map must be left clean
+            out = ctx.step(*cells)
+    ref = oracle.step(*cells, M, N, 0.0, 0.0, xh, yh, d0n=d0)
+    print(check(out, ref, np.float32, "64x8192"), flush=True)
+
+
 def test_step_device_matches_host_step():
     """dpep_step_device on caller-owned device buffers (allocated through the
-    same HIP runtime libdpep links) equals the host-buffer step."""
+    same HIP runtime libdpep links) equals the host-buffer step; afterwards
+    the context's own outputs are stale and dpep_get_outputs refuses them."""
     import dpep
+    from conftest import DeviceBuffers
     from dpep import workloads
     lib = dpep.load_library()
-    hip = ctypes.CDLL("libamdhip64.so.7")
-    hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
-    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
-    hip.hipFree.argtypes = [ctypes.c_void_p]
-    H2D, D2H = 1, 2
     w = workloads.small(3, seed=9, cells=30000, grid=256)
     cells = w.cells(np.float32)
     ref = run_gpu(w)
-    bufs = []
-
-    def dev(nbytes):
-        p = ctypes.c_void_p()
-        assert hip.hipMalloc(ctypes.byref(p), nbytes) == 0
-        bufs.append(p)
-        return p
-
-    try:
-        dc = []
-        for a in cells:
-            p = dev(a.nbytes)
-            assert hip.hipMemcpy(p, a.ctypes.data, a.nbytes, H2D) == 0
-            dc.append(p)
-        mnb = w.M * w.N * 4
-        dfx, dfy, dden, dphi = dev(mnb), dev(mnb), dev(mnb), dev(mnb)
-        dgx, dgy = dev(w.nc * 4), dev(w.nc * 4)
+    mn = w.M * w.N
+    with DeviceBuffers() as db:
+        dc = [db.upload(a) for a in cells]
+        dfx, dfy, dden, dphi = (db.alloc(mn * 4) for _ in range(4))
+        dgx, dgy = db.alloc(w.nc * 4), db.alloc(w.nc * 4)
         with dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh) as ctx:
             ctx.set_initial_density(w.d0n.astype(np.float32))
             rc = lib.dpep_step_device(ctx.handle, *dc, w.nc, dfx, dfy, dden, dphi,
                                       dgx, dgy, None)
             assert rc == 0, dpep.last_error()
             ctx.sync()
+            ctx._last_nc = w.nc
+            with pytest.raises(RuntimeError, match="stale"):
+                ctx.get_outputs()
         got = {}
-        for name, p, n in (("field_x", dfx, w.M * w.N), ("field_y", dfy, w.M * w.N),
-                           ("density", dden, w.M * w.N), ("potential", dphi, w.M * w.N),
+        for name, p, n in (("field_x", dfx, mn), ("field_y", dfy, mn),
+                           ("density", dden, mn), ("potential", dphi, mn),
                            ("grad_x", dgx, w.nc), ("grad_y", dgy, w.nc)):
-            h = np.empty(n, np.float32)
-            assert hip.hipMemcpy(h.ctypes.data, p, n * 4, D2H) == 0
-            got[name] = h.reshape(ref[name].shape)
-    finally:
-        for p in bufs:
-            hip.hipFree(p)
+            got[name] = db.download(p, n, np.float32).reshape(ref[name].shape)
     for k in got:
         np.testing.assert_allclose(got[k], ref[k], rtol=1e-6, atol=1e-6 * np.abs(ref[k]).max())
 
 
-# --------------------------------------------------------------------------
-# convergence-loop configuration: 100 consecutive steps
-# --------------------------------------------------------------------------
+def test_outputs_are_stale_after_new_cells():
+    """Cells uploaded after a step make its outputs stale: dpep_get_outputs
+    refuses them until the next compute; the forces returned are sized by
+    the computed step's cell count."""
+    import dpep
+    from dpep import workloads
+    w = workloads.small(3, seed=10, cells=5000, grid=64)
+    px, py, sx, sy = w.cells(np.float32)
+    with dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh) as ctx:
+        ctx.set_cells(px, py, sx, sy)
+        ctx.compute()
+        full = ctx.get_outputs()
+        assert full["grad_x"].shape == (w.nc,)
+        ctx.set_cells(px[:100], py[:100], sx[:100], sy[:100])
+        with pytest.raises(RuntimeError, match="stale"):
+            ctx.get_outputs()
+        ctx.compute()
+        assert ctx.get_outputs()["grad_x"].shape == (100,)
+
+
+@pytest.mark.parametrize("pinned", [False, True])
+def test_pinned_context_and_scatter_density(oracle, pinned):
+    """A pinned context (page-locked staging) gives the same outputs, and
+    the scatter density (DPEP_FLAG_SCATTER_DENSITY) is the cells' density
+    without the initial density."""
+    import dpep
+    from dpep import workloads
+    w = workloads.small(3, seed=12, cells=20000, grid=256)
+    px, py, sx, sy = w.cells(np.float32)
+    with dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh, pinned=pinned,
+                      scatter_density=True) as ctx:
+        ctx.set_initial_density(w.d0n.astype(np.float32))
+        if pinned:
+            hc = ctx.host_cells()
+            for k, a in zip(("px", "py", "sx", "sy"), (px, py, sx, sy)):
+                hc[k][:w.nc] = a
+            out = ctx.step(hc["px"][:w.nc], hc["py"][:w.nc], hc["sx"][:w.nc],
+                           hc["sy"][:w.nc])
+        else:
+            out = ctx.step(px, py, sx, sy)
+        raw = ctx.scatter_density()
+    ref = run_oracle(oracle, w)
+    check(out, ref, np.float32, f"pinned={pinned}")
+    e = rel_linf(raw, oracle.density(px, py, sx, sy, w.M, w.N, w.xl, w.yl, w.xh, w.yh))
+    print(f"scatter density rel Linf {e:.3e}", flush=True)
+    assert e <= 1e-5
+
+
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 def test_c5_hundred_steps(oracle, dtype):
     import dpep
