@@ -71,6 +71,12 @@ _SIGNATURES = {
     "dpep_get_scatter_density": (ctypes.c_int, [_vp, _vp]),
     "dpep_host_alloc": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(_vp)]),
     "dpep_host_free": (ctypes.c_int, [_vp]),
+    "dpep_step_device_noalloc": (ctypes.c_int, [ctypes.c_int, ctypes.c_int,
+                                                ctypes.c_double, ctypes.c_double,
+                                                ctypes.c_double, ctypes.c_double,
+                                                ctypes.c_int, ctypes.c_uint, ctypes.c_int,
+                                                _vp, _vp, _vp, _vp, _vp, ctypes.c_int,
+                                                _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

@@ -178,6 +178,27 @@ int dpep_step_device(dpep_ctx* ctx, const void* d_px, const void* d_py,
                      void* d_potential, void* d_grad_x, void* d_grad_y,
                      void* stream);
 
+/* dpep_step_device without a context, allocating nothing: no counterpart in
+ * the reference.  It is for callers that cannot allocate device memory --
+ * code under HIP graph capture, fixed serving loops.  Arguments as
+ * dpep_create (grid, die, dtype, flags among DETERMINISTIC, NO_POTENTIAL,
+ * NO_STRETCH, NO_GATHER; nc_max sizes the fixed-point scale exactly as
+ * there) plus the initial density (device, M*N; NULL = zero) and the
+ * dpep_step_device arguments; every output the step computes must be given
+ * (no context buffers to fall back on).  All scratch comes from one 64 MiB
+ * device array per GPU, held until the process ends (e.g. 1024 x 1024 bins
+ * with 2^19 float32 cells fit); a larger problem fails with DPEP_ERR_ARG
+ * and the size it needs.  Calls that overlap on one GPU share that array and
+ * race: serialise them.  Asynchronous on `stream` (NULL = the null stream);
+ * launches only kernels (no memset, no allocation, no host wait). */
+int dpep_step_device_noalloc(int num_bins_x, int num_bins_y, double xl, double yl,
+                             double xh, double yh, int dtype, unsigned flags,
+                             int nc_max, const void* d_initial_density,
+                             const void* d_px, const void* d_py, const void* d_sx,
+                             const void* d_sy, int nc, void* d_field_x,
+                             void* d_field_y, void* d_density, void* d_potential,
+                             void* d_grad_x, void* d_grad_y, void* stream);
+
 /* Per-stage milliseconds of the last step (DPEP_NUM_TIMINGS floats), the
  * values the reference server wrote into the shm header (:1798-1808). */
 int dpep_get_timings(dpep_ctx* ctx, float* out);
