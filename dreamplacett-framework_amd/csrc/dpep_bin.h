@@ -380,9 +380,14 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_count(
 
 // ---------------------------------------------------------------------------
 // K3: fill the strip-sorted records; tall cells go to B; pos[i] for G2.
+// Two forms.  This one stores each record straight to its slot (one 16- and
+// one 4-byte store per record): at a few hundred strips a workgroup's run in
+// a strip holds several records and the L2 merges the runs' partial lines;
+// it needs no staging LDS, so every workgroup is resident at once.
+// LDS: cur[S] | tot[S] | tmp[kBinThreads] | cand[kChunkCands].
 // ---------------------------------------------------------------------------
 template <typename T>
-__global__ __launch_bounds__(kBinThreads) void k_bin_fill(
+__global__ __launch_bounds__(kBinThreads) void k_bin_fill_direct(
     const T* __restrict__ px, const T* __restrict__ py,
     const T* __restrict__ sx, const T* __restrict__ sy, int nc, Grid g,
     BinArgs b)
@@ -445,6 +450,181 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill(
             b.recm[p1] = span_word(c.bxl - (s1 << b.lgR), nx, ny, c.byl);
         }
         b.pos[i] = pos_pair(p0, p1);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// K3, staged form, for grids of many strips (a workgroup's run in a strip
+// is then one or two records, and straight stores become one partial line
+// each: 2.8x the record bytes written at 4096 x 4096).
+// A workgroup's records of one strip occupy one run of the strip's range
+// (its base from strip_offsets).  They are ranked per strip (LDS atomics),
+// staged in LDS in strip order (the block's counting sort) and copied out
+// with consecutive threads on consecutive slots, so a wave's stores cover
+// whole runs instead of one scattered 16- and 4-byte store per record: the
+// lines of a run are written whole, by one workgroup, at once.  A staged
+// slot's strip is found again by a binary search of the strip offsets, so
+// the stage holds only the records (20 bytes each at float32) and five
+// workgroups fit a CU: one round at 1.1 M cells.  Records past kStage
+// slots go straight to their place.
+// LDS: cur[S] | cnt[S] | tmp[kBinThreads + kChunkCands] | off[S + 1] |
+// staged geometry[kStage] | staged span words[kStage].
+// ---------------------------------------------------------------------------
+constexpr int kStage = 1344;   // about the records of a 1024-cell block (1.3 to
+                               // 1.4 per cell), so five workgroups fit a CU
+
+// The staged form from this many strips on: fewer strips give longer runs,
+// whose straight stores the L2 already merges, and the stage's scans and
+// LDS then cost more than they save (measured on MI355X: 64 strips
+// +4.5 us, 256 strips even, 1024 strips -25 us).
+constexpr int kStageMinStrips = 512;
+
+template <typename T>
+__host__ __device__ constexpr size_t fill_lds_staged(int S)
+{
+    return ((size_t)(3 * S + 1 + kBinThreads + kChunkCands) * sizeof(unsigned) + 15) / 16 * 16 +
+           (size_t)kStage * (sizeof(vec4_t<T>) + sizeof(unsigned));
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBinThreads, 5) void k_bin_fill_staged(
+    const T* __restrict__ px, const T* __restrict__ py,
+    const T* __restrict__ sx, const T* __restrict__ sy, int nc, Grid g,
+    BinArgs b)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int S = b.S;
+    unsigned* cur = reinterpret_cast<unsigned*>(smem);
+    unsigned* cnt = cur + S;              // strip totals, then this block's counts
+    unsigned* tmp = cnt + S;
+    unsigned* off = tmp + kBinThreads + kChunkCands;   // S + 1 entries
+    vec4_t<T>* sg = reinterpret_cast<vec4_t<T>*>(
+        smem + ((size_t)(3 * S + 1 + kBinThreads + kChunkCands) * sizeof(unsigned) + 15) / 16 *
+                   16);
+    unsigned* sm = reinterpret_cast<unsigned*>(sg + kStage);
+    const int tid = threadIdx.x;
+    // the cells' loads are issued first: their latency overlaps the offsets
+    const int c0 = blockIdx.x * kCellsPerGroup;
+    T cx[kCellsPerThread], cy[kCellsPerThread], cw[kCellsPerThread], chh[kCellsPerThread];
+    load_cells(px, py, sx, sy, nc, c0, tid, cx, cy, cw, chh);
+    strip_offsets(b, cur, cnt, tmp);
+    __syncthreads();
+    for (int s = tid; s < S; s += kBinThreads) cnt[s] = 0u;
+    __syncthreads();
+    vec4_t<T>* recg = reinterpret_cast<vec4_t<T>*>(b.recg);
+    unsigned long long* Bm = reinterpret_cast<unsigned long long*>(b.B);
+    // per cell: its record geometry, span words, strips and ranks in them
+    vec4_t<T> geo[kCellsPerThread];
+    unsigned m0[kCellsPerThread], m1[kCellsPerThread], r0[kCellsPerThread],
+        r1[kCellsPerThread];
+    int s0v[kCellsPerThread], s1v[kCellsPerThread];
+#pragma unroll
+    for (int j = 0; j < kCellsPerThread; ++j) {
+        s0v[j] = s1v[j] = -1;
+        const int i = c0 + tid + j * kBinThreads;
+        if (i >= nc) continue;
+        CellSpan c;
+        if (!cell_span((double)cx[j], (double)cy[j], (double)cw[j], (double)chh[j], g, c)) {
+            b.pos[i] = pos_pair(kPosNone, kPosNone);
+            continue;
+        }
+        int s0, s1;
+        bool tall;
+        cell_strips(c, b.R, b.lgR, s0, s1, tall);
+        if (tall) {
+            const double sc = c.ratio() * g.inv_ba;
+            for (int k = c.bxl; k <= c.bxh; ++k) {
+                const double tx = overlap_1d(c.x, c.w, g.xl, g.bsx, k);
+                if (tx <= 0.0) continue;
+                const double stx = sc * tx;
+                const size_t rowi = (size_t)k * g.N;
+                for (int q = c.byl; q <= c.byh; ++q) {
+                    const double ty = overlap_1d(c.y, c.h, g.yl, g.bsy, q);
+                    if (ty <= 0.0) continue;
+                    atomicAdd(&Bm[rowi + q], to_fixed(stx * ty, g.fix_scale));
+                }
+            }
+            // the column blocks of B this cell touches, in each of its strips
+            const int CB = side_block(g.N);
+            for (int s = s0; s <= s1; ++s)
+                side_mark(b.bigflag + (size_t)s * kSideWords, c.byl, c.byh, CB);
+            b.pos[i] = pos_pair(kPosTall, kPosNone);
+            continue;
+        }
+        // strip-relative record, evaluated in float64 and rounded once
+        const double ex = (c.x - (g.xl + c.bxl * g.bsx)) * g.inv_bsx;
+        const double ey = (c.y - (g.yl + c.byl * g.bsy)) * g.inv_bsy;
+        geo[j] = {(T)ex, (T)ey, (T)((double)cw[j] * g.inv_bsx),
+                  (T)((double)chh[j] * g.inv_bsy)};
+        const int nx = c.bxh - c.bxl, ny = c.byh - c.byl;
+        s0v[j] = s0;
+        m0[j] = span_word(c.bxl - (s0 << b.lgR), nx, ny, c.byl);
+        r0[j] = atomicAdd(&cnt[s0], 1u);
+        if (s1 != s0) {
+            s1v[j] = s1;
+            m1[j] = span_word(c.bxl - (s1 << b.lgR), nx, ny, c.byl);
+            r1[j] = atomicAdd(&cnt[s1], 1u);
+        }
+    }
+    __syncthreads();
+    // offsets of the strips' runs within the block: exclusive scan of cnt
+    unsigned nrec;
+    {
+        const int per = (S + kBinThreads - 1) / kBinThreads;
+        const int a0 = min(tid * per, S), a1 = min(a0 + per, S);
+        unsigned run = 0u;
+        for (int s = a0; s < a1; ++s) run += cnt[s];
+        unsigned base = block_exclusive_scan(run, tmp, nrec);
+        for (int s = a0; s < a1; ++s) {
+            off[s] = base;
+            base += cnt[s];
+        }
+        if (tid == 0) off[S] = nrec;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kCellsPerThread; ++j) {
+        if (s0v[j] < 0) continue;
+        const int i = c0 + tid + j * kBinThreads;
+        const unsigned k0 = off[s0v[j]] + r0[j], d0 = cur[s0v[j]] + r0[j];
+        if (k0 < (unsigned)kStage) {
+            sg[k0] = geo[j];
+            sm[k0] = m0[j];
+        } else {
+            recg[d0] = geo[j];
+            b.recm[d0] = m0[j];
+        }
+        unsigned d1 = kPosNone;
+        if (s1v[j] >= 0) {
+            const unsigned k1 = off[s1v[j]] + r1[j];
+            d1 = cur[s1v[j]] + r1[j];
+            if (k1 < (unsigned)kStage) {
+                sg[k1] = geo[j];
+                sm[k1] = m1[j];
+            } else {
+                recg[d1] = geo[j];
+                b.recm[d1] = m1[j];
+            }
+        }
+        b.pos[i] = pos_pair(d0, d1);
+    }
+    __syncthreads();
+    // staged records out, consecutive threads on consecutive slots: slot k
+    // belongs to the last strip s with off[s] <= k (empty strips share
+    // their successor's offset and are passed over), at cur[s] + k - off[s]
+    const unsigned ns = nrec < (unsigned)kStage ? nrec : (unsigned)kStage;
+    int lg = 0;
+    while ((1 << lg) < S + 1) ++lg;
+    for (unsigned k = tid; k < ns; k += kBinThreads) {
+        int lo = 0, hi = S;                   // off[lo] <= k < off[hi]
+        for (int q = 0; q < lg; ++q) {
+            const int mid = (lo + hi) >> 1;
+            if (mid > lo && off[mid] <= k) lo = mid;
+            else if (mid > lo) hi = mid;
+        }
+        const unsigned d = cur[lo] + (k - off[lo]);
+        recg[d] = sg[k];
+        b.recm[d] = sm[k];
     }
 }
 

@@ -45,12 +45,17 @@ hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
     b.G1 = (int)g1_of(nc);
     if (b.R != strip_rows(g.N)) return hipErrorInvalidValue;   // the kernel's R
     const size_t count_lds = (size_t)b.S * sizeof(unsigned);
-    const size_t fill_lds = (size_t)(2 * b.S + kBinThreads + kChunkCands) * sizeof(unsigned);
+    const bool staged = b.S >= kStageMinStrips;
+    const size_t fill_lds = staged ? fill_lds_staged<T>(b.S)
+                                   : (size_t)(2 * b.S + kBinThreads + kChunkCands) * sizeof(unsigned);
     hipError_t e;
     k_bin_count<T><<<b.G1, kBinThreads, count_lds, s>>>(px, py, sx, sy, nc, g, b);
     if ((e = hipGetLastError())) return e;
     if (ev && (e = hipEventRecord(ev[0], s))) return e;
-    k_bin_fill<T><<<b.G1, kBinThreads, fill_lds, s>>>(px, py, sx, sy, nc, g, b);
+    if (staged)
+        k_bin_fill_staged<T><<<b.G1, kBinThreads, fill_lds, s>>>(px, py, sx, sy, nc, g, b);
+    else
+        k_bin_fill_direct<T><<<b.G1, kBinThreads, fill_lds, s>>>(px, py, sx, sy, nc, g, b);
     if ((e = hipGetLastError())) return e;
     if (ev && (e = hipEventRecord(ev[1], s))) return e;
     e = dispatch_n<T>(g.N, [&](auto lc) -> hipError_t {
@@ -130,6 +135,11 @@ static hipError_t prepare_bin_type()
                                        (int)acc_lds_bytes<T, L>());
         });
     if (e) return e;
+    // K3's LDS grows with the strips: at most 8192 / 2 (float32) or 4096 / 4
+    if ((e = hipFuncSetAttribute((const void*)k_bin_fill_staged<T>,
+                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 (int)fill_lds_staged<T>(sizeof(T) == 4 ? 4096 : 1024))))
+        return e;
     return hipFuncSetAttribute((const void*)k_gather_bin<T>,
                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)kTileBytes);

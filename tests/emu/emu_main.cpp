@@ -98,7 +98,7 @@ static std::vector<T> table(int L, bool post)
 }
 
 template <typename T, int LM, int LN>
-static int run(int nc, bool det, bool pot, int ch, bool tall)
+static int run(int nc, bool det, bool pot, int ch, bool tall, bool force_stage)
 {
     using namespace dpep;
     const int M = LM, N = LN;
@@ -176,11 +176,17 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
     memset(b.B, 0, mn * 8);
     memset(b.bigflag, 0, kSideWords * p.S * sizeof(unsigned));
     const size_t hist = (size_t)p.S * sizeof(unsigned);
+    // the library stages K3's records from kStageMinStrips strips on; "stage"
+    // forces the staged form on any grid
+    const bool stage = force_stage || p.S >= kStageMinStrips;
     for (int rep = 0; rep < 2; ++rep) {   // two steps: B / flags must be clean again
         launch(b.G1, kBinThreads, hist, [&] { k_bin_count<T>(px, py, sx, sy, nc, g, b); });
-        launch(b.G1, kBinThreads,
-               (size_t)(2 * p.S + kBinThreads + kChunkCands) * sizeof(unsigned),
-               [&] { k_bin_fill<T>(px, py, sx, sy, nc, g, b); });
+        if (stage)
+            launch(b.G1, kBinThreads, fill_lds_staged<T>(p.S),
+                   [&] { k_bin_fill_staged<T>(px, py, sx, sy, nc, g, b); });
+        else
+            launch(b.G1, kBinThreads, (size_t)(2 * p.S + kBinThreads + kChunkCands) * sizeof(unsigned),
+                   [&] { k_bin_fill_direct<T>(px, py, sx, sy, nc, g, b); });
         launch(b.Wacc, kAccThreads, acc_lds_bytes<T, LN>(),
                [&] { k_strip_acc<T, LN>(g, b, a, d0n, dens, Tt); });
         for (int s2 = 0; s2 < p.S; ++s2)
@@ -246,9 +252,9 @@ static int run(int nc, bool det, bool pot, int ch, bool tall)
 }
 
 template <typename T>
-static int dispatch(int M, int N, int nc, bool det, bool pot, int ch, bool tall)
+static int dispatch(int M, int N, int nc, bool det, bool pot, int ch, bool tall, bool stage)
 {
-#define CASE(a, b) if (M == a && N == b) return run<T, a, b>(nc, det, pot, ch, tall);
+#define CASE(a, b) if (M == a && N == b) return run<T, a, b>(nc, det, pot, ch, tall, stage);
     CASE(8, 8) CASE(16, 16) CASE(8, 32) CASE(64, 64) CASE(16, 128) CASE(128, 16)
     CASE(256, 32) CASE(32, 256) CASE(32, 2048) CASE(16, 4096)
     if constexpr (sizeof(T) == 4) { CASE(8, 8192) }
@@ -262,14 +268,15 @@ int main(int argc, char** argv)
     if (argc < 5) { fprintf(stderr, "usage: %s f32|f64 M N nc [det] [nopot]\n", argv[0]); return 2; }
     const bool f64 = !strcmp(argv[1], "f64");
     const int M = atoi(argv[2]), N = atoi(argv[3]), nc = atoi(argv[4]);
-    bool det = false, pot = true, tall = false;
+    bool det = false, pot = true, tall = false, stage = false;
     int ch = 0;
     for (int i = 5; i < argc; ++i) {
         if (!strcmp(argv[i], "det")) det = true;
         if (!strcmp(argv[i], "nopot")) pot = false;
         if (!strcmp(argv[i], "tall")) tall = true;
+        if (!strcmp(argv[i], "stage")) stage = true;
         if (!strncmp(argv[i], "ch=", 3)) ch = atoi(argv[i] + 3);
     }
-    return f64 ? dispatch<double>(M, N, nc, det, pot, ch, tall)
-               : dispatch<float>(M, N, nc, det, pot, ch, tall);
+    return f64 ? dispatch<double>(M, N, nc, det, pot, ch, tall, stage)
+               : dispatch<float>(M, N, nc, det, pot, ch, tall, stage);
 }

@@ -37,15 +37,20 @@ def emu(tmp_path_factory):
 
 
 # ch=<n> forces n entries per strip work item (exercises the split-strip
-# reduce); tall gives a tenth of the cells a span of 3..40 rows (side map B).
+# reduce); tall gives a tenth of the cells a span of 3..40 rows (side map B);
+# stage forces K3's staged form (the library picks it from 512 strips on).
 CASES = [
     "f32 8 8 50", "f32 16 16 200 tall", "f32 8 32 60 nopot", "f32 16 128 3000 ch=128",
     "f32 128 16 300", "f64 8 8 40", "f64 64 64 1000 ch=100 tall",
     "f32 64 64 2000 ch=64 tall", "f32 256 32 600", "f32 32 256 400 tall",
-    "f32 32 2048 500",
+    "f32 32 2048 500", "f64 32 2048 300 tall",
+    "f32 32 2048 0",         # no cells: the last kernel runs the potential alone
+    "f32 32 2048 400 nopot",
     "f32 16 4096 2000 tall", "f64 16 4096 100",
     "f32 16 128 9000 tall",  # chunks chosen per step: both strips split
     "f32 8 8192 3000 tall",  # 2-row strips, the largest LDS tile and row FFT
+    "f32 64 64 2000 tall stage", "f64 64 64 1500 ch=100 stage",
+    "f32 16 128 9000 tall stage",  # blocks beyond the stage: records stored straight
 ]
 
 
