@@ -14,6 +14,7 @@ HBM before the timed region; one step = one dpep_compute() on them.
 Prints ONE JSON line (the driver's contract).
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -31,7 +32,8 @@ import numpy as np  # noqa: E402
 HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "kernels_c3_1.1M_2048.md")
 # kernel name prefix in the rocprofv3 summary for each bench kernel key
-PMC_NAMES = {"bin_count": "k_bin_count", "bin_fill": "k_bin_fill",
+PMC_NAMES = {"bin_count": "k_bin_count",
+             "bin_fill": ("k_bin_fill_direct", "k_bin_fill_staged"),
              "strip_acc": "k_strip_acc",
              "col_pass": "k_col_pass", "row_inv": "k_row_inv",
              "gather_bin": "k_gather_bin", "gather_out": "k_gather_out"}
@@ -75,7 +77,7 @@ def pmc_traffic(key):
                   any(cols[0].startswith(n + "<") for n in names)):
                 total += float(cols[col]) * 1e6
                 found += 1
-    return round(total) if found == len(names) else None
+    return round(total) if found else None
 
 
 def step_bytes(nc, M, N, esz, potential=True):
@@ -135,6 +137,111 @@ def host_path(w, dtype, potential, px, py, sx, sy, steps=5):
                          "compute_ms": round(float(med[1]), 3),
                          "d2h_ms": round(float(med[2]), 3)}
     return res
+
+
+def hip_runtime():
+    """The HIP runtime libdpep.so runs on (found in this process's memory map
+    once libdpep is loaded), for the device copies below."""
+    import dpep
+    dpep.load_library()
+    path = None
+    with open("/proc/self/maps") as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) >= 6 and "libamdhip64" in os.path.basename(parts[-1]):
+                path = parts[-1]
+                break
+    if path is None:
+        raise RuntimeError("libdpep.so loaded no libamdhip64")
+    hip = ctypes.CDLL(path)
+    hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                   ctypes.c_int, ctypes.c_void_p]
+    hip.hipMemset.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t]
+    hip.hipFree.argtypes = [ctypes.c_void_p]
+    return hip
+
+
+def stream_copy(nbytes=1 << 30, reps=20):
+    """On-box STREAM-copy reference: a device-to-device copy of `nbytes`
+    (4x the 256 MB Infinity Cache), timed over `reps` copies after one
+    warm-up; GB/s counts the bytes read plus the bytes written."""
+    hip = hip_runtime()
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    assert hip.hipMalloc(ctypes.byref(a), nbytes) == 0
+    assert hip.hipMalloc(ctypes.byref(b), nbytes) == 0
+    try:
+        assert hip.hipMemset(a, 1, nbytes) == 0
+        D2D = 3
+        assert hip.hipMemcpyAsync(b, a, nbytes, D2D, None) == 0
+        assert hip.hipDeviceSynchronize() == 0
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            assert hip.hipMemcpyAsync(b, a, nbytes, D2D, None) == 0
+        assert hip.hipDeviceSynchronize() == 0
+        dt = (time.perf_counter() - t0) / reps
+    finally:
+        hip.hipFree(a)
+        hip.hipFree(b)
+    return {"gbps": round(2 * nbytes / dt / 1e9, 1), "bytes": nbytes,
+            "method": f"hipMemcpyAsync device-to-device of {nbytes >> 20} MiB, {reps} "
+                      "copies after a warm-up; (read + write bytes) / time"}
+
+
+def cold_steps(w, dtype, potential, cells, n_ctx=3, steps=60, warmup=6):
+    """The step with the Infinity Cache cold: n_ctx contexts, each with its
+    own device copy of the cells and its own buffers (about 330 MB each at
+    1.1 M cells on 2048 x 2048), stepped in rotation on one stream, so each
+    step's inputs, scratch and outputs were evicted from the 256 MB cache by
+    the other contexts' steps since its own last one.  ms per step."""
+    import dpep
+    lib = dpep.load_library()
+    hip = hip_runtime()
+    H2D = 1
+    ctxs, bufs = [], []
+    hip.hipStreamCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
+    hip.hipStreamDestroy.argtypes = [ctypes.c_void_p]
+    st = ctypes.c_void_p()            # one stream: the contexts' steps in order
+    assert hip.hipStreamCreate(ctypes.byref(st)) == 0
+    try:
+        for _ in range(n_ctx):
+            c = dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh, dtype=dtype,
+                             potential=potential)
+            c.set_initial_density(w.d0n.astype(dtype))
+            dev = []
+            for a in cells:
+                p = ctypes.c_void_p()
+                assert hip.hipMalloc(ctypes.byref(p), a.nbytes) == 0
+                bufs.append(p)
+                assert hip.hipMemcpy(p, a.ctypes.data, a.nbytes, H2D) == 0
+                dev.append(p)
+            ctxs.append((c, dev))
+
+        def step(i):
+            c, dev = ctxs[i % n_ctx]
+            rc = lib.dpep_step_device(c.handle, *dev, w.nc, None, None, None, None, None,
+                                      None, st)
+            if rc:
+                raise RuntimeError(dpep.last_error())
+
+        for i in range(warmup):
+            step(i)
+        assert hip.hipStreamSynchronize(st) == 0
+        t0 = time.perf_counter()
+        for i in range(steps):
+            step(i)
+        assert hip.hipStreamSynchronize(st) == 0
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+    finally:
+        hip.hipStreamSynchronize(st)
+        for c, _ in ctxs:
+            c.close()
+        for p in bufs:
+            hip.hipFree(p)
+        hip.hipStreamDestroy(st)
+    return round(ms, 4)
 
 
 def cpu_baseline(w, seconds, max_steps=400):
@@ -259,6 +366,14 @@ def main():
                                    if headline else None),
                 "algorithmic_bytes": kb[dom], "avg_us": round(kt[dom], 2)}
 
+    stream, cold_ms = None, None
+    if not args.no_profile:
+        cold_ms = cold_steps(w, dtype, potential, (px, py, sx, sy))
+        stream = stream_copy()
+        if roof:
+            roof["stream_gbps"] = stream["gbps"]
+            roof["frac_of_stream"] = round(roof["achieved"] / stream["gbps"], 4)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(w, args.cpu_seconds)
@@ -288,6 +403,11 @@ def main():
         "hbm_fraction_3pass_model": round(
             step_bytes_3pass(w.nc, w.M, w.N, esz, potential) / (ms * 1e-3) / HBM_PEAK, 4),
         "roofline": roof,
+        "stream_copy": stream,
+        "hbm_fraction_3pass_vs_stream": (round(
+            step_bytes_3pass(w.nc, w.M, w.N, esz, potential) / (ms * 1e-3) /
+            (stream["gbps"] * 1e9), 4) if stream else None),
+        "cold_ms_per_step": cold_ms,
         "kernel_us": {k: round(v, 2) for k, v in kt.items()} if kt else None,
         "host_step_ms": host_ms,
         "host_step": host,
