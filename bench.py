@@ -33,7 +33,7 @@ HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "kernels_c3_1.1M_2048.md")
 # kernel name prefix in the rocprofv3 summary for each bench kernel key
 PMC_NAMES = {"bin_count": "k_bin_count",
-             "bin_fill": ("k_bin_fill_direct", "k_bin_fill_staged"),
+             "bin_fill": ("k_bin_fill_direct", "k_bin_fill_staged", "k_bin_fill_once"),
              "strip_acc": "k_strip_acc",
              "col_pass": "k_col_pass", "row_inv": "k_row_inv",
              "gather_bin": "k_gather_bin", "gather_out": "k_gather_out"}
@@ -282,6 +282,10 @@ def main():
     ap.add_argument("--dtype", choices=["f32", "f64"], default="f32")
     ap.add_argument("--deterministic", action="store_true")
     ap.add_argument("--no-potential", action="store_true")
+    ap.add_argument("--two-pass", action="store_true",
+                    help="count the cells before sorting them on every step "
+                         "(by default a step sorts in one pass on the plan the "
+                         "previous step made from its counts)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="wall-clock budget of the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -308,7 +312,8 @@ def main():
     px, py, sx, sy = w.cells(dtype)
 
     ctx = dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh, dtype=dtype,
-                       deterministic=args.deterministic, potential=potential)
+                       deterministic=args.deterministic, potential=potential,
+                       two_pass=args.two_pass)
     ctx.set_initial_density(w.d0n.astype(dtype))
     ctx.set_cells(px, py, sx, sy)          # inputs resident in HBM from here
     for _ in range(args.warmup):
@@ -397,6 +402,9 @@ def main():
             "cells": w.nc, "bins_x": w.M, "bins_y": w.N,
             "deterministic": bool(args.deterministic), "potential": potential,
             "gather": True,
+            "binning": ("two-pass (count, then sort) every step" if args.two_pass else
+                        "one pass on the plan the previous step made from its counts "
+                        "(the first step counts first)"),
         },
         "hbm_fraction_step": round(bstep / (ms * 1e-3) / HBM_PEAK, 4),
         "step_bytes": bstep,

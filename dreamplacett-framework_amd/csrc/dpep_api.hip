@@ -88,6 +88,12 @@ struct dpep_ctx {
     int nc = -1;                 // resident cells (-1: none uploaded)
     int last_nc = 0;             // cells of the last computed step
     int stepped = 0;
+    // the last step left its counts for this one (parity par ^ 1): fill in
+    // one pass.  A failed step leaves the counts in an unknown state: the
+    // next one re-zeroes both sets and counts first.
+    int planned = 0;
+    int scrub = 0;
+    int par = 0;                 // parity of the next step's set of counts
     // which of the context's own output buffers hold the last step's results
     // (kOut* bits): a step on caller-owned outputs leaves the others stale,
     // and new cells uploaded after the step make every output stale
@@ -129,8 +135,8 @@ static void release(dpep_ctx* c)
     void* bufs[] = {c->d_px, c->d_py, c->d_sx, c->d_sy, c->d_d0n,
                     c->d_density, c->d_potential, c->d_fx, c->d_fy, c->d_gx,
                     c->d_gy, c->d_T, c->d_Ux, c->d_Uy, c->d_twM,
-                    c->d_postM, c->d_twN, c->d_postN, b.cnt, b.xtot, b.strip_off,
-                    b.nch, b.item_start, b.items, b.nitems, b.done, b.recg,
+                    c->d_postM, c->d_twN, c->d_postN, b.cnt, b.xtot, b.pbase,
+                    b.pcap, b.pool_n, b.pstrip, b.items, b.nitems, b.done, b.recg,
                     b.recm, b.pos, b.gtmp,
                     b.bigflag, b.B, b.chunk, b.items_g, c->d_raw};
     for (void* p : bufs)
@@ -162,13 +168,23 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
         !fy || !c->d_T || !c->d_Ux || !c->d_Uy || (a.potential && !phi) ||
         !b.xtot ||
         (nc > 0 && (!px || !py || !sx || !sy)) ||
-        (gather && (!gx || !gy)) || !b.cnt || !b.strip_off || !b.nch ||
-        !b.item_start || !b.items || !b.nitems || !b.done || !b.recg ||
+        (gather && (!gx || !gy)) || !b.cnt || !b.pbase || !b.pcap ||
+        !b.pool_n || !b.pstrip || !b.items || !b.nitems || !b.done || !b.recg ||
         !b.recm || !b.pos ||
         !b.gtmp || !b.bigflag || !b.B || !b.chunk || !b.items_g)
         return fail(DPEP_ERR_STATE, "internal: a kernel argument is NULL");
     if (nc > c->nc_max)
         return fail(DPEP_ERR_ARG, "nc=%d exceeds nc_max=%d", nc, c->nc_max);
+    if (c->scrub) {
+        HIP_TRY(hipMemsetAsync(b.xtot, 0, 2 * (size_t)kCountSlots * b.S * sizeof(unsigned), s));
+        HIP_TRY(hipMemsetAsync(b.pool_n, 0, 2 * sizeof(unsigned), s));
+        c->scrub = 0;
+    }
+    // one pass over the cells when the previous step left its counts
+    const bool once = c->planned && !(c->flags & DPEP_FLAG_TWO_PASS);
+    c->bins.par = c->par;
+    c->planned = 0;
+    c->scrub = 1;                 // until the step's last launch succeeds
 
     // with profiling on, this step's stage boundaries go to one ring slot
     hipEvent_t* pe = prof ? &c->prof_ev[(size_t)(c->prof_steps % c->prof_slots) *
@@ -180,7 +196,7 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
     if (timed) HIP_TRY(hipEventRecord(c->ev[0], s));
     if (prof) HIP_TRY(hipEventRecord(pe[0], s));
     HIP_TRY(launch_bin_scatter<T>(px, py, sx, sy, nc, c->grid, c->bins, c->sargs, d0n,
-                                  dens, (T*)c->d_T, s, prof ? pe + 1 : nullptr));
+                                  dens, (T*)c->d_T, once, s, prof ? pe + 1 : nullptr));
 
     HIP_TRY(launch_col_pass<T>(c->sargs, (T*)c->d_T, (T*)c->d_Ux, (T*)c->d_Uy, s));
     if (prof) HIP_TRY(hipEventRecord(pe[4], s));
@@ -192,6 +208,9 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
                                      gx, gy, s, prof ? pe[6] : nullptr));
     else if (prof)
         HIP_TRY(hipEventRecord(pe[6], s));
+    c->planned = 1;
+    c->scrub = 0;
+    c->par ^= 1;
     if (prof) HIP_TRY(hipEventRecord(pe[kNumStages], s));
     if (timed) HIP_TRY(hipEventRecord(c->ev[kNumStages], s));
     if (prof) c->prof_steps++;
@@ -261,7 +280,7 @@ int dpep_abi_version(void) { return DPEP_ABI_VERSION; }
 
 const char* dpep_build_info(void)
 {
-    return "dpep abi 3; HIP kernels for gfx950; scatter/P1/P2/P3/gather";
+    return "dpep abi 4; HIP kernels for gfx950; scatter/P1/P2/P3/gather";
 }
 
 const char* dpep_last_error(void) { return g_last_error.c_str(); }
@@ -278,14 +297,15 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
         return fail(DPEP_ERR_UNSUPPORTED,
                     "num_bins_x=%d num_bins_y=%d: both must be powers of two in [8, %d]",
                     M, N, maxL);
-    if (nc_max < 0) return fail(DPEP_ERR_ARG, "nc_max=%d must be >= 0", nc_max);
+    if (nc_max < 0 || nc_max > kMaxCells)
+        return fail(DPEP_ERR_ARG, "nc_max=%d must be in [0, %d]", nc_max, kMaxCells);
     if (!(xh > xl) || !(yh > yl) || !isfinite(xl) || !isfinite(yl) ||
         !isfinite(xh) || !isfinite(yh))
         return fail(DPEP_ERR_ARG, "die [%g,%g]x[%g,%g] is empty or not finite",
                     xl, xh, yl, yh);
     if (flags & ~(DPEP_FLAG_DETERMINISTIC | DPEP_FLAG_NO_POTENTIAL |
                   DPEP_FLAG_NO_STRETCH | DPEP_FLAG_NO_GATHER | DPEP_FLAG_STEP_TIMINGS |
-                  DPEP_FLAG_SCATTER_DENSITY))
+                  DPEP_FLAG_SCATTER_DENSITY | DPEP_FLAG_TWO_PASS))
         return fail(DPEP_ERR_ARG, "unknown flag bits 0x%x", flags);
 
     if (const hipError_t e = prepare_kernels())
@@ -333,21 +353,30 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
             set_item_grids(b, acc, gat, cus);
         }
         HIP_TRY(hipMalloc((void**)&b.cnt, (size_t)p.G1max * p.S * sizeof(unsigned)));
-        HIP_TRY(hipMalloc((void**)&b.xtot, (size_t)kCountSlots * p.S * sizeof(unsigned)));
-        HIP_TRY(hipMemset(b.xtot, 0, (size_t)kCountSlots * p.S * sizeof(unsigned)));
-        HIP_TRY(hipMalloc((void**)&b.strip_off, (size_t)(p.S + 1) * sizeof(unsigned)));
-        HIP_TRY(hipMalloc((void**)&b.nch, (size_t)p.S * sizeof(unsigned)));
-        HIP_TRY(hipMalloc((void**)&b.item_start, (size_t)p.S * sizeof(unsigned)));
+        // two sets of (slot, strip) counts: this step's and the last one's
+        HIP_TRY(hipMalloc((void**)&b.xtot, 2 * (size_t)kCountSlots * p.S * sizeof(unsigned)));
+        HIP_TRY(hipMemset(b.xtot, 0, 2 * (size_t)kCountSlots * p.S * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.pbase, (size_t)kCountSlots * p.S * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.pcap, (size_t)kCountSlots * p.S * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.pool_n, 2 * sizeof(unsigned)));
+        HIP_TRY(hipMemset(b.pool_n, 0, 2 * sizeof(unsigned)));
+        // records: the plan's regions, then an overflow pool of one slot per
+        // possible record
+        b.reg_cap = (unsigned)p.reg_cap;
+        b.pool0 = (unsigned)p.reg_cap;
+        b.pool_cap = (unsigned)p.cap;
+        const size_t nrec = p.reg_cap + p.cap;
+        HIP_TRY(hipMalloc((void**)&b.pstrip, p.cap * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.items, (size_t)b.Wacc * sizeof(uint4)));
         HIP_TRY(hipMalloc((void**)&b.items_g, (size_t)b.Wgat * sizeof(uint4)));
         HIP_TRY(hipMalloc((void**)&b.nitems, 2 * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.chunk, 2 * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.done, (size_t)p.S * sizeof(unsigned)));
         HIP_TRY(hipMemset(b.done, 0, (size_t)p.S * sizeof(unsigned)));
-        HIP_TRY(hipMalloc(&b.recg, p.cap * p.geo_bytes));
-        HIP_TRY(hipMalloc((void**)&b.recm, p.cap * sizeof(unsigned)));
+        HIP_TRY(hipMalloc(&b.recg, nrec * p.geo_bytes));
+        HIP_TRY(hipMalloc((void**)&b.recm, nrec * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.pos, (size_t)(nc_max > 0 ? nc_max : 1) * sizeof(unsigned long long)));
-        HIP_TRY(hipMalloc(&b.gtmp, p.cap * 2 * c->esz));
+        HIP_TRY(hipMalloc(&b.gtmp, nrec * 2 * c->esz));
         HIP_TRY(hipMalloc((void**)&b.bigflag, (size_t)kSideWords * p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc(&b.B, (size_t)M * N * accb));
         // B and the strip flags must start at zero; each step leaves them so.

@@ -149,19 +149,20 @@ __device__ __forceinline__ bool load_span(const T* px, const T* py,
                      (double)sy[i], g, c);
 }
 
-// The kCellsPerThread cells of thread tid in the workgroup's block starting
-// at c0 (zero past nc).  A full block loads unconditionally: with a branch per
-// cell the compiler moves each float32 -> float64 conversion into the branch
-// and waits there for the load, so the four cells' loads no longer overlap.
-template <typename T>
+// The kCellsPerThread cells of thread tid in the block of NT * kCellsPerThread
+// cells starting at c0 (zero past nc).  A full block loads unconditionally:
+// with a branch per cell the compiler moves each float32 -> float64
+// conversion into the branch and waits there for the load, so the four
+// cells' loads no longer overlap.
+template <typename T, int NT = kBinThreads>
 __device__ __forceinline__ void load_cells(const T* __restrict__ px, const T* __restrict__ py,
                                            const T* __restrict__ sx, const T* __restrict__ sy,
                                            int nc, int c0, int tid, T* cx, T* cy, T* cw, T* ch)
 {
-    if (c0 + kCellsPerGroup <= nc) {
+    if (c0 + NT * kCellsPerThread <= nc) {
 #pragma unroll
         for (int j = 0; j < kCellsPerThread; ++j) {
-            const int i = c0 + tid + j * kBinThreads;
+            const int i = c0 + tid + j * NT;
             cx[j] = px[i];
             cy[j] = py[i];
             cw[j] = sx[i];
@@ -170,7 +171,7 @@ __device__ __forceinline__ void load_cells(const T* __restrict__ px, const T* __
     } else {
 #pragma unroll
         for (int j = 0; j < kCellsPerThread; ++j) {
-            const int i = c0 + tid + j * kBinThreads;
+            const int i = c0 + tid + j * NT;
             const bool ok = i < nc;
             cx[j] = ok ? px[i] : (T)0;
             cy[j] = ok ? py[i] : (T)0;
@@ -193,94 +194,95 @@ __device__ __forceinline__ unsigned long long to_fixed(float v, float scale)
 }
 
 // ---------------------------------------------------------------------------
-// Strip table: strip_off = exclusive scan of the strip totals, the first
-// entry of each (workgroup, strip), the chunk list.  Built in K3's prologue.
+// The plan: regions of the (slot, strip) pairs and the K4 / G1 work items.
 // ---------------------------------------------------------------------------
+// Exclusive prefix sum of one value per thread over the NT threads of a
+// workgroup: a shuffle scan within each wave, then the waves' totals through
+// LDS (two barriers; a Hillis-Steele scan in LDS took sixteen).
+// tmp: NT / 64 words.
+constexpr int kWave = 64;
+
+template <int NT = kBinThreads>
 __device__ __forceinline__ unsigned block_exclusive_scan(unsigned v,
                                                          unsigned* tmp,
                                                          unsigned& total)
 {
-    // Hillis-Steele over kBinThreads values in LDS.
-    const int tid = threadIdx.x;
-    tmp[tid] = v;
-    __syncthreads();
-    for (int off = 1; off < kBinThreads; off <<= 1) {
-        const unsigned a = tid >= off ? tmp[tid - off] : 0u;
-        __syncthreads();
-        tmp[tid] += a;
-        __syncthreads();
+    constexpr int kBinWaves = NT / kWave;
+    const int tid = threadIdx.x, lane = tid % kWave, wv = tid / kWave;
+    unsigned x = v;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const unsigned y = __shfl_up(x, (unsigned)o, kWave);
+        if (lane >= o) x += y;
     }
-    const unsigned incl = tmp[tid];
-    total = tmp[kBinThreads - 1];
+    if (lane == kWave - 1) tmp[wv] = x;
     __syncthreads();
-    return incl - v;
+    unsigned before = 0u, all = 0u;
+#pragma unroll
+    for (int k = 0; k < kBinWaves; ++k) {
+        const unsigned t = tmp[k];
+        before += k < wv ? t : 0u;
+        all += t;
+    }
+    total = all;
+    __syncthreads();
+    return before + x - v;
 }
 
-// Offsets of this K3 workgroup's strip entries, from K1's slot totals: every
-// workgroup scans the strip totals itself (S values, a few microseconds of
-// L2 reads spread over the grid) instead of one workgroup building a table
-// behind all of K1.  cur[s] = first entry of workgroup g in strip s =
-// strip offset + totals of the slots before g's + g's base within its slot.
-// Workgroup 0 also publishes the strip table for K4 / G1 (strip offsets,
-// chunk sizes and counts, the two work-item lists).  LDS: cur[S] | tot[S] |
-// tmp[kBinThreads] | cand[kChunkCands].
-__device__ __forceinline__ void strip_offsets(const BinArgs& b, unsigned* cur,
-                                              unsigned* tot, unsigned* tmp)
+// The (slot, strip) counts of the step of parity par: [kCountSlots][S].
+__device__ __forceinline__ unsigned* counts_of(const BinArgs& b, int par)
 {
-    const int tid = threadIdx.x;
-    const int S = b.S;
-    const int x = (int)(blockIdx.x % kCountSlots);
-    const unsigned* row = b.cnt + (size_t)blockIdx.x * S;
-    for (int s = tid; s < S; s += kBinThreads) {
-        unsigned t = 0u, pre = 0u;
-#pragma unroll
-        for (int xx = 0; xx < kCountSlots; ++xx) {
-            const unsigned v = b.xtot[(size_t)xx * S + s];
-            pre += xx < x ? v : 0u;
-            t += v;
-        }
-        tot[s] = t;
-        cur[s] = pre + row[s];
-    }
-    __syncthreads();
-    // exclusive scan of the strip totals (each thread a run of strips)
-    const int per = (S + kBinThreads - 1) / kBinThreads;
-    const int r0 = min(tid * per, S), r1 = min(r0 + per, S);
-    unsigned run = 0u;
-    for (int s = r0; s < r1; ++s) run += tot[s];
-    unsigned total;
-    unsigned base = block_exclusive_scan(run, tmp, total);
-    const unsigned base0 = base;              // offset of strip r0
-    const bool pub = blockIdx.x == 0;         // uniform across the group
-    for (int s = r0; s < r1; ++s) {
-        const unsigned t = tot[s];
-        cur[s] += base;
-        if (pub) b.strip_off[s] = base;
-        base += t;
-    }
-    if (!pub) return;
-    if (tid == 0) b.strip_off[S] = total;
-    // Chunk sizes of this step: the smallest kChunkMin << k whose item count
-    // sum_s max(1, ceil(t_s / chunk)) fits the workgroups the device holds at
-    // once (Pacc for K4, Pgat for G1), so a skewed placement spreads its heavy
-    // strips over otherwise idle CUs; every strip in one item when even the
-    // largest does not fit.
-    unsigned* cand = tmp + kBinThreads;
-    for (int k = tid; k < kChunkCands; k += kBinThreads) cand[k] = 0u;
-    __syncthreads();
+    return b.xtot + (size_t)(par & 1) * kCountSlots * b.S;
+}
+
+// Chunk sizes and the K4 / G1 work items from the strip totals tot[S] (LDS,
+// the totals the plan expects), by one workgroup of NT threads; thread tid
+// owns strips [r0, r1).  The chunk size of a list is the smallest
+// kChunkMin << k whose item count sum_s max(1, ceil(t_s / chunk)) fits the
+// workgroups the device holds at once (Pacc for K4, Pgat for G1), so a
+// skewed placement spreads its heavy strips over otherwise idle CUs; every
+// strip in one item when even the largest does not fit.  An item is
+// {strip | chunk << 16, first, end strip-relative record, chunks of the
+// strip}; the last chunk of a strip runs to the strip's actual end.
+// LDS: tmp[NT + kChunkCands].
+template <int NT = kBinThreads>
+__device__ __forceinline__ void publish_items(const BinArgs& b, const unsigned* tot,
+                                              unsigned* tmp, int r0, int r1)
+{
+    constexpr int kBinWaves = NT / kWave;
+    const int tid = threadIdx.x, lane = tid % kWave, wv = tid / kWave;
     int lg_min = 0;
     while ((1 << lg_min) < kChunkMin) ++lg_min;
-    // each lane starts at its own candidate: the lanes of a wave add into
-    // different LDS words (same-word atomics from a whole wave serialise)
-    for (int j = 0; j < kChunkCands; ++j) {
-        const int k = (j + tid) % kChunkCands;
-        const unsigned sh = (unsigned)(lg_min + k), ch = 1u << sh;
-        unsigned c = 0u;
-        for (int s = r0; s < r1; ++s) {
-            const unsigned n = (tot[s] + (ch - 1u)) >> sh;
-            c += n > 1u ? n : 1u;
+    // item counts of every candidate: wave wv counts candidates wv,
+    // wv + kBinWaves, ... over all strips (its lanes split them; tot[] is
+    // complete: the caller's scan has passed a barrier since it was
+    // written), the reductions of a wave's candidates interleaved so their
+    // shuffle latencies overlap; one barrier
+    unsigned* cand = tmp;                       // [kChunkCands]
+    constexpr int KPW = (kChunkCands + kBinWaves - 1) / kBinWaves;
+    unsigned c[KPW];
+#pragma unroll
+    for (int q = 0; q < KPW; ++q) c[q] = 0u;
+    for (int s = lane; s < b.S; s += kWave) {
+        const unsigned t = tot[s];
+#pragma unroll
+        for (int q = 0; q < KPW; ++q) {
+            const unsigned sh = (unsigned)(lg_min + wv + q * kBinWaves);
+            const unsigned n = sh < 32u ? (t + ((1u << sh) - 1u)) >> sh : 1u;
+            c[q] += n > 1u ? n : 1u;
         }
-        if (c) atomicAdd(&cand[k], c);
+    }
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) {
+#pragma unroll
+        for (int q = 0; q < KPW; ++q) c[q] += __shfl_xor(c[q], o, kWave);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int q = 0; q < KPW; ++q) {
+            const int k = wv + q * kBinWaves;
+            if (k < kChunkCands) cand[k] = c[q];
+        }
     }
     __syncthreads();
     auto pick = [&](int P) -> unsigned {
@@ -297,13 +299,11 @@ __device__ __forceinline__ void strip_offsets(const BinArgs& b, unsigned* cur,
     unsigned cha = pick(b.Pacc);
     if (b.ch_force <= 0 && cha < (unsigned)kAccChunkMin) cha = (unsigned)kAccChunkMin;
     const unsigned chg = pick(b.Pgat);
+    __syncthreads();                            // cand (tmp) is read: free again
     if (tid == 0) {
         b.chunk[0] = cha;
         b.chunk[1] = chg;
     }
-    // work items (strip, chunk) of K4, then of G1: {strip | chunk << 16,
-    // first record, end record, chunks of the strip}, so a workgroup has its
-    // record range from one load
     for (int list = 0; list < 2; ++list) {
         const unsigned ch = list == 0 ? cha : chg;
         uint4* items = list == 0 ? b.items : b.items_g;
@@ -314,25 +314,190 @@ __device__ __forceinline__ void strip_offsets(const BinArgs& b, unsigned* cur,
             nrun += n > 1u ? n : 1u;
         }
         unsigned ntotal;
-        unsigned ibase = block_exclusive_scan(nrun, tmp, ntotal);
-        unsigned off = base0;
+        unsigned ibase = block_exclusive_scan<NT>(nrun, tmp, ntotal);
         for (int s = r0; s < r1; ++s) {
             const unsigned t = tot[s];
             unsigned n = (t + ch - 1u) / ch;
             n = n > 1u ? n : 1u;
-            if (list == 0) {
-                b.nch[s] = n;
-                b.item_start[s] = ibase;
-            }
             for (unsigned c = 0; c < n; ++c)
                 if (ibase + c < W)
-                    items[ibase + c] = uint4{(unsigned)s | (c << 16), off + c * ch,
-                                             off + min((c + 1u) * ch, t), n};
+                    items[ibase + c] = uint4{(unsigned)s | (c << 16), c * ch,
+                                             min((c + 1u) * ch, t), n};
             ibase += n;
-            off += t;
         }
         if (tid == 0) b.nitems[list] = ntotal < W ? ntotal : W;
     }
+}
+
+// Fresh plan, in K3 after K1: offsets of this workgroup's strip entries
+// from K1's slot totals.  Every workgroup scans the totals itself (S values,
+// a few microseconds of L2 reads spread over the grid) instead of one
+// workgroup building a table behind all of K1.  The regions of a strip are
+// its slots' totals back to back, exactly: cur[s] = strip offset + totals
+// of the slots before g's + g's base within its slot.  Workgroup 0 also
+// publishes the plan for K4 / G1.  LDS: cur[S] | tot[S] | tmp[kBinThreads]
+// | cand[kChunkCands].
+__device__ __forceinline__ void fresh_offsets(const BinArgs& b, unsigned* cur,
+                                              unsigned* tot, unsigned* tmp)
+{
+    const int tid = threadIdx.x;
+    const int S = b.S;
+    const int x = count_slot((int)blockIdx.x * kCellsPerGroup);
+    const unsigned* row = b.cnt + (size_t)blockIdx.x * S;
+    const unsigned* xt = counts_of(b, b.par);
+    for (int s = tid; s < S; s += kBinThreads) {
+        unsigned t = 0u, pre = 0u;
+#pragma unroll
+        for (int xx = 0; xx < kCountSlots; ++xx) {
+            const unsigned v = xt[(size_t)xx * S + s];
+            pre += xx < x ? v : 0u;
+            t += v;
+        }
+        tot[s] = t;
+        cur[s] = pre + row[s];
+    }
+    __syncthreads();
+    // exclusive scan of the strip totals (each thread a run of strips)
+    const int per = (S + kBinThreads - 1) / kBinThreads;
+    const int r0 = min(tid * per, S), r1 = min(r0 + per, S);
+    unsigned run = 0u;
+    for (int s = r0; s < r1; ++s) run += tot[s];
+    unsigned total;
+    unsigned base = block_exclusive_scan(run, tmp, total);
+    const bool pub = blockIdx.x == 0;         // uniform across the group
+    for (int s = r0; s < r1; ++s) {
+        cur[s] += base;
+        if (pub) {
+            unsigned o = base;
+#pragma unroll
+            for (int xx = 0; xx < kCountSlots; ++xx) {
+                const unsigned v = xt[(size_t)xx * S + s];
+                b.pbase[(size_t)xx * S + s] = o;
+                b.pcap[(size_t)xx * S + s] = v;
+                o += v;
+            }
+        }
+        base += tot[s];
+    }
+    if (pub) publish_items(b, tot, tmp, r0, r1);
+}
+
+// Capacity a one-pass step gives a region that counted d records in the
+// step before.
+__device__ __forceinline__ unsigned region_cap(unsigned d, int tight)
+{
+    return tight ? d / 2u : d + d / 8u + kRegionSlack;
+}
+
+// One-pass plan, in K3 without K1: the regions of this step from the
+// previous step's counts (the other parity's set), each its count plus
+// slack, strip after strip and slot after slot (they fit b.reg_cap:
+// region_capacity).  start[s], room[s]: the region of this workgroup's slot
+// in strip s.  Workgroup 0 also publishes the plan for K4 / G1: the regions
+// and the work items, chunked by the expected strip totals.  NT threads.
+// LDS: start[S] | room[S] | tot[S] | tmp[NT + kChunkCands].
+template <int NT>
+__device__ __forceinline__ void once_offsets(const BinArgs& b, unsigned* start,
+                                             unsigned* room, unsigned* tot, unsigned* tmp)
+{
+    const int tid = threadIdx.x;
+    const int S = b.S;
+    const int x = count_slot((int)blockIdx.x * kOnceCells);
+    const unsigned* prev = counts_of(b, b.par ^ 1);
+    const int per = (S + NT - 1) / NT;
+    const int r0 = min(tid * per, S), r1 = min(r0 + per, S);
+    unsigned run = 0u;
+    for (int s = r0; s < r1; ++s) {
+        unsigned t = 0u;
+#pragma unroll
+        for (int xx = 0; xx < kCountSlots; ++xx) {
+            const unsigned d = prev[(size_t)xx * S + s];
+            t += d;
+            run += region_cap(d, b.tight);
+        }
+        tot[s] = t;
+    }
+    unsigned total;
+    unsigned base = block_exclusive_scan<NT>(run, tmp, total);
+    const bool pub = blockIdx.x == 0;         // uniform across the group
+    for (int s = r0; s < r1; ++s) {
+#pragma unroll
+        for (int xx = 0; xx < kCountSlots; ++xx) {
+            const size_t q = (size_t)xx * S + s;
+            const unsigned c = region_cap(prev[q], b.tight);
+            if (xx == x) {
+                start[s] = base;
+                room[s] = c;
+            }
+            if (pub) {
+                b.pbase[q] = base;
+                b.pcap[q] = c;
+            }
+            base += c;
+        }
+    }
+    if (pub) publish_items<NT>(b, tot, tmp, r0, r1);
+}
+
+// A strip's records by strip-relative number: region after region (slot
+// order), min(counted, capacity) records each.  Number v of region j sits
+// at record slot v + D[j], D[j] = E[0] + ... + E[j]; P[j] is the region's
+// first number.  (Written out for the 8 regions, and as a sum of steps
+// rather than a choice among the D[j]: either of the plainer forms leaves
+// the map in scratch memory.)
+static_assert(kCountSlots == 8, "strip_map / map_record are written for 8 regions");
+struct StripMap {
+    unsigned P[kCountSlots];
+    unsigned E[kCountSlots];
+    unsigned n;                 // records of the strip in its regions
+};
+
+__device__ __forceinline__ void strip_map(const BinArgs& b, int s, StripMap& m)
+{
+    const unsigned* xt = counts_of(b, b.par);
+    unsigned p = 0u, dprev = 0u;
+    auto region = [&](int xx, unsigned& P, unsigned& E) {
+        const size_t q = (size_t)xx * b.S + s;
+        const unsigned c = xt[q], cap = b.pcap[q];
+        const unsigned d = b.pbase[q] - p;
+        P = p;
+        E = d - dprev;
+        dprev = d;
+        p += c < cap ? c : cap;
+    };
+    region(0, m.P[0], m.E[0]);
+    region(1, m.P[1], m.E[1]);
+    region(2, m.P[2], m.E[2]);
+    region(3, m.P[3], m.E[3]);
+    region(4, m.P[4], m.E[4]);
+    region(5, m.P[5], m.E[5]);
+    region(6, m.P[6], m.E[6]);
+    region(7, m.P[7], m.E[7]);
+    m.n = p;
+}
+
+__device__ __forceinline__ unsigned map_record(const StripMap& m, unsigned v)
+{
+    unsigned r = v + m.E[0];
+    r += v >= m.P[1] ? m.E[1] : 0u;
+    r += v >= m.P[2] ? m.E[2] : 0u;
+    r += v >= m.P[3] ? m.E[3] : 0u;
+    r += v >= m.P[4] ? m.E[4] : 0u;
+    r += v >= m.P[5] ? m.E[5] : 0u;
+    r += v >= m.P[6] ? m.E[6] : 0u;
+    r += v >= m.P[7] ? m.E[7] : 0u;
+    return r;
+}
+
+// The strip-relative records [e0, e1) of work item it, clamped to what the
+// strip holds this step (the last chunk takes everything past its start).
+__device__ __forceinline__ void item_range(const uint4& it, const StripMap& m,
+                                           unsigned& e0, unsigned& e1)
+{
+    const unsigned c = it.x >> 16, n = it.w;
+    e0 = it.y < m.n ? it.y : m.n;
+    e1 = c + 1u == n ? m.n : (it.z < m.n ? it.z : m.n);
+    if (e1 < e0) e1 = e0;
 }
 
 // ---------------------------------------------------------------------------
@@ -367,11 +532,11 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_count(
         if (s1 != s0) atomicAdd(&hist[s1], 1u);
     }
     __syncthreads();
-    // workgroup g adds into slot g % kCountSlots: a label only, it spreads the
+    // the block adds into its count slot: a label only, it spreads the
     // atomics over kCountSlots addresses per strip; the returned old total is
-    // g's base within its slot
+    // the block's base within its slot
     unsigned* row = b.cnt + (size_t)blockIdx.x * b.S;
-    unsigned* slot = b.xtot + (size_t)(blockIdx.x % kCountSlots) * b.S;
+    unsigned* slot = counts_of(b, b.par) + (size_t)count_slot((int)blockIdx.x * kCellsPerGroup) * b.S;
     for (int s = tid; s < b.S; s += kBinThreads) {
         const unsigned h = hist[s];
         row[s] = h ? atomicAdd(&slot[s], h) : 0u;
@@ -399,7 +564,7 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill_direct(
     const int c0 = blockIdx.x * kCellsPerGroup;
     T cx[kCellsPerThread], cy[kCellsPerThread], cw[kCellsPerThread], chh[kCellsPerThread];
     load_cells(px, py, sx, sy, nc, c0, tid, cx, cy, cw, chh);
-    strip_offsets(b, cur, cur + b.S, cur + 2 * b.S);
+    fresh_offsets(b, cur, cur + b.S, cur + 2 * b.S);
     __syncthreads();
     vec4_t<T>* recg = reinterpret_cast<vec4_t<T>*>(b.recg);
     unsigned long long* Bm = reinterpret_cast<unsigned long long*>(b.B);
@@ -458,7 +623,7 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill_direct(
 // is then one or two records, and straight stores become one partial line
 // each: 2.8x the record bytes written at 4096 x 4096).
 // A workgroup's records of one strip occupy one run of the strip's range
-// (its base from strip_offsets).  They are ranked per strip (LDS atomics),
+// (its base from fresh_offsets).  They are ranked per strip (LDS atomics),
 // staged in LDS in strip order (the block's counting sort) and copied out
 // with consecutive threads on consecutive slots, so a wave's stores cover
 // whole runs instead of one scattered 16- and 4-byte store per record: the
@@ -507,7 +672,7 @@ __global__ __launch_bounds__(kBinThreads, 5) void k_bin_fill_staged(
     const int c0 = blockIdx.x * kCellsPerGroup;
     T cx[kCellsPerThread], cy[kCellsPerThread], cw[kCellsPerThread], chh[kCellsPerThread];
     load_cells(px, py, sx, sy, nc, c0, tid, cx, cy, cw, chh);
-    strip_offsets(b, cur, cnt, tmp);
+    fresh_offsets(b, cur, cnt, tmp);
     __syncthreads();
     for (int s = tid; s < S; s += kBinThreads) cnt[s] = 0u;
     __syncthreads();
@@ -628,6 +793,268 @@ __global__ __launch_bounds__(kBinThreads, 5) void k_bin_fill_staged(
     }
 }
 
+// One record's fixed-point contributions to the bins of rows [k0, k1] (its
+// strip): add(row, column, value) for each bin it overlaps.  K4 adds them
+// into its LDS tile; an overflow record's go into the side map B, the same
+// values in either place.
+template <typename T, typename Add>
+__device__ __forceinline__ void record_density(const vec4_t<T>& rg, unsigned rm, int k0,
+                                               int k1, int stretch, T fs, Add&& add)
+{
+    const SpanBox sb = span_of(rm, k0);
+    T xr, yr, rat;
+    stretch_of<T>(rg, stretch, xr, yr, rat);
+    const T dx = rg.x, dy = rg.y;
+    const int ka = max(sb.bxl, k0), kb = min(sb.bxl + sb.nx, k1);
+    // y overlaps of the (usual) first 4 columns, shared by the rows
+    T tyv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        tyv[q] = q <= sb.ny ? min(yr, (T)(q + 1)) - max(dy, (T)q) : (T)0;
+    for (int k = ka; k <= kb; ++k) {
+        const T jx = (T)(k - sb.bxl);
+        const T tx = min(xr, jx + (T)1) - max(dx, jx);
+        if (!(tx > (T)0)) continue;
+        const T rtx = rat * tx;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (tyv[q] > (T)0) add(k, sb.byl + q, to_fixed(rtx * tyv[q], fs));
+        for (int q = 4; q <= sb.ny; ++q) {
+            const T ty = min(yr, (T)(q + 1)) - max(dy, (T)q);
+            if (!(ty > (T)0)) continue;
+            add(k, sb.byl + q, to_fixed(rtx * ty, fs));
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// K3, single pass (no K1): the regions are sized from the previous step's
+// counts (once_offsets).  Workgroup g ranks its records per strip in LDS,
+// reserves one run per strip in region g % kCountSlots of the strip (one
+// atomic per strip it touches: the total is the next step's count), and
+// stores each record straight to its slot.  Records past the region's
+// capacity -- a strip that gained more than the slack -- go to the overflow
+// pool: their density into the side map B (device-scope atomics, the values
+// K4 would add) with the strip's column blocks marked, their gather by G1's
+// pool pass.  Every record is computed as in the fresh fill, so the results
+// do not depend on which records overflow.
+// LDS: start[S] | room[S] | cnt[S] (the expected strip totals while the plan
+// is made) | tmp[kBinThreads + kChunkCands] | pool count, pool base.
+// ---------------------------------------------------------------------------
+__host__ __device__ constexpr size_t fill_once_lds(int S)
+{
+    return (size_t)(3 * S + kOnceThreads + kChunkCands + 2) * sizeof(unsigned);
+}
+
+// NT = kOnceThreads threads, kCellsPerThread cells each: blocks of twice the
+// cells of K1's, so half the reservation atomics land on each counter and
+// a block's runs in a strip are twice as long.  float32: six waves per
+// SIMD, three workgroups per CU, so 1.1 M cells fit the GPU in one round
+// (float64 keeps its registers: it would spill).
+template <typename T>
+__global__ __launch_bounds__(kOnceThreads, sizeof(T) == 4 ? 6 : 4) void k_bin_fill_once(
+    const T* __restrict__ px, const T* __restrict__ py,
+    const T* __restrict__ sx, const T* __restrict__ sy, int nc, Grid g,
+    BinArgs b)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int S = b.S;
+    unsigned* start = reinterpret_cast<unsigned*>(smem);   // first slot of the run
+    unsigned* room = start + S;                 // slots of the run in the region
+    unsigned* cnt = room + S;                   // this block's records per strip
+    unsigned* tmp = cnt + S;
+    unsigned* npool = tmp + kOnceThreads + kChunkCands;  // [0] overflow, [1] pool base
+    const int tid = threadIdx.x;
+    unsigned* xrow = counts_of(b, b.par) + (size_t)count_slot((int)blockIdx.x * kOnceCells) * S;
+    // the cells' loads are issued first: their latency overlaps the plan
+    constexpr int NT = kOnceThreads;
+    const int c0 = blockIdx.x * (NT * kCellsPerThread);
+    T cx[kCellsPerThread], cy[kCellsPerThread], cw[kCellsPerThread], chh[kCellsPerThread];
+    load_cells<T, NT>(px, py, sx, sy, nc, c0, tid, cx, cy, cw, chh);
+    once_offsets<NT>(b, start, room, cnt, tmp);
+    __syncthreads();
+    for (int s = tid; s < S; s += NT) cnt[s] = 0u;
+    if (tid == 0) npool[0] = 0u;
+    __syncthreads();
+    vec4_t<T>* recg = reinterpret_cast<vec4_t<T>*>(b.recg);
+    unsigned long long* Bm = reinterpret_cast<unsigned long long*>(b.B);
+    vec4_t<T> geo[kCellsPerThread];
+    unsigned m0[kCellsPerThread], m1[kCellsPerThread], r0[kCellsPerThread],
+        r1[kCellsPerThread], p0[kCellsPerThread], p1[kCellsPerThread];
+    int s0v[kCellsPerThread], s1v[kCellsPerThread];
+#pragma unroll
+    for (int j = 0; j < kCellsPerThread; ++j) {
+        s0v[j] = s1v[j] = -1;
+        p0[j] = p1[j] = kPosNone;
+        const int i = c0 + tid + j * NT;
+        if (i >= nc) continue;
+        CellSpan c;
+        if (!cell_span((double)cx[j], (double)cy[j], (double)cw[j], (double)chh[j], g, c))
+            continue;
+        int s0, s1;
+        bool tall;
+        cell_strips(c, b.R, b.lgR, s0, s1, tall);
+        if (tall) {
+            const double sc = c.ratio() * g.inv_ba;
+            for (int k = c.bxl; k <= c.bxh; ++k) {
+                const double tx = overlap_1d(c.x, c.w, g.xl, g.bsx, k);
+                if (tx <= 0.0) continue;
+                const double stx = sc * tx;
+                const size_t rowi = (size_t)k * g.N;
+                for (int q = c.byl; q <= c.byh; ++q) {
+                    const double ty = overlap_1d(c.y, c.h, g.yl, g.bsy, q);
+                    if (ty <= 0.0) continue;
+                    atomicAdd(&Bm[rowi + q], to_fixed(stx * ty, g.fix_scale));
+                }
+            }
+            const int CB = side_block(g.N);
+            for (int s = s0; s <= s1; ++s)
+                side_mark(b.bigflag + (size_t)s * kSideWords, c.byl, c.byh, CB);
+            p0[j] = kPosTall;
+            continue;
+        }
+        // strip-relative record, evaluated in float64 and rounded once
+        const double ex = (c.x - (g.xl + c.bxl * g.bsx)) * g.inv_bsx;
+        const double ey = (c.y - (g.yl + c.byl * g.bsy)) * g.inv_bsy;
+        geo[j] = {(T)ex, (T)ey, (T)((double)cw[j] * g.inv_bsx),
+                  (T)((double)chh[j] * g.inv_bsy)};
+        const int nx = c.bxh - c.bxl, ny = c.byh - c.byl;
+        s0v[j] = s0;
+        m0[j] = span_word(c.bxl - (s0 << b.lgR), nx, ny, c.byl);
+        r0[j] = atomicAdd(&cnt[s0], 1u);
+        if (s1 != s0) {
+            s1v[j] = s1;
+            m1[j] = span_word(c.bxl - (s1 << b.lgR), nx, ny, c.byl);
+            r1[j] = atomicAdd(&cnt[s1], 1u);
+        }
+    }
+    __syncthreads();
+    // one run per strip: its place in the region, and how much of it fits
+    for (int s = tid; s < S; s += NT) {
+        const unsigned h = cnt[s];
+        if (h) {
+            const unsigned o = atomicAdd(&xrow[s], h);
+            start[s] += o;
+            room[s] = room[s] > o ? room[s] - o : 0u;
+        }
+    }
+    __syncthreads();
+    // records that fit: straight to their slot; the others (bit 2j / 2j + 1
+    // of ovm) take a place in this block's share of the pool: p = their rank
+    // in the block's overflow, resolved below
+    unsigned ovm = 0u;
+#pragma unroll
+    for (int j = 0; j < kCellsPerThread; ++j) {
+        if (s0v[j] < 0) continue;
+        if (r0[j] < room[s0v[j]]) {
+            p0[j] = start[s0v[j]] + r0[j];
+            recg[p0[j]] = geo[j];
+            b.recm[p0[j]] = m0[j];
+        } else {
+            p0[j] = atomicAdd(&npool[0], 1u);
+            ovm |= 1u << (2 * j);
+        }
+        if (s1v[j] >= 0) {
+            if (r1[j] < room[s1v[j]]) {
+                p1[j] = start[s1v[j]] + r1[j];
+                recg[p1[j]] = geo[j];
+                b.recm[p1[j]] = m1[j];
+            } else {
+                p1[j] = atomicAdd(&npool[0], 1u);
+                ovm |= 1u << (2 * j + 1);
+            }
+        }
+    }
+    __syncthreads();
+    const unsigned nover = npool[0];            // uniform across the group
+    if (nover) {
+        if (tid == 0) npool[1] = atomicAdd(&b.pool_n[b.par & 1], nover);
+        __syncthreads();
+        const unsigned pb = npool[1];
+        const T fs = (T)g.fix_scale;
+        const int CB = side_block(g.N);
+        auto place = [&](unsigned& p, int s, unsigned m, const vec4_t<T>& gm) {
+            const unsigned q = pb + p;          // index in the pool
+            if (q >= b.pool_cap) {      // cannot happen: the pool holds 2 nc
+                p = kPosNone;
+                return;
+            }
+            p = b.pool0 + q;
+            recg[p] = gm;
+            b.recm[p] = m;
+            b.pstrip[q] = (unsigned)s;
+            const int k0 = s << b.lgR;
+            record_density<T>(gm, m, k0, k0 + b.R - 1, g.stretch, fs,
+                              [&](int k, int col, unsigned long long v) {
+                                  atomicAdd(&Bm[(size_t)k * g.N + col], v);
+                              });
+            const SpanBox sb = span_of(m, k0);
+            side_mark(b.bigflag + (size_t)s * kSideWords, sb.byl, sb.byl + sb.ny, CB);
+        };
+        if (ovm) {
+#pragma unroll
+            for (int j = 0; j < kCellsPerThread; ++j) {
+                if ((ovm >> (2 * j)) & 1u) place(p0[j], s0v[j], m0[j], geo[j]);
+                if ((ovm >> (2 * j + 1)) & 1u) place(p1[j], s1v[j], m1[j], geo[j]);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kCellsPerThread; ++j) {
+        const int i = c0 + tid + j * NT;
+        if (i < nc) b.pos[i] = pos_pair(p0[j], p1[j]);
+    }
+}
+
+// One record's partial force over rows [ka', kb'] = its rows within
+// [kg0, kg1] (a row group of its strip with first row k0): row(k, c) gives
+// the bins of row k from column c on, indexable by q, each an (fx, fy)
+// pair.  G1 reads the pairs from its LDS copy of the rows, the overflow
+// records' pass from the field maps: the same values in the same order, so
+// the same partial.
+template <typename T, typename Row>
+__device__ __forceinline__ vec2_t<T> record_partial(const vec4_t<T>& rg, unsigned rm, int k0,
+                                                    int kg0, int kg1, int stretch, T ba,
+                                                    Row&& row)
+{
+    const SpanBox sb = span_of(rm, k0);
+    T xr, yr, rat;
+    stretch_of<T>(rg, stretch, xr, yr, rat);
+    const T dx = rg.x, dy = rg.y;
+    const int ka = max(sb.bxl, kg0), kb = min(sb.bxl + sb.nx, kg1);
+    // y overlaps of the (usual) first 4 columns, shared by the rows
+    T tyv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        tyv[q] = q <= sb.ny ? min(yr, (T)(q + 1)) - max(dy, (T)q) : (T)0;
+    T ax = (T)0, ay = (T)0;
+    for (int k = ka; k <= kb; ++k) {
+        const T jx = (T)(k - sb.bxl);
+        const T tx = min(xr, jx + (T)1) - max(dx, jx);
+        if (!(tx > (T)0)) continue;
+        const auto rf = row(k, sb.byl);
+        T sx_ = (T)0, sy_ = (T)0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (tyv[q] > (T)0) {
+                const vec2_t<T> f = rf[q];
+                sx_ += tyv[q] * f.x;
+                sy_ += tyv[q] * f.y;
+            }
+        for (int q = 4; q <= sb.ny; ++q) {
+            const T ty = min(yr, (T)(q + 1)) - max(dy, (T)q);
+            if (!(ty > (T)0)) continue;
+            const vec2_t<T> f = rf[q];
+            sx_ += ty * f.x;
+            sy_ += ty * f.y;
+        }
+        ax += tx * sx_;
+        ay += tx * sy_;
+    }
+    const T sc = rat * ba;
+    return vec2_t<T>{sc * ax, sc * ay};
+}
+
 // rho = D0 + fixed-point sum, rounded once to T.
 template <typename T>
 __device__ __forceinline__ void flush_value(unsigned long long v, size_t gi,
@@ -684,68 +1111,47 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     extern __shared__ __align__(16) unsigned char smem[];
     A* tile = reinterpret_cast<A*>(smem);
     const int w = blockIdx.x;
-    if (w == 0)   // K3 has read the slot totals: zero them for the next step
-        for (int e = threadIdx.x; e < kCountSlots * b.S; e += kAccThreads) b.xtot[e] = 0u;
+    const int tid = threadIdx.x;
+    if (w == 0) {   // K3 has read the previous step's counts: zero them
+        unsigned* old = counts_of(b, b.par ^ 1);
+        for (int e = tid; e < kCountSlots * b.S; e += kAccThreads) old[e] = 0u;
+        if (tid == 0) b.pool_n[(b.par ^ 1) & 1] = 0u;
+    }
     if (w >= (int)b.nitems[0]) return;          // uniform across the group
     const uint4 item = b.items[w];
     const int s = (int)(item.x & 0xFFFFu);
-    const int tid = threadIdx.x;
     const int k0 = s * R, k1 = k0 + R - 1;
     const unsigned n = item.w;                  // chunks of this strip
     unsigned* last_flag = reinterpret_cast<unsigned*>(tile + RN);   // LDS word
-    const unsigned e0 = item.y, e1 = item.z;    // this chunk's records
-    const vec4_t<T>* recg = reinterpret_cast<const vec4_t<T>*>(b.recg);
-    const T fs = (T)g.fix_scale;
+    // the strip's map (its loads in flight while the tile is zeroed), then
     // one record per thread per pass, the next one's loads in flight while
     // it is added (measured faster here than 2, 4 or 8 records per pass, or
-    // than two ahead); the first ones are issued before the tile is zeroed
-    constexpr int kBatch = 1;
+    // than two ahead)
+    StripMap sm;
+    strip_map(b, s, sm);
+    for (int e = tid; e < RN; e += kAccThreads) tile[e] = 0ull;
+    unsigned e0, e1;                            // this chunk's records
+    item_range(item, sm, e0, e1);
+    const vec4_t<T>* recg = reinterpret_cast<const vec4_t<T>*>(b.recg);
+    const T fs = (T)g.fix_scale;
     vec4_t<T> rgn{};
     unsigned rmn = 0u;
     if (e0 + tid < e1) {
-        rgn = recg[e0 + tid];
-        rmn = b.recm[e0 + tid];
+        const unsigned r = map_record(sm, e0 + tid);
+        rgn = recg[r];
+        rmn = b.recm[r];
     }
-    for (int e = tid; e < RN; e += kAccThreads) tile[e] = 0ull;
     __syncthreads();
-    for (unsigned eb = e0 + tid; eb < e1; eb += kBatch * kAccThreads) {
-        vec4_t<T> rg[kBatch];
-        unsigned rm[kBatch];
-        rg[0] = rgn;
-        rm[0] = rmn;
+    for (unsigned eb = e0 + tid; eb < e1; eb += kAccThreads) {
+        const vec4_t<T> rg = rgn;
+        const unsigned rm = rmn;
         if (eb + kAccThreads < e1) {     // the next record, in flight meanwhile
-            rgn = recg[eb + kAccThreads];
-            rmn = b.recm[eb + kAccThreads];
+            const unsigned r = map_record(sm, eb + kAccThreads);
+            rgn = recg[r];
+            rmn = b.recm[r];
         }
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
-            if (eb + j * kAccThreads >= e1) continue;
-            const SpanBox sb = span_of(rm[j], k0);
-            T xr, yr, rat;
-            stretch_of<T>(rg[j], g.stretch, xr, yr, rat);
-            const T dx = rg[j].x, dy = rg[j].y;
-            const int ka = max(sb.bxl, k0), kb = min(sb.bxl + sb.nx, k1);
-            // y overlaps of the (usual) first 4 columns, shared by the rows
-            T tyv[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                tyv[q] = q <= sb.ny ? min(yr, (T)(q + 1)) - max(dy, (T)q) : (T)0;
-            for (int k = ka; k <= kb; ++k) {
-                const T jx = (T)(k - sb.bxl);
-                const T tx = min(xr, jx + (T)1) - max(dx, jx);
-                if (!(tx > (T)0)) continue;
-                const T rtx = rat * tx;
-                A* trow = tile + (k - k0) * N + sb.byl;
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    if (tyv[q] > (T)0) atomicAdd(&trow[q], to_fixed(rtx * tyv[q], fs));
-                for (int q = 4; q <= sb.ny; ++q) {
-                    const T ty = min(yr, (T)(q + 1)) - max(dy, (T)q);
-                    if (!(ty > (T)0)) continue;
-                    atomicAdd(&trow[q], to_fixed(rtx * ty, fs));
-                }
-            }
-        }
+        record_density<T>(rg, rm, k0, k1, g.stretch, fs,
+                          [&](int k, int q, A v) { atomicAdd(&tile[(k - k0) * N + q], v); });
     }
     __syncthreads();
 
@@ -937,129 +1343,129 @@ __host__ __device__ constexpr int gather_rows(int R, int N)
     return rg;
 }
 
+// A row of the two field maps from some column on, indexed like G1's LDS
+// pairs.
+template <typename T>
+struct FieldRow {
+    const T* x;
+    const T* y;
+    __device__ __forceinline__ vec2_t<T> operator[](int q) const { return vec2_t<T>{x[q], y[q]}; }
+};
+
 template <typename T>
 __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
     Grid g, BinArgs b, const T* __restrict__ fx, const T* __restrict__ fy)
 {
     extern __shared__ __align__(16) unsigned char smem[];
     const int w = blockIdx.x;
-    if (w >= (int)b.nitems[1]) return;          // uniform across the group
-    const uint4 item = b.items_g[w];
-    const int s = (int)(item.x & 0xFFFFu);
     const int tid = threadIdx.x;
     const int R = b.R, N = g.N;
     const int RG = gather_rows<T>(R, N);
-    const int k0 = s * R;
-    // both fields of a bin side by side: one 2-element LDS read per bin
-    vec2_t<T>* lf = reinterpret_cast<vec2_t<T>*>(smem);
-    const unsigned e0 = item.y, e1 = item.z;    // this item's records
     const vec4_t<T>* recg = reinterpret_cast<const vec4_t<T>*>(b.recg);
     vec2_t<T>* out = reinterpret_cast<vec2_t<T>*>(b.gtmp);
     const T ba = (T)(g.bsx * g.bsy);
-    for (int kg0 = k0; kg0 < k0 + R; kg0 += RG) {
-        const int kg1 = kg0 + RG - 1;
-        __syncthreads();                    // previous group's readers done
-        const size_t gb = (size_t)kg0 * N;
-        {
-            // 16-byte vectors, all of a thread's loads in flight at once
-            using V16 = typename std::conditional<sizeof(T) == 4, float4, double2>::type;
-            constexpr int V = 16 / (int)sizeof(T);
-            // RG rows of both maps fill at most kTileBytes
-            constexpr int PV = (int)(kTileBytes / (2 * 16) / kAccThreads);
-            const int nv = RG * N / V;
-            const V16* gx4 = reinterpret_cast<const V16*>(fx + gb);
-            const V16* gy4 = reinterpret_cast<const V16*>(fy + gb);
-            V16* l4 = reinterpret_cast<V16*>(lf);
-            // V bins of fx and of fy -> V interleaved (fx, fy) pairs
-            auto put = [&](int e, const V16& x, const V16& y) {
-                if constexpr (sizeof(T) == 4) {
-                    l4[2 * e] = V16{x.x, y.x, x.y, y.y};
-                    l4[2 * e + 1] = V16{x.z, y.z, x.w, y.w};
-                } else {
-                    l4[2 * e] = V16{x.x, y.x};
-                    l4[2 * e + 1] = V16{x.y, y.y};
-                }
-            };
-            if (nv == PV * kAccThreads) {
-                V16 vx[PV], vy[PV];
-#pragma unroll
-                for (int j = 0; j < PV; ++j) {
-                    vx[j] = gx4[tid + j * kAccThreads];
-                    vy[j] = gy4[tid + j * kAccThreads];
-                }
-#pragma unroll
-                for (int j = 0; j < PV; ++j) put(tid + j * kAccThreads, vx[j], vy[j]);
-            } else {
-                for (int e = tid; e < nv; e += kAccThreads) put(e, gx4[e], gy4[e]);
-            }
-        }
-        __syncthreads();
-        const bool first = kg0 == k0;
-        constexpr int kBatch = 1;       // one record per pass, the next one in flight
-        vec4_t<T> rgn{};
-        unsigned rmn = 0u;
-        if (e0 + tid < e1) {
-            rgn = recg[e0 + tid];
-            rmn = b.recm[e0 + tid];
-        }
-        for (unsigned eb = e0 + tid; eb < e1; eb += kBatch * kAccThreads) {
-            vec4_t<T> rgb[kBatch];
-            unsigned rmb[kBatch];
-            rgb[0] = rgn;
-            rmb[0] = rmn;
-            if (eb + kAccThreads < e1) {
-                rgn = recg[eb + kAccThreads];
-                rmn = b.recm[eb + kAccThreads];
-            }
-#pragma unroll
-            for (int j = 0; j < kBatch; ++j) {
-                const unsigned e = eb + j * kAccThreads;
-                if (e >= e1) continue;
-                const vec4_t<T>& rg = rgb[j];
-                const SpanBox sb = span_of(rmb[j], k0);
-                T xr, yr, rat;
-                stretch_of<T>(rg, g.stretch, xr, yr, rat);
-                const T dx = rg.x, dy = rg.y;
-                const int ka = max(sb.bxl, kg0), kb = min(sb.bxl + sb.nx, kg1);
-                // y overlaps of the (usual) first 4 columns, shared by the rows
-                T tyv[4];
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    tyv[q] = q <= sb.ny ? min(yr, (T)(q + 1)) - max(dy, (T)q) : (T)0;
-                T ax = (T)0, ay = (T)0;
-                for (int k = ka; k <= kb; ++k) {
-                    const T jx = (T)(k - sb.bxl);
-                    const T tx = min(xr, jx + (T)1) - max(dx, jx);
-                    if (!(tx > (T)0)) continue;
-                    const vec2_t<T>* rf = lf + (size_t)(k - kg0) * N + sb.byl;
-                    T sx_ = (T)0, sy_ = (T)0;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        if (tyv[q] > (T)0) {
-                            const vec2_t<T> f = rf[q];
-                            sx_ += tyv[q] * f.x;
-                            sy_ += tyv[q] * f.y;
-                        }
-                    for (int q = 4; q <= sb.ny; ++q) {
-                        const T ty = min(yr, (T)(q + 1)) - max(dy, (T)q);
-                        if (!(ty > (T)0)) continue;
-                        const vec2_t<T> f = rf[q];
-                        sx_ += ty * f.x;
-                        sy_ += ty * f.y;
+    if (w < (int)b.nitems[1]) {                 // uniform across the group
+        const uint4 item = b.items_g[w];
+        const int s = (int)(item.x & 0xFFFFu);
+        const int k0 = s * R;
+        StripMap sm;
+        strip_map(b, s, sm);
+        unsigned e0, e1;                        // this item's records
+        item_range(item, sm, e0, e1);
+        // both fields of a bin side by side: one 2-element LDS read per bin
+        vec2_t<T>* lf = reinterpret_cast<vec2_t<T>*>(smem);
+        for (int kg0 = k0; kg0 < k0 + R; kg0 += RG) {
+            const int kg1 = kg0 + RG - 1;
+            __syncthreads();                    // previous group's readers done
+            const size_t gb = (size_t)kg0 * N;
+            {
+                // 16-byte vectors, all of a thread's loads in flight at once
+                using V16 = typename std::conditional<sizeof(T) == 4, float4, double2>::type;
+                constexpr int V = 16 / (int)sizeof(T);
+                // RG rows of both maps fill at most kTileBytes
+                constexpr int PV = (int)(kTileBytes / (2 * 16) / kAccThreads);
+                const int nv = RG * N / V;
+                const V16* gx4 = reinterpret_cast<const V16*>(fx + gb);
+                const V16* gy4 = reinterpret_cast<const V16*>(fy + gb);
+                V16* l4 = reinterpret_cast<V16*>(lf);
+                // V bins of fx and of fy -> V interleaved (fx, fy) pairs
+                auto put = [&](int e, const V16& x, const V16& y) {
+                    if constexpr (sizeof(T) == 4) {
+                        l4[2 * e] = V16{x.x, y.x, x.y, y.y};
+                        l4[2 * e + 1] = V16{x.z, y.z, x.w, y.w};
+                    } else {
+                        l4[2 * e] = V16{x.x, y.x};
+                        l4[2 * e + 1] = V16{x.y, y.y};
                     }
-                    ax += tx * sx_;
-                    ay += tx * sy_;
+                };
+                if (nv == PV * kAccThreads) {
+                    V16 vx[PV], vy[PV];
+#pragma unroll
+                    for (int j = 0; j < PV; ++j) {
+                        vx[j] = gx4[tid + j * kAccThreads];
+                        vy[j] = gy4[tid + j * kAccThreads];
+                    }
+#pragma unroll
+                    for (int j = 0; j < PV; ++j) put(tid + j * kAccThreads, vx[j], vy[j]);
+                } else {
+                    for (int e = tid; e < nv; e += kAccThreads) put(e, gx4[e], gy4[e]);
                 }
-                const T sc = rat * ba;
-                vec2_t<T> v = {sc * ax, sc * ay};
+            }
+            __syncthreads();
+            const bool first = kg0 == k0;
+            // one record per pass, the next one in flight
+            vec4_t<T> rgn{};
+            unsigned rmn = 0u, rn = 0u;
+            if (e0 + tid < e1) {
+                rn = map_record(sm, e0 + tid);
+                rgn = recg[rn];
+                rmn = b.recm[rn];
+            }
+            for (unsigned eb = e0 + tid; eb < e1; eb += kAccThreads) {
+                const vec4_t<T> rg = rgn;
+                const unsigned rm = rmn, r = rn;
+                if (eb + kAccThreads < e1) {
+                    rn = map_record(sm, eb + kAccThreads);
+                    rgn = recg[rn];
+                    rmn = b.recm[rn];
+                }
+                vec2_t<T> v = record_partial<T>(
+                    rg, rm, k0, kg0, kg1, g.stretch, ba,
+                    [&](int k, int c) { return lf + (k - kg0) * N + c; });
                 if (!first) {
-                    const vec2_t<T> o = out[e];
+                    const vec2_t<T> o = out[r];
                     v.x += o.x;
                     v.y += o.y;
                 }
-                out[e] = v;
+                out[r] = v;
             }
         }
+    }
+    // the overflow pool (records past their region's capacity, rare): each
+    // record's partial over its strip's row groups straight from the field
+    // maps, in G1's order, grid-strided over every workgroup
+    const unsigned np = b.pool_n[b.par & 1];
+    for (unsigned p = (unsigned)w * kAccThreads + tid; p < np;
+         p += gridDim.x * kAccThreads) {
+        if (p >= b.pool_cap) break;
+        const unsigned r = b.pool0 + p;
+        const int k0 = (int)b.pstrip[p] * R;
+        const vec4_t<T> rg = recg[r];
+        const unsigned rm = b.recm[r];
+        vec2_t<T> v{};
+        for (int kg0 = k0; kg0 < k0 + R; kg0 += RG) {
+            vec2_t<T> u = record_partial<T>(
+                rg, rm, k0, kg0, kg0 + RG - 1, g.stretch, ba, [&](int k, int c) {
+                    const size_t o = (size_t)k * N + c;
+                    return FieldRow<T>{fx + o, fy + o};
+                });
+            if (kg0 != k0) {
+                u.x += v.x;
+                u.y += v.y;
+            }
+            v = u;
+        }
+        out[r] = v;
     }
 }
 

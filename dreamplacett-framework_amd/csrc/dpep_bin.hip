@@ -40,22 +40,32 @@ template <typename T>
 hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
                               const T* sy, int nc, const Grid& g,
                               BinArgs b, const SpectralArgs& a, const T* d0n, T* dens,
-                              T* Tt, hipStream_t s, hipEvent_t* ev)
+                              T* Tt, bool once, hipStream_t s, hipEvent_t* ev)
 {
     b.G1 = (int)g1_of(nc);
     if (b.R != strip_rows(g.N)) return hipErrorInvalidValue;   // the kernel's R
-    const size_t count_lds = (size_t)b.S * sizeof(unsigned);
-    const bool staged = b.S >= kStageMinStrips;
-    const size_t fill_lds = staged ? fill_lds_staged<T>(b.S)
-                                   : (size_t)(2 * b.S + kBinThreads + kChunkCands) * sizeof(unsigned);
+    if (once && b.pool_cap < 2u * (unsigned)(nc > 0 ? nc : 0)) return hipErrorInvalidValue;
     hipError_t e;
-    k_bin_count<T><<<b.G1, kBinThreads, count_lds, s>>>(px, py, sx, sy, nc, g, b);
-    if ((e = hipGetLastError())) return e;
-    if (ev && (e = hipEventRecord(ev[0], s))) return e;
-    if (staged)
-        k_bin_fill_staged<T><<<b.G1, kBinThreads, fill_lds, s>>>(px, py, sx, sy, nc, g, b);
-    else
-        k_bin_fill_direct<T><<<b.G1, kBinThreads, fill_lds, s>>>(px, py, sx, sy, nc, g, b);
+    if (once) {
+        if (ev && (e = hipEventRecord(ev[0], s))) return e;
+        const int per = kOnceThreads * kCellsPerThread;
+        const unsigned grid = (unsigned)(nc > per ? (nc + per - 1) / per : 1);
+        k_bin_fill_once<T><<<grid, kOnceThreads, fill_once_lds(b.S), s>>>(px, py, sx, sy, nc,
+                                                                          g, b);
+    } else {
+        const size_t count_lds = (size_t)b.S * sizeof(unsigned);
+        const bool staged = b.S >= kStageMinStrips;
+        const size_t fill_lds =
+            staged ? fill_lds_staged<T>(b.S)
+                   : (size_t)(2 * b.S + kBinThreads + kChunkCands) * sizeof(unsigned);
+        k_bin_count<T><<<b.G1, kBinThreads, count_lds, s>>>(px, py, sx, sy, nc, g, b);
+        if ((e = hipGetLastError())) return e;
+        if (ev && (e = hipEventRecord(ev[0], s))) return e;
+        if (staged)
+            k_bin_fill_staged<T><<<b.G1, kBinThreads, fill_lds, s>>>(px, py, sx, sy, nc, g, b);
+        else
+            k_bin_fill_direct<T><<<b.G1, kBinThreads, fill_lds, s>>>(px, py, sx, sy, nc, g, b);
+    }
     if ((e = hipGetLastError())) return e;
     if (ev && (e = hipEventRecord(ev[1], s))) return e;
     e = dispatch_n<T>(g.N, [&](auto lc) -> hipError_t {
@@ -81,8 +91,8 @@ hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
     hipError_t e = hipGetLastError();
     if (e) return e;
     if (ev && (e = hipEventRecord(ev, s))) return e;
-    k_gather_out<T><<<g1_of(nc), kBinThreads, kGatherOutLds, s>>>(px, py, sx, sy, nc, g, b, fx, fy, gx,
-                                                      gy);
+    k_gather_out<T><<<g1_of(nc), kBinThreads, kGatherOutLds, s>>>(px, py, sx, sy, nc, g, b, fx,
+                                                                  fy, gx, gy);
     return hipGetLastError();
 }
 
@@ -140,6 +150,11 @@ static hipError_t prepare_bin_type()
                                  hipFuncAttributeMaxDynamicSharedMemorySize,
                                  (int)fill_lds_staged<T>(sizeof(T) == 4 ? 4096 : 1024))))
         return e;
+    // the one-pass K3's strip tables: at most 8192 * 8192 bins in 2-row strips
+    if ((e = hipFuncSetAttribute((const void*)k_bin_fill_once<T>,
+                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 (int)fill_once_lds(4096))))
+        return e;
     return hipFuncSetAttribute((const void*)k_gather_bin<T>,
                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)kTileBytes);
@@ -155,11 +170,11 @@ hipError_t bin_prepare()
 template hipError_t launch_bin_scatter<float>(const float*, const float*, const float*,
                                               const float*, int, const Grid&, BinArgs,
                                               const SpectralArgs&, const float*, float*,
-                                              float*, hipStream_t, hipEvent_t*);
+                                              float*, bool, hipStream_t, hipEvent_t*);
 template hipError_t launch_bin_scatter<double>(const double*, const double*,
                                                const double*, const double*, int,
                                                const Grid&, BinArgs, const SpectralArgs&,
-                                               const double*, double*, double*,
+                                               const double*, double*, double*, bool,
                                                hipStream_t, hipEvent_t*);
 template hipError_t bin_occupancy<float>(int, int, int&, int&);
 template hipError_t bin_occupancy<double>(int, int, int&, int&);

@@ -66,40 +66,81 @@ hipError_t launch_row_inv(const SpectralArgs& a, const T* Ux, const T* Uy,
 constexpr int kBinThreads = 256;       // K1 / K3 workgroup size
 constexpr int kCellsPerThread = 4;     // K1 / K3 cells per thread
 constexpr int kCellsPerGroup = kBinThreads * kCellsPerThread;
+constexpr int kOnceThreads = 512;      // one-pass K3 workgroup size
+constexpr int kOnceCells = kOnceThreads * kCellsPerThread;
 constexpr int kAccThreads = 1024;      // K4 workgroup size
 constexpr int kCountSlots = 8;         // strip-total counters per strip
+// The count slot of the cells of block [c0, c0 + ...): by blocks of
+// kOnceCells cells in every kernel that counts, so a fresh step's counts
+// size a one-pass step's regions slot by slot.
+__host__ __device__ constexpr int count_slot(int c0) { return (c0 / kOnceCells) % kCountSlots; }
 constexpr int kMaxSpanY = 4095;        // larger y spans take the tall path
 constexpr int kSideBits = 128;         // column blocks tracked per strip in B
 constexpr int kSideWords = kSideBits / 32;
+
+// Cells of one problem at most: record numbers (regions, then the overflow
+// pool: about 4.25 per cell) stay below the reserved pos values.
+constexpr int kMaxCells = 1 << 28;
 
 // Chunk sizes a step may choose for K4 / G1 work items: kChunkMin << k.
 constexpr int kChunkMin = 1024;
 constexpr int kChunkCands = 21;        // up to 2^30 records: never splits
 constexpr int kAccChunkMin = 8192;     // smallest K4 chunk a step chooses
 
+// Records of the (slot, strip) regions a step's plan may hold beyond the
+// records themselves: each region gets its last demand plus an eighth plus
+// kRegionSlack, so the regions of all slots and strips fit
+// region_capacity() records.
+constexpr unsigned kRegionSlack = 16;
+
 // Shared between host (sizing) and device.
+//
+// Records live in kCountSlots regions per strip (workgroup g reserves its
+// runs in region g % kCountSlots of each strip: the reservation atomics are
+// spread over kCountSlots counters per strip).  K3's workgroup 0 publishes
+// the step's plan: where the regions are (pbase, pcap) and the K4 / G1 work
+// items.  Within a strip the records are numbered region after region,
+// without the unfilled tail of each region ("strip-relative" numbers).  Two
+// ways to fill:
+//   fresh  K1 counts every (slot, strip) first; K3 places the regions
+//          exactly (none overflows);
+//   once   K3 alone: each region sized from the previous step's count of it
+//          plus slack; K3 reserves in the regions as it sorts, and records
+//          past a region's capacity go to the overflow pool (their density
+//          through the side map B).
+// The counts of a step stay for the next one: two sets, by step parity.
+// K4's workgroup 0 re-zeroes the older set (and its pool count) once K3 has
+// read it.
 struct BinArgs {
     int S, R, lgR;          // strips, rows per strip, log2 R
     int G1;                 // K1/K3 workgroups of this step
     int Pacc, Pgat;         // K4 / G1 workgroups the device holds at once
     int Wacc, Wgat;         // K4 / G1 grids = capacities of their item lists
     int ch_force;           // > 0: every chunk this many records (tests only)
-    unsigned* cnt;          // [G1max][S] base of workgroup g in its slot
-    unsigned* xtot;         // [kCountSlots][S] slot totals (zero between steps)
-    unsigned* strip_off;    // [S + 1] entry offset of each strip
-    unsigned* chunk;        // [2] records per K4 / G1 item, chosen per step
-    unsigned* nch;          // [S] K4 chunks per strip
-    unsigned* item_start;   // [S] first K4 work item of each strip
-    uint4* items;           // [Wacc] K4 items: {strip | chunk << 16, first
-                            // record, end record, chunks of the strip}
+    int tight;              // 1: size each region at half its previous count,
+                            // so the step overflows (tests only)
+    int par;                // parity of this step: its set of counts
+    unsigned reg_cap;       // records the regions of a plan may hold in total
+    unsigned pool0;         // record number of the overflow pool's first entry
+    unsigned pool_cap;      // capacity of the overflow pool (0: fresh-only)
+    unsigned* cnt;          // [G1max][S] fresh: base of workgroup g in its slot
+    unsigned* xtot;         // [2][kCountSlots][S] records counted / reserved per
+                            // (slot, strip), the set of parity par this step
+    unsigned* pbase;        // [kCountSlots][S] plan: first record of a region
+    unsigned* pcap;         // [kCountSlots][S] plan: capacity of a region
+    unsigned* chunk;        // [2] records per K4 / G1 item, chosen per plan
+    uint4* items;           // [Wacc] K4 items: {strip | chunk << 16, first,
+                            // end strip-relative record, chunks of the strip}
     unsigned* nitems;       // [2] K4, G1 item counts
     uint4* items_g;         // [Wgat] G1 items (same layout)
+    unsigned* pool_n;       // [2] overflow records of the step of each parity
+    unsigned* pstrip;       // [pool_cap] strip of each overflow record
     unsigned* done;         // [S] K4 chunks done per strip (zero between steps)
-    void* recg;             // [2 nc_max] record geometry, vec4 of T
-    unsigned* recm;         // [2 nc_max] record span word
+    void* recg;             // [pool0 + pool_cap] record geometry, vec4 of T
+    unsigned* recm;         // [pool0 + pool_cap] record span word
     unsigned long long* pos;   // [nc_max] records of cell i: first strip (or
                                // kPosTall / kPosNone) | second strip << 32
-    void* gtmp;             // [2 nc_max] vec2 forces in record order
+    void* gtmp;             // [pool0 + pool_cap] vec2 forces by record
     unsigned* bigflag;      // [kSideWords S] per strip: bitmap of the column
                             // blocks of its rows that hold tall-cell sums in B
                             // (zero between steps)
@@ -134,8 +175,16 @@ constexpr size_t kTileBytes = 131072;  // LDS tile of K4 (uint64 words) and G1
 struct BinPlan {
     int S, R, lgR, G1max;
     size_t cap;             // records (2 per cell)
+    size_t reg_cap;         // region capacity of a planned step (>= cap)
     size_t geo_bytes;       // bytes of one record's geometry (4 elements)
 };
+
+// Records all (slot, strip) regions of a plan hold at most: every region's
+// demand d plus d / 8 plus kRegionSlack, with sum d <= cap.
+inline size_t region_capacity(size_t cap, int S)
+{
+    return cap + cap / 8 + (size_t)kRegionSlack * kCountSlots * (size_t)S;
+}
 
 inline BinPlan make_bin_plan(int M, int N, int nc_max, size_t elem_bytes)
 {
@@ -151,6 +200,7 @@ inline BinPlan make_bin_plan(int M, int N, int nc_max, size_t elem_bytes)
     const long long nc = nc_max > 1 ? nc_max : 1;
     p.G1max = (int)((nc + kCellsPerGroup - 1) / kCellsPerGroup);
     p.cap = (size_t)(2 * nc);
+    p.reg_cap = region_capacity(p.cap, p.S);
     return p;
 }
 
@@ -179,14 +229,17 @@ inline void set_item_grids(BinArgs& b, int acc_per_cu, int gat_per_cu, int cus)
     b.Wgat = b.Pgat > b.S ? b.Pgat : b.S;
 }
 
-// Strip-binned scatter (K1, K3, K4; K4 also runs the row DCT, writing T)
-// and gather (G1, G2); the scatter's ev (nullable) receives 3 events: after
-// K1, K3, K4; the gather's ev (nullable) is recorded between G1 and G2.
+// Strip-binned scatter (K1 unless `once`, K3, K4; K4 also runs the row DCT,
+// writing T) and gather (G1, G2); the scatter's ev (nullable) receives 3
+// events: after K1 (at the start when `once`), K3, K4; the gather's ev
+// (nullable) is recorded between G1 and G2.  `once` needs the counts of a
+// previous step (parity b.par ^ 1) on the same buffers and an overflow pool
+// of 2 * nc records (pool_cap).
 template <typename T>
 hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
                               const T* sy, int nc, const Grid& g, BinArgs b,
                               const SpectralArgs& a, const T* d0n, T* dens, T* Tt,
-                              hipStream_t s, hipEvent_t* ev);
+                              bool once, hipStream_t s, hipEvent_t* ev);
 template <typename T>
 hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
                              const T* sy, int nc, const Grid& g,

@@ -70,12 +70,14 @@ struct Carve {
 };
 
 // The scratch layout of one call.  The regions that must start at zero (slot
-// totals, chunk tickets, side-map marks, the side map, and the zero initial
-// density when the caller passes none) come first, in one run.
+// totals, the overflow count, chunk tickets, side-map marks, the side map,
+// and the zero initial density when the caller passes none) come first, in
+// one run.  Every call counts before it sorts (no counts survive between
+// calls), so the records need no overflow pool.
 struct Layout {
-    size_t xtot, done, bigflag, B, d0zero, zero_end;
+    size_t xtot, pool_n, done, bigflag, B, d0zero, zero_end;
     size_t twM, postM, twN, postN, T, Ux, Uy;
-    size_t cnt, strip_off, nch, item_start, items, items_g, nitems, chunk;
+    size_t cnt, pbase, pcap, pstrip, items, items_g, nitems, chunk;
     size_t recg, recm, pos, gtmp;
     size_t total;
 };
@@ -87,7 +89,8 @@ Layout plan_layout(int M, int N, int nc, size_t esz, const BinPlan& p, const Bin
     const size_t ncs = (size_t)(nc > 0 ? nc : 1);
     Carve c;
     Layout l{};
-    l.xtot = c.take((size_t)kCountSlots * p.S * sizeof(unsigned));
+    l.xtot = c.take(2 * (size_t)kCountSlots * p.S * sizeof(unsigned));
+    l.pool_n = c.take(2 * sizeof(unsigned));
     l.done = c.take((size_t)p.S * sizeof(unsigned));
     l.bigflag = c.take((size_t)kSideWords * p.S * sizeof(unsigned));
     l.B = c.take(mn * sizeof(unsigned long long));
@@ -101,9 +104,9 @@ Layout plan_layout(int M, int N, int nc, size_t esz, const BinPlan& p, const Bin
     l.Ux = c.take(mn * esz);
     l.Uy = c.take(mn * esz);
     l.cnt = c.take((size_t)p.G1max * p.S * sizeof(unsigned));
-    l.strip_off = c.take((size_t)(p.S + 1) * sizeof(unsigned));
-    l.nch = c.take((size_t)p.S * sizeof(unsigned));
-    l.item_start = c.take((size_t)p.S * sizeof(unsigned));
+    l.pbase = c.take((size_t)kCountSlots * p.S * sizeof(unsigned));
+    l.pcap = c.take((size_t)kCountSlots * p.S * sizeof(unsigned));
+    l.pstrip = c.take(sizeof(unsigned));
     l.items = c.take((size_t)b.Wacc * sizeof(uint4));
     l.items_g = c.take((size_t)b.Wgat * sizeof(uint4));
     l.nitems = c.take(2 * sizeof(unsigned));
@@ -173,9 +176,14 @@ int run(int M, int N, const Grid& g, int dtype, bool potential, bool gather, int
     b.bigflag = (unsigned*)(sc + l.bigflag);
     b.B = sc + l.B;
     b.cnt = (unsigned*)(sc + l.cnt);
-    b.strip_off = (unsigned*)(sc + l.strip_off);
-    b.nch = (unsigned*)(sc + l.nch);
-    b.item_start = (unsigned*)(sc + l.item_start);
+    b.pool_n = (unsigned*)(sc + l.pool_n);
+    b.pbase = (unsigned*)(sc + l.pbase);
+    b.pcap = (unsigned*)(sc + l.pcap);
+    b.pstrip = (unsigned*)(sc + l.pstrip);
+    b.reg_cap = (unsigned)p.cap;
+    b.pool0 = (unsigned)p.cap;
+    b.pool_cap = 0u;
+    b.par = 0;
     b.items = (uint4*)(sc + l.items);
     b.items_g = (uint4*)(sc + l.items_g);
     b.nitems = (unsigned*)(sc + l.nitems);
@@ -206,7 +214,7 @@ int run(int M, int N, const Grid& g, int dtype, bool potential, bool gather, int
     NA_TRY(launch_tables<T>(M, (T*)(sc + l.twM), (T*)(sc + l.postM), s));
     NA_TRY(launch_tables<T>(N, (T*)(sc + l.twN), (T*)(sc + l.postN), s));
     NA_TRY(launch_bin_scatter<T>((const T*)px, (const T*)py, (const T*)sx, (const T*)sy, nc,
-                                 g, b, a, d0, (T*)dens, Tt, s, nullptr));
+                                 g, b, a, d0, (T*)dens, Tt, false, s, nullptr));
     NA_TRY(launch_col_pass<T>(a, Tt, Ux, Uy, s));
     NA_TRY(launch_row_inv<T>(a, Ux, Uy, (T*)fx, (T*)fy, (T*)phi, s));
     if (gather)

@@ -31,6 +31,7 @@ DPEP_FLAG_NO_STRETCH = 0x4
 DPEP_FLAG_NO_GATHER = 0x8
 DPEP_FLAG_STEP_TIMINGS = 0x10
 DPEP_FLAG_SCATTER_DENSITY = 0x20
+DPEP_FLAG_TWO_PASS = 0x40
 
 OUTPUT_NAMES = ("density", "potential", "field_x", "field_y", "grad_x", "grad_y")
 
@@ -171,6 +172,9 @@ class Context:
     buffers, valid until the next get_outputs or close().
     scatter_density=True keeps the scattered cells' density without the
     initial density (scatter_density()), as the reference's read-back.
+    two_pass=True counts the cells per strip before sorting them on every
+    step, instead of sorting in one pass into the room the previous step
+    sized (same results; for a context stepped with unrelated placements).
     """
 
     def __init__(self, num_bins_x: int, num_bins_y: int, nc_max: int,
@@ -178,7 +182,8 @@ class Context:
                  dtype=np.float32, deterministic: bool = False,
                  potential: bool = True, stretch: bool = True,
                  gather: bool = True, step_timings: bool = False,
-                 pinned: bool = False, scatter_density: bool = False):
+                 pinned: bool = False, scatter_density: bool = False,
+                 two_pass: bool = False):
         self._lib = load_library()
         self._h = None
         self._pin: Optional[_Pinned] = None
@@ -200,6 +205,8 @@ class Context:
             flags |= DPEP_FLAG_STEP_TIMINGS
         if scatter_density:
             flags |= DPEP_FLAG_SCATTER_DENSITY
+        if two_pass:
+            flags |= DPEP_FLAG_TWO_PASS
         self.flags = flags
         self.potential = potential
         self.gather = gather

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define DPEP_ABI_VERSION 3
+#define DPEP_ABI_VERSION 4
 
 /* status codes */
 #define DPEP_OK 0
@@ -69,6 +69,17 @@ extern "C" {
                                         density without the initial density
                                         (one more M*N map written per step),
                                         for dpep_get_scatter_density       */
+#define DPEP_FLAG_TWO_PASS 0x40u     /* count the cells per strip before
+                                        sorting them on every step.  By
+                                        default a step after the first sorts
+                                        in one pass into room the previous
+                                        step sized from its own counts (plus
+                                        an eighth); cells beyond that room
+                                        still land correctly, through device
+                                        atomics, but a context stepped with
+                                        unrelated placements is faster with
+                                        this flag.  Results are bitwise the
+                                        same either way.                   */
 
 /* timing slots, the reference's 9-float shm header order
  * (integration/scatter_ttnn_client.py:151-163): h2d, scatter, gather,

@@ -34,26 +34,29 @@ int oracle_gather(const double*, const double*, const double*, const double*, lo
                   double*);
 }
 
-// shuffle groups of the current launch (the only width the kernels use)
-static constexpr int kEmuShflWidth = 16;
-static std::vector<std::unique_ptr<std::barrier<>>> emu_groups;
+// shuffle groups of the current launch: teams of 16 lanes and waves of 64
+static std::vector<std::unique_ptr<std::barrier<>>> emu_groups16, emu_groups64;
 double emu_shfl_slot[1024];
 std::barrier<>* emu_group_barrier(unsigned group, int width)
 {
-    if (width != kEmuShflWidth || group >= emu_groups.size()) {
+    auto& gs = width == 16 ? emu_groups16 : emu_groups64;
+    if ((width != 16 && width != 64) || group >= gs.size()) {
         fprintf(stderr, "shuffle width %d / group %u not emulated\n", width, group);
         abort();
     }
-    return emu_groups[group].get();
+    return gs[group].get();
 }
 
 static void launch(unsigned grid, unsigned block, size_t shm, const std::function<void()>& body)
 {
     blockDim = dim3(block);
     gridDim = dim3(grid);
-    emu_groups.clear();
-    for (unsigned q = 0; q < block / kEmuShflWidth; ++q)
-        emu_groups.push_back(std::make_unique<std::barrier<>>(kEmuShflWidth));
+    emu_groups16.clear();
+    emu_groups64.clear();
+    for (unsigned q = 0; q < block / 16; ++q)
+        emu_groups16.push_back(std::make_unique<std::barrier<>>(16));
+    for (unsigned q = 0; q < (block + 63) / 64; ++q)
+        emu_groups64.push_back(std::make_unique<std::barrier<>>(block - 64 * q < 64 ? block - 64 * q : 64));
     if (shm > sizeof(dpep::smem)) { fprintf(stderr, "LDS %zu too big\n", shm); abort(); }
     // One OS thread per GPU thread of a block, created once per launch; the
     // blocks run one after another, fenced by barriers, with the LDS
@@ -146,30 +149,37 @@ static int run(int nc, bool det, bool pot, int ch, bool tall, bool force_stage)
     b.S = p.S; b.R = p.R; b.lgR = p.lgR;
     if (ch > 0) {   // fixed chunks: every list can hold all of them
         b.ch_force = ch;
-        b.Pacc = b.Pgat = p.S + (int)((p.cap + ch - 1) / ch) + 1;
+        b.Pacc = b.Pgat = p.S + (int)((p.reg_cap + ch - 1) / ch) + 1;
         b.Wacc = b.Wgat = b.Pacc;
     } else {        // chosen per step, as on the device, for a 2-CU "device"
         set_item_grids(b, 2, 3, 2);
     }
     b.G1 = (nc + kCellsPerGroup - 1) / kCellsPerGroup;
     if (b.G1 < 1) b.G1 = 1;
+    const size_t nslot = (size_t)kCountSlots * p.S;
     b.cnt = exact<unsigned>((size_t)b.G1 * p.S);
-    b.xtot = exact<unsigned>((size_t)kCountSlots * p.S);
-    memset(b.xtot, 0, (size_t)kCountSlots * p.S * sizeof(unsigned));
-    b.strip_off = exact<unsigned>(p.S + 1);
-    b.nch = exact<unsigned>(p.S);
-    b.item_start = exact<unsigned>(p.S);
+    b.xtot = exact<unsigned>(2 * nslot);           // two sets, by step parity
+    memset(b.xtot, 0, 2 * nslot * sizeof(unsigned));
+    b.pbase = exact<unsigned>(nslot);
+    b.pcap = exact<unsigned>(nslot);
+    b.pool_n = exact<unsigned>(2);
+    b.pool_n[0] = b.pool_n[1] = 0u;
+    b.reg_cap = (unsigned)p.reg_cap;
+    b.pool0 = (unsigned)p.reg_cap;
+    b.pool_cap = (unsigned)p.cap;
+    b.pstrip = exact<unsigned>(p.cap);
+    const size_t nrec = p.reg_cap + p.cap;
     b.items = exact<uint4>(b.Wacc);
     b.items_g = exact<uint4>(b.Wgat);
     b.nitems = exact<unsigned>(2);
     b.chunk = exact<unsigned>(2);
     if (sizeof(vec4_t<T>) != p.geo_bytes) { fprintf(stderr, "record size mismatch\n"); return 4; }
-    b.recg = malloc(p.cap * p.geo_bytes);
-    b.recm = exact<unsigned>(p.cap);
+    b.recg = malloc(nrec * p.geo_bytes);
+    b.recm = exact<unsigned>(nrec);
     b.done = exact<unsigned>(p.S);
     memset(b.done, 0, p.S * sizeof(unsigned));
     b.pos = exact<unsigned long long>(nc > 0 ? nc : 1);
-    b.gtmp = exact<vec2_t<T>>(p.cap);
+    b.gtmp = exact<vec2_t<T>>(nrec);
     b.bigflag = exact<unsigned>(kSideWords * p.S);
     b.raw = exact<T>(mn);        // the scatter density without D0, checked below
     b.B = malloc(mn * 8);
@@ -179,47 +189,84 @@ static int run(int nc, bool det, bool pot, int ch, bool tall, bool force_stage)
     // the library stages K3's records from kStageMinStrips strips on; "stage"
     // forces the staged form on any grid
     const bool stage = force_stage || p.S >= kStageMinStrips;
-    for (int rep = 0; rep < 2; ++rep) {   // two steps: B / flags must be clean again
-        launch(b.G1, kBinThreads, hist, [&] { k_bin_count<T>(px, py, sx, sy, nc, g, b); });
-        if (stage)
-            launch(b.G1, kBinThreads, fill_lds_staged<T>(p.S),
-                   [&] { k_bin_fill_staged<T>(px, py, sx, sy, nc, g, b); });
-        else
-            launch(b.G1, kBinThreads, (size_t)(2 * p.S + kBinThreads + kChunkCands) * sizeof(unsigned),
-                   [&] { k_bin_fill_direct<T>(px, py, sx, sy, nc, g, b); });
+    unsigned pool_seen = 0;
+    // one step: fresh (K1 + K3) or in one pass on the previous step's counts
+    auto step = [&](bool once) -> int {
+        if (once) {
+            const int per = kOnceThreads * kCellsPerThread;
+            launch(nc > per ? (nc + per - 1) / per : 1, kOnceThreads, fill_once_lds(p.S),
+                   [&] { k_bin_fill_once<T>(px, py, sx, sy, nc, g, b); });
+        } else {
+            launch(b.G1, kBinThreads, hist, [&] { k_bin_count<T>(px, py, sx, sy, nc, g, b); });
+            if (stage)
+                launch(b.G1, kBinThreads, fill_lds_staged<T>(p.S),
+                       [&] { k_bin_fill_staged<T>(px, py, sx, sy, nc, g, b); });
+            else
+                launch(b.G1, kBinThreads,
+                       (size_t)(2 * p.S + kBinThreads + kChunkCands) * sizeof(unsigned),
+                       [&] { k_bin_fill_direct<T>(px, py, sx, sy, nc, g, b); });
+        }
+        pool_seen = b.pool_n[b.par];
         launch(b.Wacc, kAccThreads, acc_lds_bytes<T, LN>(),
                [&] { k_strip_acc<T, LN>(g, b, a, d0n, dens, Tt); });
         for (int s2 = 0; s2 < p.S; ++s2)
             if (b.done[s2]) { fprintf(stderr, "strip chunk counter left set\n"); return 4; }
         for (int s2 = 0; s2 < kSideWords * p.S; ++s2)
             if (b.bigflag[s2]) { fprintf(stderr, "bigflag left set\n"); return 4; }
-        for (int s2 = 0; s2 < kCountSlots * p.S; ++s2)
-            if (b.xtot[s2]) { fprintf(stderr, "slot totals left set\n"); return 4; }
-    }
-    {
-        constexpr int F = fpw<T>(LM);
-        const size_t shm = (size_t)F * lds_len(LM) * sizeof(vec2_t<T>);
-        launch(N / (2 * F), col_threads<T>(LM), shm, [&] { k_col_pass<T, LM, F>(a, Tt, Ux, Uy); });
-    }
-    {
-        constexpr int F = fpw<T>(LN);
-        const size_t shm = (size_t)F * lds_len(LN) * sizeof(vec2_t<T>);
-        const unsigned grid = (M / (2 * F)) * (pot ? 3 : 2);
-        launch(grid, row_threads<T>(LN), shm, [&] { k_row_inv<T, LN, F>(a, Ux, Uy, fx, fy, phi); });
-    }
-    if (nc > 0) {
-        const size_t glds = (size_t)gather_rows<T>(p.R, N) * N * 2 * sizeof(T);
-        launch(b.Wgat, kAccThreads, glds, [&] { k_gather_bin<T>(g, b, fx, fy); });
-        launch(b.G1, kBinThreads, kGatherOutLds, [&] { k_gather_out<T>(px, py, sx, sy, nc, g, b, fx, fy, gx, gy); });
-    }
-    {
+        {
+            constexpr int F = fpw<T>(LM);
+            const size_t shm = (size_t)F * lds_len(LM) * sizeof(vec2_t<T>);
+            launch(N / (2 * F), col_threads<T>(LM), shm, [&] { k_col_pass<T, LM, F>(a, Tt, Ux, Uy); });
+        }
+        {
+            constexpr int F = fpw<T>(LN);
+            const size_t shm = (size_t)F * lds_len(LN) * sizeof(vec2_t<T>);
+            const unsigned grid = (M / (2 * F)) * (pot ? 3 : 2);
+            launch(grid, row_threads<T>(LN), shm, [&] { k_row_inv<T, LN, F>(a, Ux, Uy, fx, fy, phi); });
+        }
+        if (nc > 0) {
+            const size_t glds = (size_t)gather_rows<T>(p.R, N) * N * 2 * sizeof(T);
+            launch(b.Wgat, kAccThreads, glds, [&] { k_gather_bin<T>(g, b, fx, fy); });
+            launch(b.G1, kBinThreads, kGatherOutLds,
+                   [&] { k_gather_out<T>(px, py, sx, sy, nc, g, b, fx, fy, gx, gy); });
+        }
+        // the older set of counts is zero again for the next step
+        const unsigned* older = b.xtot + (size_t)(b.par ^ 1) * nslot;
+        for (size_t s2 = 0; s2 < nslot; ++s2)
+            if (older[s2]) { fprintf(stderr, "previous counts left set\n"); return 4; }
+        if (b.pool_n[b.par ^ 1]) { fprintf(stderr, "previous overflow count left set\n"); return 4; }
+        b.par ^= 1;
         const unsigned char* Bb = (const unsigned char*)b.B;
         for (size_t i = 0; i < mn * 8; ++i)
             if (Bb[i]) { fprintf(stderr, "side map B not re-zeroed at byte %zu (row %zu)\n", i, i / 8 / N); return 4; }
-    }
-    printf("emu plan S=%d R=%d chunks=%u/%u items=%u/%u of %d/%d records=%u\n", p.S, p.R,
-           b.chunk[0], b.chunk[1], b.nitems[0], b.nitems[1], b.Wacc, b.Wgat,
-           b.strip_off[p.S]);
+        return 0;
+    };
+    // step 1 counts first; step 2 sorts in one pass into regions sized
+    // from step 1's counts (no overflow: same cells); step 3 sizes them at
+    // half of step 2's counts, so it overflows about half its records --
+    // and must give bitwise step 2's results
+    int rc = step(false);
+    if (rc) return rc;
+    if (pool_seen) { fprintf(stderr, "fresh step used the pool\n"); return 4; }
+    rc = step(true);
+    if (rc) return rc;
+    if (pool_seen) { fprintf(stderr, "one-pass step on the same cells overflowed (%u)\n", pool_seen); return 4; }
+    std::vector<T> keep[7];
+    T* outs[7] = {dens, fx, fy, gx, gy, (T*)b.raw, phi};
+    const size_t lens[7] = {mn, mn, mn, (size_t)nc, (size_t)nc, mn, pot ? mn : 0};
+    for (int k = 0; k < 7; ++k) keep[k].assign(outs[k], outs[k] + lens[k]);
+    b.tight = 1;                  // regions at half of step 2's counts
+    rc = step(true);
+    b.tight = 0;
+    if (rc) return rc;
+    const unsigned pool_tight = pool_seen;
+    for (int k = 0; k < 7; ++k)
+        if (lens[k] && memcmp(keep[k].data(), outs[k], lens[k] * sizeof(T))) {
+            fprintf(stderr, "overflowing step differs from the planned one in output %d\n", k);
+            return 4;
+        }
+    printf("emu plan S=%d R=%d chunks=%u/%u items=%u/%u of %d/%d overflow=%u\n", p.S, p.R,
+           b.chunk[0], b.chunk[1], b.nitems[0], b.nitems[1], b.Wacc, b.Wgat, pool_tight);
 
     // oracle
     std::vector<double> dpx(nc), dpy(nc), dsx(nc), dsy(nc), dd0(mn), rho(mn), rphi(mn), rfx(mn), rfy(mn), rgx(nc), rgy(nc);

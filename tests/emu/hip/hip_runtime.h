@@ -49,15 +49,28 @@ inline void __threadfence() { std::atomic_thread_fence(std::memory_order_seq_cst
 // values through one slot each, between two waits on the group's barrier.
 extern std::barrier<>* emu_group_barrier(unsigned group, int width);
 extern double emu_shfl_slot[1024];
-inline double __shfl_xor(double v, int mask, int width)
+template <typename V>
+inline V __shfl_xor(V v, int mask, int width)
 {
     const unsigned t = threadIdx.x, first = t - t % (unsigned)width;
     std::barrier<>& b = *emu_group_barrier(first / (unsigned)width, width);
-    emu_shfl_slot[t] = v;
+    emu_shfl_slot[t] = (double)v;
     b.arrive_and_wait();
     const double r = emu_shfl_slot[first + ((t - first) ^ (unsigned)mask) % (unsigned)width];
     b.arrive_and_wait();
-    return r;
+    return (V)r;
+}
+// __shfl_up: lane l gets lane l - delta's value (its own below delta)
+template <typename V>
+inline V __shfl_up(V v, unsigned delta, int width)
+{
+    const unsigned t = threadIdx.x, first = t - t % (unsigned)width;
+    std::barrier<>& b = *emu_group_barrier(first / (unsigned)width, width);
+    emu_shfl_slot[t] = (double)v;
+    b.arrive_and_wait();
+    const double r = t - first >= delta ? emu_shfl_slot[t - delta] : (double)v;
+    b.arrive_and_wait();
+    return (V)r;
 }
 // __hip_atomic_load is a clang builtin, available to host code as well
 #ifndef __HIP_MEMORY_SCOPE_AGENT

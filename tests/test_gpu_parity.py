@@ -34,12 +34,21 @@ def check(out, ref, dtype, tag=""):
 
 
 def run_gpu(w, dtype=np.float32, cells=None, **kw):
+    """Two steps on the same cells: the first counts the cells per strip
+    before sorting them, the second sorts in one pass into the room the
+    first planned.  Both must give bitwise the same outputs; returns the
+    second's."""
     import dpep
     px, py, sx, sy = cells if cells is not None else w.cells(dtype)
     with dpep.Context(w.M, w.N, max(len(px), 1), w.xl, w.yl, w.xh, w.yh,
                       dtype=dtype, **kw) as ctx:
         ctx.set_initial_density(w.d0n.astype(dtype))
-        return ctx.step(px, py, sx, sy)
+        first = ctx.step(px, py, sx, sy)
+        second = ctx.step(px, py, sx, sy)
+    for k in first:
+        assert np.array_equal(first[k], second[k], equal_nan=True), \
+            f"{k}: the one-pass step differs from the counted one"
+    return second
 
 
 def run_oracle(oracle, w, dtype=np.float32, cells=None, stretch=True):
@@ -144,6 +153,42 @@ def test_deterministic_mode_is_bitwise_reproducible_and_order_free():
     c = run_gpu(w, deterministic=True, cells=cells)
     for k in ("density", "potential", "field_x", "field_y"):
         assert np.array_equal(a[k], c[k]), k
+
+
+@pytest.mark.parametrize("grid,dtype", [(512, np.float32), (4096, np.float32),
+                                        (512, np.float64)])
+def test_one_pass_overflow_matches_counted_step(oracle, grid, dtype):
+    """A context stepped on one placement, then on a very different one:
+    the one-pass sort of the second placement runs out of room in most
+    strips (the room was planned for the first), so most of its records go
+    through the overflow pool (their density by device atomics into the side
+    map, their gather from the field maps).  Its outputs must equal, bitwise,
+    those of a context that counts first (DPEP_FLAG_TWO_PASS), and the
+    oracle's; a third step (planned from the second's counts) overflows no
+    more and gives the same again."""
+    import dpep
+    from dpep import workloads
+    b = workloads.small(5, seed=22, cells=60000, grid=grid)     # one hot square
+    cb = b.cells(dtype)
+    rng = np.random.default_rng(23)                              # the same cells
+    ca = (rng.uniform(b.xl, b.xh - cb[2]).astype(dtype),         # spread out
+          rng.uniform(b.yl, b.yh - cb[3]).astype(dtype), cb[2], cb[3])
+    with dpep.Context(b.M, b.N, b.nc, b.xl, b.yl, b.xh, b.yh, dtype=dtype) as ctx:
+        ctx.set_initial_density(b.d0n.astype(dtype))
+        ctx.step(*ca)
+        over = ctx.step(*cb)
+        again = ctx.step(*cb)
+    with dpep.Context(b.M, b.N, b.nc, b.xl, b.yl, b.xh, b.yh, dtype=dtype,
+                      two_pass=True) as ctx:
+        ctx.set_initial_density(b.d0n.astype(dtype))
+        ref2 = ctx.step(*cb)
+    for k in ref2:
+        assert np.array_equal(over[k], ref2[k]), f"{k}: overflowing step differs"
+        assert np.array_equal(again[k], ref2[k]), f"{k}: re-planned step differs"
+    errs = check(over, run_oracle(oracle, b, dtype, cells=cb), dtype,
+                 f"overflow {grid} {np.dtype(dtype).name}")
+    print(f"one-pass overflow {grid}^2 {np.dtype(dtype).name}: " +
+          " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
 
 
 # --------------------------------------------------------------------------
