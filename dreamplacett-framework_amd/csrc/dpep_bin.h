@@ -1374,6 +1374,13 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
         item_range(item, sm, e0, e1);
         // both fields of a bin side by side: one 2-element LDS read per bin
         vec2_t<T>* lf = reinterpret_cast<vec2_t<T>*>(smem);
+        vec4_t<T> rg0{};
+        unsigned rm0 = 0u, rn0 = 0u;
+        if (e0 + tid < e1) {                    // the first record, before the rows
+            rn0 = map_record(sm, e0 + tid);
+            rg0 = recg[rn0];
+            rm0 = b.recm[rn0];
+        }
         for (int kg0 = k0; kg0 < k0 + R; kg0 += RG) {
             const int kg1 = kg0 + RG - 1;
             __syncthreads();                    // previous group's readers done
@@ -1414,9 +1421,9 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
             __syncthreads();
             const bool first = kg0 == k0;
             // one record per pass, the next one in flight
-            vec4_t<T> rgn{};
-            unsigned rmn = 0u, rn = 0u;
-            if (e0 + tid < e1) {
+            vec4_t<T> rgn = rg0;
+            unsigned rmn = rm0, rn = rn0;
+            if (kg0 != k0 && e0 + tid < e1) {
                 rn = map_record(sm, e0 + tid);
                 rgn = recg[rn];
                 rmn = b.recm[rn];
