@@ -149,19 +149,18 @@ __device__ __forceinline__ bool load_span(const T* px, const T* py,
                      (double)sy[i], g, c);
 }
 
-// The kCellsPerThread cells of thread tid in the block of NT * kCellsPerThread
-// cells starting at c0 (zero past nc).  A full block loads unconditionally:
-// with a branch per cell the compiler moves each float32 -> float64
-// conversion into the branch and waits there for the load, so the four
-// cells' loads no longer overlap.
-template <typename T, int NT = kBinThreads>
+// The CPT cells of thread tid in the block of NT * CPT cells starting at c0
+// (zero past nc).  A full block loads unconditionally: with a branch per
+// cell the compiler moves each float32 -> float64 conversion into the branch
+// and waits there for the load, so the cells' loads no longer overlap.
+template <typename T, int NT = kBinThreads, int CPT = kCellsPerThread>
 __device__ __forceinline__ void load_cells(const T* __restrict__ px, const T* __restrict__ py,
                                            const T* __restrict__ sx, const T* __restrict__ sy,
                                            int nc, int c0, int tid, T* cx, T* cy, T* cw, T* ch)
 {
-    if (c0 + NT * kCellsPerThread <= nc) {
+    if (c0 + NT * CPT <= nc) {
 #pragma unroll
-        for (int j = 0; j < kCellsPerThread; ++j) {
+        for (int j = 0; j < CPT; ++j) {
             const int i = c0 + tid + j * NT;
             cx[j] = px[i];
             cy[j] = py[i];
@@ -170,7 +169,7 @@ __device__ __forceinline__ void load_cells(const T* __restrict__ px, const T* __
         }
     } else {
 #pragma unroll
-        for (int j = 0; j < kCellsPerThread; ++j) {
+        for (int j = 0; j < CPT; ++j) {
             const int i = c0 + tid + j * NT;
             const bool ok = i < nc;
             cx[j] = ok ? px[i] : (T)0;
@@ -342,7 +341,7 @@ __device__ __forceinline__ void fresh_offsets(const BinArgs& b, unsigned* cur,
 {
     const int tid = threadIdx.x;
     const int S = b.S;
-    const int x = count_slot((int)blockIdx.x * kCellsPerGroup);
+    const int x = count_slot((int)blockIdx.x * kCellsPerGroup, b.qcells);
     const unsigned* row = b.cnt + (size_t)blockIdx.x * S;
     const unsigned* xt = counts_of(b, b.par);
     for (int s = tid; s < S; s += kBinThreads) {
@@ -402,7 +401,7 @@ __device__ __forceinline__ void once_offsets(const BinArgs& b, unsigned* start,
 {
     const int tid = threadIdx.x;
     const int S = b.S;
-    const int x = count_slot((int)blockIdx.x * kOnceCells);
+    const int x = count_slot((int)blockIdx.x * b.qcells, b.qcells);
     const unsigned* prev = counts_of(b, b.par ^ 1);
     const int per = (S + NT - 1) / NT;
     const int r0 = min(tid * per, S), r1 = min(r0 + per, S);
@@ -536,7 +535,8 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_count(
     // atomics over kCountSlots addresses per strip; the returned old total is
     // the block's base within its slot
     unsigned* row = b.cnt + (size_t)blockIdx.x * b.S;
-    unsigned* slot = counts_of(b, b.par) + (size_t)count_slot((int)blockIdx.x * kCellsPerGroup) * b.S;
+    unsigned* slot =
+        counts_of(b, b.par) + (size_t)count_slot((int)blockIdx.x * kCellsPerGroup, b.qcells) * b.S;
     for (int s = tid; s < b.S; s += kBinThreads) {
         const unsigned h = hist[s];
         row[s] = h ? atomicAdd(&slot[s], h) : 0u;
@@ -846,12 +846,13 @@ __host__ __device__ constexpr size_t fill_once_lds(int S)
     return (size_t)(3 * S + kOnceThreads + kChunkCands + 2) * sizeof(unsigned);
 }
 
-// NT = kOnceThreads threads, kCellsPerThread cells each: blocks of twice the
-// cells of K1's, so half the reservation atomics land on each counter and
-// a block's runs in a strip are twice as long.  float32: six waves per
+// NT = kOnceThreads threads, CPT cells each: blocks of QC = NT * CPT cells
+// (b.qcells: counting_block, twice K1's unless that leaves CUs idle), so
+// fewer reservation atomics land on each counter and a block's runs in a
+// strip are longer.  float32: six waves per
 // SIMD, three workgroups per CU, so 1.1 M cells fit the GPU in one round
 // (float64 keeps its registers: it would spill).
-template <typename T>
+template <typename T, int CPT>
 __global__ __launch_bounds__(kOnceThreads, sizeof(T) == 4 ? 6 : 4) void k_bin_fill_once(
     const T* __restrict__ px, const T* __restrict__ py,
     const T* __restrict__ sx, const T* __restrict__ sy, int nc, Grid g,
@@ -865,12 +866,12 @@ __global__ __launch_bounds__(kOnceThreads, sizeof(T) == 4 ? 6 : 4) void k_bin_fi
     unsigned* tmp = cnt + S;
     unsigned* npool = tmp + kOnceThreads + kChunkCands;  // [0] overflow, [1] pool base
     const int tid = threadIdx.x;
-    unsigned* xrow = counts_of(b, b.par) + (size_t)count_slot((int)blockIdx.x * kOnceCells) * S;
+    constexpr int NT = kOnceThreads, QC = NT * CPT;
+    const int c0 = (int)blockIdx.x * QC;
+    unsigned* xrow = counts_of(b, b.par) + (size_t)count_slot(c0, QC) * S;
     // the cells' loads are issued first: their latency overlaps the plan
-    constexpr int NT = kOnceThreads;
-    const int c0 = blockIdx.x * (NT * kCellsPerThread);
-    T cx[kCellsPerThread], cy[kCellsPerThread], cw[kCellsPerThread], chh[kCellsPerThread];
-    load_cells<T, NT>(px, py, sx, sy, nc, c0, tid, cx, cy, cw, chh);
+    T cx[CPT], cy[CPT], cw[CPT], chh[CPT];
+    load_cells<T, NT, CPT>(px, py, sx, sy, nc, c0, tid, cx, cy, cw, chh);
     once_offsets<NT>(b, start, room, cnt, tmp);
     __syncthreads();
     for (int s = tid; s < S; s += NT) cnt[s] = 0u;
@@ -878,12 +879,12 @@ __global__ __launch_bounds__(kOnceThreads, sizeof(T) == 4 ? 6 : 4) void k_bin_fi
     __syncthreads();
     vec4_t<T>* recg = reinterpret_cast<vec4_t<T>*>(b.recg);
     unsigned long long* Bm = reinterpret_cast<unsigned long long*>(b.B);
-    vec4_t<T> geo[kCellsPerThread];
-    unsigned m0[kCellsPerThread], m1[kCellsPerThread], r0[kCellsPerThread],
-        r1[kCellsPerThread], p0[kCellsPerThread], p1[kCellsPerThread];
-    int s0v[kCellsPerThread], s1v[kCellsPerThread];
+    vec4_t<T> geo[CPT];
+    unsigned m0[CPT], m1[CPT], r0[CPT],
+        r1[CPT], p0[CPT], p1[CPT];
+    int s0v[CPT], s1v[CPT];
 #pragma unroll
-    for (int j = 0; j < kCellsPerThread; ++j) {
+    for (int j = 0; j < CPT; ++j) {
         s0v[j] = s1v[j] = -1;
         p0[j] = p1[j] = kPosNone;
         const int i = c0 + tid + j * NT;
@@ -944,7 +945,7 @@ __global__ __launch_bounds__(kOnceThreads, sizeof(T) == 4 ? 6 : 4) void k_bin_fi
     // in the block's overflow, resolved below
     unsigned ovm = 0u;
 #pragma unroll
-    for (int j = 0; j < kCellsPerThread; ++j) {
+    for (int j = 0; j < CPT; ++j) {
         if (s0v[j] < 0) continue;
         if (r0[j] < room[s0v[j]]) {
             p0[j] = start[s0v[j]] + r0[j];
@@ -993,14 +994,14 @@ __global__ __launch_bounds__(kOnceThreads, sizeof(T) == 4 ? 6 : 4) void k_bin_fi
         };
         if (ovm) {
 #pragma unroll
-            for (int j = 0; j < kCellsPerThread; ++j) {
+            for (int j = 0; j < CPT; ++j) {
                 if ((ovm >> (2 * j)) & 1u) place(p0[j], s0v[j], m0[j], geo[j]);
                 if ((ovm >> (2 * j + 1)) & 1u) place(p1[j], s1v[j], m1[j], geo[j]);
             }
         }
     }
 #pragma unroll
-    for (int j = 0; j < kCellsPerThread; ++j) {
+    for (int j = 0; j < CPT; ++j) {
         const int i = c0 + tid + j * NT;
         if (i < nc) b.pos[i] = pos_pair(p0[j], p1[j]);
     }

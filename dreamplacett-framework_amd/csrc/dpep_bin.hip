@@ -43,15 +43,19 @@ hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
                               T* Tt, bool once, hipStream_t s, hipEvent_t* ev)
 {
     b.G1 = (int)g1_of(nc);
+    b.qcells = counting_block(nc, b.cus);
     if (b.R != strip_rows(g.N)) return hipErrorInvalidValue;   // the kernel's R
     if (once && b.pool_cap < 2u * (unsigned)(nc > 0 ? nc : 0)) return hipErrorInvalidValue;
     hipError_t e;
     if (once) {
         if (ev && (e = hipEventRecord(ev[0], s))) return e;
-        const int per = kOnceThreads * kCellsPerThread;
-        const unsigned grid = (unsigned)(nc > per ? (nc + per - 1) / per : 1);
-        k_bin_fill_once<T><<<grid, kOnceThreads, fill_once_lds(b.S), s>>>(px, py, sx, sy, nc,
-                                                                          g, b);
+        const unsigned grid = (unsigned)(nc > b.qcells ? (nc + b.qcells - 1) / b.qcells : 1);
+        if (b.qcells == kOnceCells)
+            k_bin_fill_once<T, kCellsPerThread><<<grid, kOnceThreads, fill_once_lds(b.S), s>>>(
+                px, py, sx, sy, nc, g, b);
+        else
+            k_bin_fill_once<T, kCellsPerThread / 2><<<grid, kOnceThreads, fill_once_lds(b.S), s>>>(
+                px, py, sx, sy, nc, g, b);
     } else {
         const size_t count_lds = (size_t)b.S * sizeof(unsigned);
         const bool staged = b.S >= kStageMinStrips;
@@ -151,7 +155,11 @@ static hipError_t prepare_bin_type()
                                  (int)fill_lds_staged<T>(sizeof(T) == 4 ? 4096 : 1024))))
         return e;
     // the one-pass K3's strip tables: at most 8192 * 8192 bins in 2-row strips
-    if ((e = hipFuncSetAttribute((const void*)k_bin_fill_once<T>,
+    if ((e = hipFuncSetAttribute((const void*)k_bin_fill_once<T, kCellsPerThread>,
+                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 (int)fill_once_lds(4096))))
+        return e;
+    if ((e = hipFuncSetAttribute((const void*)k_bin_fill_once<T, kCellsPerThread / 2>,
                                  hipFuncAttributeMaxDynamicSharedMemorySize,
                                  (int)fill_once_lds(4096))))
         return e;

@@ -67,13 +67,17 @@ constexpr int kBinThreads = 256;       // K1 / K3 workgroup size
 constexpr int kCellsPerThread = 4;     // K1 / K3 cells per thread
 constexpr int kCellsPerGroup = kBinThreads * kCellsPerThread;
 constexpr int kOnceThreads = 512;      // one-pass K3 workgroup size
-constexpr int kOnceCells = kOnceThreads * kCellsPerThread;
+constexpr int kOnceCells = kOnceThreads * kCellsPerThread;   // its largest block
 constexpr int kAccThreads = 1024;      // K4 workgroup size
 constexpr int kCountSlots = 8;         // strip-total counters per strip
-// The count slot of the cells of block [c0, c0 + ...): by blocks of
-// kOnceCells cells in every kernel that counts, so a fresh step's counts
-// size a one-pass step's regions slot by slot.
-__host__ __device__ constexpr int count_slot(int c0) { return (c0 / kOnceCells) % kCountSlots; }
+// The count slot of the cells of block [c0, c0 + ...): by blocks of `unit`
+// cells (the step's one-pass block, BinArgs::qcells) in every kernel that
+// counts, so a fresh step's counts size a one-pass step's regions slot by
+// slot.
+__host__ __device__ constexpr int count_slot(int c0, int unit)
+{
+    return (c0 >> __builtin_ctz((unsigned)unit)) & (kCountSlots - 1);   // unit: 2^k
+}
 constexpr int kMaxSpanY = 4095;        // larger y spans take the tall path
 constexpr int kSideBits = 128;         // column blocks tracked per strip in B
 constexpr int kSideWords = kSideBits / 32;
@@ -120,6 +124,9 @@ struct BinArgs {
     int tight;              // 1: size each region at half its previous count,
                             // so the step overflows (tests only)
     int par;                // parity of this step: its set of counts
+    int cus;                // CUs of the device
+    int qcells;             // cells per one-pass block, the unit of the count
+                            // slots (set per step: counting_block)
     unsigned reg_cap;       // records the regions of a plan may hold in total
     unsigned pool0;         // record number of the overflow pool's first entry
     unsigned pool_cap;      // capacity of the overflow pool (0: fresh-only)
@@ -223,10 +230,20 @@ inline void make_spectral_args(SpectralArgs& a, const Grid& g, int dtype, bool p
 // at least one workgroup per strip).
 inline void set_item_grids(BinArgs& b, int acc_per_cu, int gat_per_cu, int cus)
 {
+    b.cus = cus > 0 ? cus : 1;
     b.Pacc = (acc_per_cu > 0 ? acc_per_cu : 1) * (cus > 0 ? cus : 1);
     b.Pgat = (gat_per_cu > 0 ? gat_per_cu : 1) * (cus > 0 ? cus : 1);
     b.Wacc = b.Pacc > b.S ? b.Pacc : b.S;
     b.Wgat = b.Pgat > b.S ? b.Pgat : b.S;
+}
+
+// The cells per counting block of a step with nc cells: kOnceCells when
+// that still gives every CU two blocks, else half of it (at 210 k cells,
+// 103 blocks of 2048 would leave most CUs idle in the one-pass K3).
+inline int counting_block(int nc, int cus)
+{
+    const long long blocks = ((long long)(nc > 0 ? nc : 0) + kOnceCells - 1) / kOnceCells;
+    return blocks >= 2LL * (cus > 0 ? cus : 1) ? kOnceCells : kOnceCells / 2;
 }
 
 // Strip-binned scatter (K1 unless `once`, K3, K4; K4 also runs the row DCT,

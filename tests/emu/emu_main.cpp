@@ -192,10 +192,15 @@ static int run(int nc, bool det, bool pot, int ch, bool tall, bool force_stage)
     unsigned pool_seen = 0;
     // one step: fresh (K1 + K3) or in one pass on the previous step's counts
     auto step = [&](bool once) -> int {
+        b.qcells = counting_block(nc, b.cus);   // as launch_bin_scatter sets it
         if (once) {
-            const int per = kOnceThreads * kCellsPerThread;
-            launch(nc > per ? (nc + per - 1) / per : 1, kOnceThreads, fill_once_lds(p.S),
-                   [&] { k_bin_fill_once<T>(px, py, sx, sy, nc, g, b); });
+            const unsigned grid = nc > b.qcells ? (nc + b.qcells - 1) / b.qcells : 1;
+            if (b.qcells == kOnceCells)
+                launch(grid, kOnceThreads, fill_once_lds(p.S),
+                       [&] { k_bin_fill_once<T, kCellsPerThread>(px, py, sx, sy, nc, g, b); });
+            else
+                launch(grid, kOnceThreads, fill_once_lds(p.S),
+                       [&] { k_bin_fill_once<T, kCellsPerThread / 2>(px, py, sx, sy, nc, g, b); });
         } else {
             launch(b.G1, kBinThreads, hist, [&] { k_bin_count<T>(px, py, sx, sy, nc, g, b); });
             if (stage)
@@ -265,8 +270,9 @@ static int run(int nc, bool det, bool pot, int ch, bool tall, bool force_stage)
             fprintf(stderr, "overflowing step differs from the planned one in output %d\n", k);
             return 4;
         }
-    printf("emu plan S=%d R=%d chunks=%u/%u items=%u/%u of %d/%d overflow=%u\n", p.S, p.R,
-           b.chunk[0], b.chunk[1], b.nitems[0], b.nitems[1], b.Wacc, b.Wgat, pool_tight);
+    printf("emu plan S=%d R=%d chunks=%u/%u items=%u/%u of %d/%d block=%d overflow=%u\n", p.S,
+           p.R, b.chunk[0], b.chunk[1], b.nitems[0], b.nitems[1], b.Wacc, b.Wgat, b.qcells,
+           pool_tight);
 
     // oracle
     std::vector<double> dpx(nc), dpy(nc), dsx(nc), dsy(nc), dd0(mn), rho(mn), rphi(mn), rfx(mn), rfy(mn), rgx(nc), rgy(nc);
