@@ -1530,11 +1530,14 @@ __global__ __launch_bounds__(256) void k_fixed_flush(unsigned long long* __restr
 // ---------------------------------------------------------------------------
 // LDS of G2: the tall-cell count and list, one bit per list entry marking
 // the cells too large for a team, and the workgroup-wide reduction buffer
-constexpr size_t kGatherOutLds =
-    ((1 + kCellsPerGroup + kCellsPerGroup / 32) * sizeof(unsigned) + 15) / 16 * 16 +
-    2 * kBinThreads * sizeof(double);
+template <int NT, int CPT>
+__host__ __device__ constexpr size_t gather_out_lds()
+{
+    return ((1 + NT * CPT + NT * CPT / 32) * sizeof(unsigned) + 15) / 16 * 16 +
+           2 * NT * sizeof(double);
+}
 
-template <typename T>
+template <typename T, int NT>
 __device__ __forceinline__ void gather_tall(int i, const T* __restrict__ px,
                                             const T* __restrict__ py,
                                             const T* __restrict__ sx,
@@ -1550,7 +1553,7 @@ __device__ __forceinline__ void gather_tall(int i, const T* __restrict__ px,
     if (ok) {
         const int ny1 = c.byh - c.byl + 1;
         const long long nb = (long long)(c.bxh - c.bxl + 1) * ny1;
-        for (long long e = tid; e < nb; e += kBinThreads) {
+        for (long long e = tid; e < nb; e += NT) {
             const int k = c.bxl + (int)(e / ny1), q = c.byl + (int)(e % ny1);
             const double tx = overlap_1d(c.x, c.w, g.xl, g.bsx, k);
             const double ty = overlap_1d(c.y, c.h, g.yl, g.bsy, q);
@@ -1563,19 +1566,19 @@ __device__ __forceinline__ void gather_tall(int i, const T* __restrict__ px,
         }
     }
     red[tid] = ax;
-    red[kBinThreads + tid] = ay;
+    red[NT + tid] = ay;
     __syncthreads();
-    for (int h = kBinThreads / 2; h > 0; h >>= 1) {
+    for (int h = NT / 2; h > 0; h >>= 1) {
         if (tid < h) {
             red[tid] += red[tid + h];
-            red[kBinThreads + tid] += red[kBinThreads + tid + h];
+            red[NT + tid] += red[NT + tid + h];
         }
         __syncthreads();
     }
     if (tid == 0) {
         const double rat = ok ? c.ratio() : 0.0;
         gx[i] = ok ? (T)(red[0] * rat) : (T)0;
-        gy[i] = ok ? (T)(red[kBinThreads] * rat) : (T)0;
+        gy[i] = ok ? (T)(red[NT] * rat) : (T)0;
     }
     __syncthreads();                      // red is reused by the next cell
 }
@@ -1630,13 +1633,13 @@ __device__ __forceinline__ bool gather_tall_team(int i, int lane, const T* __res
     return true;
 }
 
-// One workgroup per K3 block of kCellsPerGroup cells (same cell-to-thread
-// map): the records of a block sit in one short run per strip, so the
-// block's partials are read by one CU while they are still in its caches.
+// One workgroup of NT threads per one-pass K3 block of NT * CPT cells (the
+// same cell-to-thread map): the records of a block sit in one short run per
+// strip, so each run's partials are read whole, by one CU.
 // Tall cells: a team of kTallTeam threads per cell of at most kTallTeamBins
 // bins, larger ones one at a time by the whole workgroup.
-template <typename T>
-__global__ __launch_bounds__(kBinThreads) void k_gather_out(
+template <typename T, int NT, int CPT>
+__global__ __launch_bounds__(NT) void k_gather_out(
     const T* __restrict__ px, const T* __restrict__ py,
     const T* __restrict__ sx, const T* __restrict__ sy, int nc, Grid g,
     BinArgs b, const T* __restrict__ fx, const T* __restrict__ fy,
@@ -1645,31 +1648,32 @@ __global__ __launch_bounds__(kBinThreads) void k_gather_out(
     extern __shared__ __align__(16) unsigned char smem[];
     unsigned* ntall = reinterpret_cast<unsigned*>(smem);
     unsigned* list = ntall + 1;
-    unsigned* large = list + kCellsPerGroup;
+    constexpr int QC = NT * CPT;                // cells of the block
+    unsigned* large = list + QC;
     double* red = reinterpret_cast<double*>(
-        smem + ((1 + kCellsPerGroup + kCellsPerGroup / 32) * sizeof(unsigned) + 15) / 16 * 16);
+        smem + ((1 + QC + QC / 32) * sizeof(unsigned) + 15) / 16 * 16);
     if (threadIdx.x == 0) *ntall = 0u;
-    if (threadIdx.x < kCellsPerGroup / 32) large[threadIdx.x] = 0u;
+    if (threadIdx.x < QC / 32) large[threadIdx.x] = 0u;
     __syncthreads();
-    const int c0 = blockIdx.x * kCellsPerGroup + threadIdx.x;
+    const int c0 = blockIdx.x * QC + threadIdx.x;
     const vec2_t<T>* res = reinterpret_cast<const vec2_t<T>*>(b.gtmp);
-    unsigned p[kCellsPerThread], p2[kCellsPerThread];
+    unsigned p[CPT], p2[CPT];
 #pragma unroll
-    for (int j = 0; j < kCellsPerThread; ++j) {
-        const int i = c0 + j * kBinThreads;
+    for (int j = 0; j < CPT; ++j) {
+        const int i = c0 + j * NT;
         const unsigned long long pp = i < nc ? b.pos[i] : pos_pair(kPosNone, kPosNone);
         p[j] = (unsigned)pp;
         p2[j] = (unsigned)(pp >> 32);
     }
-    vec2_t<T> v[kCellsPerThread], v2[kCellsPerThread];
+    vec2_t<T> v[CPT], v2[CPT];
 #pragma unroll
-    for (int j = 0; j < kCellsPerThread; ++j) {
+    for (int j = 0; j < CPT; ++j) {
         v[j] = p[j] < kPosNone ? res[p[j]] : vec2_t<T>{(T)0, (T)0};
         v2[j] = p2[j] < kPosNone ? res[p2[j]] : vec2_t<T>{(T)0, (T)0};
     }
 #pragma unroll
-    for (int j = 0; j < kCellsPerThread; ++j) {
-        const int i = c0 + j * kBinThreads;
+    for (int j = 0; j < CPT; ++j) {
+        const int i = c0 + j * NT;
         if (i >= nc) break;
         if (p[j] == kPosTall) {
             list[atomicAdd(ntall, 1u)] = (unsigned)i;
@@ -1683,7 +1687,7 @@ __global__ __launch_bounds__(kBinThreads) void k_gather_out(
     if (n == 0u) return;
     // one team per tall cell; a team's lane 0 marks the cells too large for
     // it, which the whole workgroup gathers afterwards
-    constexpr int kTeams = kBinThreads / kTallTeam;
+    constexpr int kTeams = NT / kTallTeam;
     const int team = threadIdx.x / kTallTeam, lane = threadIdx.x % kTallTeam;
     for (unsigned t = team; t < n; t += kTeams)
         if (!gather_tall_team<T>((int)list[t], lane, px, py, sx, sy, g, fx, fy, gx, gy) &&
@@ -1692,7 +1696,7 @@ __global__ __launch_bounds__(kBinThreads) void k_gather_out(
     __syncthreads();
     for (unsigned t = 0; t < n; ++t)          // uniform across the group
         if ((large[t >> 5] >> (t & 31u)) & 1u)
-            gather_tall<T>((int)list[t], px, py, sx, sy, g, fx, fy, red, gx, gy);
+            gather_tall<T, NT>((int)list[t], px, py, sx, sy, g, fx, fy, red, gx, gy);
 }
 
 }  // namespace dpep

@@ -95,8 +95,17 @@ hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
     hipError_t e = hipGetLastError();
     if (e) return e;
     if (ev && (e = hipEventRecord(ev, s))) return e;
-    k_gather_out<T><<<g1_of(nc), kBinThreads, kGatherOutLds, s>>>(px, py, sx, sy, nc, g, b, fx,
-                                                                  fy, gx, gy);
+    // blocks of the one-pass K3's cells
+    const int qc = counting_block(nc, b.cus);
+    const unsigned grid = (unsigned)((nc + qc - 1) / qc);
+    if (qc == kOnceCells)
+        k_gather_out<T, kOnceThreads, kCellsPerThread>
+            <<<grid, kOnceThreads, gather_out_lds<kOnceThreads, kCellsPerThread>(), s>>>(
+                px, py, sx, sy, nc, g, b, fx, fy, gx, gy);
+    else
+        k_gather_out<T, kOnceThreads, kCellsPerThread / 2>
+            <<<grid, kOnceThreads, gather_out_lds<kOnceThreads, kCellsPerThread / 2>(), s>>>(
+                px, py, sx, sy, nc, g, b, fx, fy, gx, gy);
     return hipGetLastError();
 }
 

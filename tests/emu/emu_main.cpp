@@ -232,8 +232,18 @@ static int run(int nc, bool det, bool pot, int ch, bool tall, bool force_stage)
         if (nc > 0) {
             const size_t glds = (size_t)gather_rows<T>(p.R, N) * N * 2 * sizeof(T);
             launch(b.Wgat, kAccThreads, glds, [&] { k_gather_bin<T>(g, b, fx, fy); });
-            launch(b.G1, kBinThreads, kGatherOutLds,
-                   [&] { k_gather_out<T>(px, py, sx, sy, nc, g, b, fx, fy, gx, gy); });
+            const int qc = counting_block(nc, b.cus);   // as launch_bin_gather
+            const unsigned gg = (unsigned)((nc + qc - 1) / qc);
+            if (qc == kOnceCells)
+                launch(gg, kOnceThreads, gather_out_lds<kOnceThreads, kCellsPerThread>(), [&] {
+                    k_gather_out<T, kOnceThreads, kCellsPerThread>(px, py, sx, sy, nc, g, b, fx,
+                                                                   fy, gx, gy);
+                });
+            else
+                launch(gg, kOnceThreads, gather_out_lds<kOnceThreads, kCellsPerThread / 2>(), [&] {
+                    k_gather_out<T, kOnceThreads, kCellsPerThread / 2>(px, py, sx, sy, nc, g, b,
+                                                                       fx, fy, gx, gy);
+                });
         }
         // the older set of counts is zero again for the next step
         const unsigned* older = b.xtot + (size_t)(b.par ^ 1) * nslot;
