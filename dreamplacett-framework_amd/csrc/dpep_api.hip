@@ -82,10 +82,12 @@ struct dpep_ctx {
     hipEvent_t ev_x0 = nullptr, ev_x1 = nullptr;
     // per-kernel profiling: a ring of `prof_slots` event sets, one per step
     std::vector<hipEvent_t> prof_ev;   // prof_slots * (kNumStages + 1)
+    std::vector<unsigned char> prof_once;   // per slot: that step ran no count kernel
     int profiling = 0;
     int prof_slots = 0;
     long prof_steps = 0;               // steps recorded since enabling
     int nc = -1;                 // resident cells (-1: none uploaded)
+    int nc_sizes = 0;            // cells whose sizes are resident in d_sx, d_sy
     int last_nc = 0;             // cells of the last computed step
     int stepped = 0;
     // the last step left its counts for this one (parity par ^ 1): fill in
@@ -194,7 +196,10 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
     // only when the caller asked for per-step timings
     const bool timed = (c->flags & DPEP_FLAG_STEP_TIMINGS) != 0;
     if (timed) HIP_TRY(hipEventRecord(c->ev[0], s));
-    if (prof) HIP_TRY(hipEventRecord(pe[0], s));
+    if (prof) {
+        c->prof_once[(size_t)(c->prof_steps % c->prof_slots)] = once ? 1 : 0;
+        HIP_TRY(hipEventRecord(pe[0], s));
+    }
     HIP_TRY(launch_bin_scatter<T>(px, py, sx, sy, nc, c->grid, c->bins, c->sargs, d0n,
                                   dens, (T*)c->d_T, once, s, prof ? pe + 1 : nullptr));
 
@@ -280,7 +285,7 @@ int dpep_abi_version(void) { return DPEP_ABI_VERSION; }
 
 const char* dpep_build_info(void)
 {
-    return "dpep abi 4; HIP kernels for gfx950; scatter/P1/P2/P3/gather";
+    return "dpep abi 5; HIP kernels for gfx950; scatter/P1/P2/P3/gather";
 }
 
 const char* dpep_last_error(void) { return g_last_error.c_str(); }
@@ -468,19 +473,29 @@ int dpep_set_cells(dpep_ctx* c, const void* px, const void* py,
     if (int rc = check_ctx(c)) return rc;
     if (nc < 0 || nc > c->nc_max)
         return fail(DPEP_ERR_ARG, "nc=%d outside [0, nc_max=%d]", nc, c->nc_max);
-    if (nc > 0 && (!px || !py || !sx || !sy))
+    const bool keep_sizes = !sx && !sy;      // positions only
+    if (nc > 0 && (!px || !py || (!keep_sizes && (!sx || !sy))))
         return fail(DPEP_ERR_ARG, "cell array is NULL");
+    if (keep_sizes && nc > c->nc_sizes)
+        return fail(DPEP_ERR_STATE,
+                    "sizes kept (sx, sy NULL) for nc=%d cells, but only %d have resident sizes",
+                    nc, c->nc_sizes);
     const size_t bytes = (size_t)nc * c->esz;
     HIP_TRY(hipEventRecord(c->ev_x0, c->stream));
     if (nc > 0) {
         HIP_TRY(hipMemcpyAsync(c->d_px, px, bytes, hipMemcpyHostToDevice, c->stream));
         HIP_TRY(hipMemcpyAsync(c->d_py, py, bytes, hipMemcpyHostToDevice, c->stream));
-        HIP_TRY(hipMemcpyAsync(c->d_sx, sx, bytes, hipMemcpyHostToDevice, c->stream));
-        HIP_TRY(hipMemcpyAsync(c->d_sy, sy, bytes, hipMemcpyHostToDevice, c->stream));
+        if (!keep_sizes) {
+            // the sizes change: none stay valid until the copies are in
+            c->nc_sizes = 0;
+            HIP_TRY(hipMemcpyAsync(c->d_sx, sx, bytes, hipMemcpyHostToDevice, c->stream));
+            HIP_TRY(hipMemcpyAsync(c->d_sy, sy, bytes, hipMemcpyHostToDevice, c->stream));
+        }
     }
     HIP_TRY(hipEventRecord(c->ev_x1, c->stream));
     HIP_TRY(hipEventSynchronize(c->ev_x1));
     c->h2d_ms = elapsed(c->ev_x0, c->ev_x1);
+    if (!keep_sizes) c->nc_sizes = nc;
     c->nc = nc;
     c->valid = 0u;          // the outputs no longer describe the resident cells
     return DPEP_OK;
@@ -641,7 +656,9 @@ int dpep_get_kernel_times(dpep_ctx* c, float* out, int n)
     const long steps = c->prof_steps < c->prof_slots ? c->prof_steps : c->prof_slots;
     for (long k = 0; k < steps; ++k) {
         const hipEvent_t* pe = &c->prof_ev[(size_t)k * (kNumStages + 1)];
-        for (int i = 0; i < kNumStages && i < n; ++i)
+        // a one-pass step launches no count kernel: its [0] interval is the
+        // two events' own cost, not a kernel's
+        for (int i = c->prof_once[(size_t)k] ? 1 : 0; i < kNumStages && i < n; ++i)
             out[i] += 1000.f * elapsed(pe[i], pe[i + 1]);
         if (n > kNumStages) out[kNumStages] += 1000.f * elapsed(pe[0], pe[kNumStages]);
     }
@@ -663,6 +680,7 @@ int dpep_set_profiling(dpep_ctx* c, int slots)
     c->prof_steps = 0;
     if (slots == 0) return DPEP_OK;
     c->prof_ev.assign((size_t)slots * (kNumStages + 1), nullptr);
+    c->prof_once.assign((size_t)slots, 0);
     for (auto& e : c->prof_ev) HIP_TRY(hipEventCreate(&e));
     c->prof_slots = slots;
     c->profiling = 1;

@@ -52,6 +52,8 @@ constexpr uint32_t kIdle = 0, kGo = 1, kDone = 2, kQuit = 3;
 constexpr size_t kHeader = 64;
 constexpr uint32_t kMagicV2 = 0x32504544u;
 constexpr uint32_t kOutDensity = 1u, kOutPotential = 2u, kOutGrads = 4u, kOutNoFields = 8u;
+// input bit of the same word: the client did not rewrite the size slots
+constexpr uint32_t kInKeepSizes = 0x10u;
 constexpr uint32_t kGatherModeHip = 16u;
 
 double now_ms()
@@ -351,9 +353,15 @@ int main(int argc, char** argv)
         const bool want_phi = (outs & kOutPotential) != 0;
         const bool want_grads = (outs & kOutGrads) != 0;
         const size_t ncb = (size_t)nc * sizeof(float);
-        pool.copy({{h_px, shm_px, ncb}, {h_py, shm_py, ncb}, {h_sx, shm_sx, ncb},
-                   {h_sy, shm_sy, ncb}});
-        if (dpep_set_cells(ctx, h_px, h_py, h_sx, h_sy, nc) != DPEP_OK) fatal("dpep_set_cells");
+        const bool keep_sizes = (outs & kInKeepSizes) != 0;
+        if (keep_sizes)
+            pool.copy({{h_px, shm_px, ncb}, {h_py, shm_py, ncb}});
+        else
+            pool.copy({{h_px, shm_px, ncb}, {h_py, shm_py, ncb}, {h_sx, shm_sx, ncb},
+                       {h_sy, shm_sy, ncb}});
+        if (dpep_set_cells(ctx, h_px, h_py, keep_sizes ? nullptr : h_sx,
+                           keep_sizes ? nullptr : h_sy, nc) != DPEP_OK)
+            fatal("dpep_set_cells");
         if (dpep_compute(ctx) != DPEP_OK) fatal("dpep_compute");
         if (dpep_get_outputs(ctx, want_dens ? h_dens : nullptr, want_phi ? h_phi : nullptr,
                              want_fields ? h_fx : nullptr, want_fields ? h_fy : nullptr,

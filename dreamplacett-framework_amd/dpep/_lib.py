@@ -89,6 +89,10 @@ class DpepError(RuntimeError):
     """A HIP runtime failure reported by libdpep."""
 
 
+# DPEP_ABI_VERSION of include/dpep.h this binding is written against
+ABI_VERSION = 5
+
+
 def load_library(path: Optional[str] = None) -> ctypes.CDLL:
     """Loads libdpep.so and declares every C ABI signature.
 
@@ -108,6 +112,9 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
+    if ABI_VERSION is not None and lib.dpep_abi_version() != ABI_VERSION:
+        raise ImportError(f"{p} has C ABI version {lib.dpep_abi_version()}, this binding "
+                          f"needs {ABI_VERSION}: rebuild the library")
     if path is None:
         _lib = lib
     return lib
@@ -280,22 +287,27 @@ class Context:
             raise RuntimeError("context was created without pinned=True")
         return dict(self._in)
 
-    def set_cells(self, px, py, sx, sy) -> None:
+    def set_cells(self, px, py, sx=None, sy=None) -> None:
+        """Uploads the cells.  sx and sy both None: positions only, the cells
+        keep the sizes of the last call that passed them (which must have
+        covered at least as many cells)."""
         n = int(np.asarray(px).size)
         if n > self.nc_max:
             raise ValueError(f"nc={n} exceeds nc_max={self.nc_max}")
-        arrs = [self._arr(a, n, nm) for a, nm in ((px, "px"), (py, "py"),
-                                                    (sx, "sx"), (sy, "sy"))]
+        if (sx is None) != (sy is None):
+            raise ValueError("sx and sy: pass both or neither")
+        names = ("px", "py") if sx is None else ("px", "py", "sx", "sy")
+        arrs = [self._arr(a, n, nm) for a, nm in zip((px, py, sx, sy), names)]
         if self._pin is not None:
             staged = []
-            for a, name in zip(arrs, ("px", "py", "sx", "sy")):
+            for a, name in zip(arrs, names):
                 dst = self._in[name]
                 if a.ctypes.data != dst.ctypes.data:     # not already staged
                     dst[:n] = a
                 staged.append(dst)
             arrs = staged
-        _check(self._lib.dpep_set_cells(self.handle, *[_ptr(a) for a in arrs], n),
-               "dpep_set_cells", self._lib)
+        ptrs = [_ptr(a) for a in arrs] + [None] * (4 - len(arrs))
+        _check(self._lib.dpep_set_cells(self.handle, *ptrs, n), "dpep_set_cells", self._lib)
         self._nc = n
 
     def compute(self) -> None:
@@ -345,9 +357,11 @@ class Context:
                "dpep_get_scatter_density", self._lib)
         return d
 
-    def step(self, px, py, sx, sy, outputs=None, copy=True) -> Dict[str, np.ndarray]:
+    def step(self, px, py, sx=None, sy=None, outputs=None,
+             copy=True) -> Dict[str, np.ndarray]:
         """set_cells + compute + get_outputs.  outputs: names from
-        OUTPUT_NAMES to fetch (default: all this context computes)."""
+        OUTPUT_NAMES to fetch (default: all this context computes); sx, sy
+        None keep the resident sizes (set_cells)."""
         self.set_cells(px, py, sx, sy)
         self.compute()
         if outputs is None:

@@ -111,6 +111,7 @@ class ScatterTTNNClient:
         self._ctx = None                     # in-process dpep.Context
         self._d0_pending: Optional[np.ndarray] = None
         self._outputs = frozenset(_ALL_OUTPUTS)
+        self._nc_sizes = 0                  # cells whose sizes the GPU side holds
         self.last_outputs: Dict[str, np.ndarray] = {}
 
     # -- shared memory -------------------------------------------------------
@@ -233,6 +234,7 @@ class ScatterTTNNClient:
                 self._kill()
         self._close_shm()
         self._ready = False
+        self._nc_sizes = 0
 
     # -- per-step call -----------------------------------------------------------
     def set_initial_density(self, init_density_normalized) -> None:
@@ -261,7 +263,10 @@ class ScatterTTNNClient:
         if self._mm is not None:
             S.set_outputs(self._mm, S.outputs_of(names))
 
-    def call(self, px, py, sx, sy) -> Tuple[object, object, dict]:
+    def call(self, px, py, sx=None, sy=None) -> Tuple[object, object, dict]:
+        """One step; returns (field_x, field_y, timing).  sx, sy None: the
+        cells keep the sizes of the last call that passed them (positions
+        alone cross the link)."""
         out, timing = self._step(px, py, sx, sy)
         if "field_x" not in out:
             raise RuntimeError("call() needs the fields: set_outputs() excluded them")
@@ -272,10 +277,10 @@ class ScatterTTNNClient:
             fx, fy = torch.from_numpy(fx), torch.from_numpy(fy)
         return fx, fy, timing
 
-    def call_full(self, px, py, sx, sy) -> Dict[str, object]:
+    def call_full(self, px, py, sx=None, sy=None) -> Dict[str, object]:
         """One step; returns the outputs set_outputs() selected (numpy; by
         default density, potential, field_x, field_y, grad_x, grad_y) and
-        timing."""
+        timing.  sx, sy None keep the sizes, as in call()."""
         out, timing = self._step(px, py, sx, sy)
         out = dict(out)
         out["timing"] = timing
@@ -287,15 +292,27 @@ class ScatterTTNNClient:
         nc = int(np.asarray(px).size)
         if nc > self.nc_max:
             raise ValueError(f"nc={nc} exceeds nc_max={self.nc_max}")
+        keep = sx is None and sy is None
+        if not keep and (sx is None or sy is None):
+            raise ValueError("sx and sy: pass both or neither")
+        if keep and nc > self._nc_sizes:
+            raise ValueError(f"sizes kept for nc={nc} cells, but only {self._nc_sizes} "
+                             "have sizes from an earlier call")
         if self._ctx is not None:
-            return self._step_inprocess(px, py, sx, sy, nc)
+            out = self._step_inprocess(px, py, sx, sy, nc)
+            if not keep:
+                self._nc_sizes = nc
+            return out
 
         v = self._views
         t0 = time.perf_counter()
-        for name, a in (("px", px), ("py", py), ("sx", sx), ("sy", sy)):
+        slots = (("px", px), ("py", py)) + (() if keep else (("sx", sx), ("sy", sy)))
+        for name, a in slots:
             v[name][:nc] = np.asarray(a, dtype=np.float32)
             v[name][nc:] = 0.0
         pos_write_ms = (time.perf_counter() - t0) * 1e3
+        word = S.outputs_of(self._outputs) | (S.IN_KEEP_SIZES if keep else 0)
+        S.set_outputs(self._mm, word)
         # nc before state (ordering on non-TSO hosts, :462-464)
         struct.pack_into("<i", self._mm, S.OFF_NC, nc)
         struct.pack_into("<I", self._mm, S.OFF_STATE, S.STATE_GO)
@@ -311,6 +328,8 @@ class ScatterTTNNClient:
                 raise TimeoutError("timeout waiting for shm DONE")
             time.sleep(0.0002)
         kernel_wait_ms = (time.perf_counter() - t0) * 1e3
+        if not keep:
+            self._nc_sizes = nc
         _, _, tm, gm = S.read_timings(self._mm)
         struct.pack_into("<I", self._mm, S.OFF_STATE, S.STATE_IDLE)
         t0 = time.perf_counter()
@@ -335,11 +354,12 @@ class ScatterTTNNClient:
         ctx = self._ctx
         t0 = time.perf_counter()
         cells = ctx.host_cells()
-        for name, a in (("px", px), ("py", py), ("sx", sx), ("sy", sy)):
+        names = ("px", "py") if sx is None else ("px", "py", "sx", "sy")
+        for name, a in zip(names, (px, py, sx, sy)):
             cells[name][:nc] = np.asarray(a, dtype=np.float32)
         pos_write_ms = (time.perf_counter() - t0) * 1e3
         t0 = time.perf_counter()
-        ctx.set_cells(*(cells[k][:nc] for k in ("px", "py", "sx", "sy")))
+        ctx.set_cells(*(cells[k][:nc] for k in names))
         ctx.compute()
         want = set(self._outputs)
         cpu_dct = _cpu_dct()
@@ -414,8 +434,14 @@ def make_forward(client: ScatterTTNNClient, keep_field_maps: bool = False,
     CPU_DCT=1, where they come from DREAMPlace's own CPU transforms of the
     returned density plus the initial density, :804-829).  With
     V13_USE_CPU_AFTER_ITER=n, iterations after the n-th call
-    original_forward instead (:540-604)."""
+    original_forward instead (:540-604).
+
+    DREAMPlace passes the same size tensors to every iteration.  While they
+    are the same torch tensors, unmodified (their version counters
+    unchanged), only the positions cross to the GPU; any other size input
+    is sent every call."""
     iteration = [0]
+    sizes_sent = {}     # key, the size tensors (held: ids stay theirs), sx, sy
 
     def _forward(ctx, pos, node_size_x_clamped, node_size_y_clamped,
                  offset_x, offset_y, ratio, bin_center_x, bin_center_y,
@@ -463,13 +489,22 @@ def make_forward(client: ScatterTTNNClient, keep_field_maps: bool = False,
         posn = _to_numpy(pos)
         # layout [movable | fixed terminals | filler] (:611-617); original
         # sizes = clamped + 2 * offset (:632-633): the GPU stretches itself
-        osx = _to_numpy(node_size_x_clamped + 2.0 * offset_x)
-        osy = _to_numpy(node_size_y_clamped + 2.0 * offset_y)
         px = np.concatenate([posn[:n_mov], posn[num_nodes - n_fil:num_nodes]])
         py = np.concatenate([posn[num_nodes:num_nodes + n_mov],
                              posn[2 * num_nodes - n_fil:2 * num_nodes]])
-        sx = np.concatenate([osx[:n_mov], osx[num_nodes - n_fil:num_nodes]])
-        sy = np.concatenate([osy[:n_mov], osy[num_nodes - n_fil:num_nodes]])
+        srcs = (node_size_x_clamped, node_size_y_clamped, offset_x, offset_y)
+        versions = tuple(getattr(t, "_version", None) for t in srcs)
+        key = (tuple(id(t) for t in srcs), versions, num_nodes, n_mov, n_fil)
+        resend = (None in versions or sizes_sent.get("key") != key or
+                  client._nc_sizes < px.size)
+        if resend:
+            osx = _to_numpy(node_size_x_clamped + 2.0 * offset_x)
+            osy = _to_numpy(node_size_y_clamped + 2.0 * offset_y)
+            sx = np.concatenate([osx[:n_mov], osx[num_nodes - n_fil:num_nodes]])
+            sy = np.concatenate([osy[:n_mov], osy[num_nodes - n_fil:num_nodes]])
+            sizes_sent.update(key=key, srcs=srcs, sx=sx, sy=sy)
+        else:
+            sx, sy = sizes_sent["sx"], sizes_sent["sy"]
         bin_area = float(bin_size_x) * float(bin_size_y)
         if not client._ready:
             client.xl, client.yl = float(xl), float(yl)
@@ -483,7 +518,8 @@ def make_forward(client: ScatterTTNNClient, keep_field_maps: bool = False,
                 wanted |= {"density"}
             client.set_outputs(wanted)
             client.start(nc_actual=px.size)
-        out = client.call_full(px, py, sx, sy)
+        out = (client.call_full(px, py, sx, sy) if resend else
+               client.call_full(px, py))
         timing = out["timing"]
 
         if cpu_dct:

@@ -27,7 +27,10 @@ and, in the header padding:
         [48:52] magic        u32  0x32504544 ("DEP2")
         [52:56] version      u32  2
         [56:60] outputs      u32  bit 0 density, bit 1 potential, bit 2 grads,
-                                  bit 3 no fields (field_x/field_y not written)
+                                  bit 3 no fields (field_x/field_y not written),
+                                  bit 4 keep sizes (sx/sy not rewritten for
+                                  this step: the server keeps the sizes of
+                                  its last step with at least nc cells)
 A version-1 server ignores bytes 48..64; a version-1 client never writes the
 magic, so the server falls back to the version-1 layout.
 """
@@ -55,6 +58,7 @@ OUT_DENSITY = 0x1
 OUT_POTENTIAL = 0x2
 OUT_GRADS = 0x4
 OUT_NO_FIELDS = 0x8
+IN_KEEP_SIZES = 0x10
 
 # state nc h2d scatter gather d2h_den upload compute download fw total gm
 HDR_TIMING_FMT = "<IifffffffffI"

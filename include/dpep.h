@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define DPEP_ABI_VERSION 4
+#define DPEP_ABI_VERSION 5
 
 /* status codes */
 #define DPEP_OK 0
@@ -132,7 +132,12 @@ int dpep_set_fixed_cells(dpep_ctx* ctx, const void* px, const void* py,
                          double target_density);
 
 /* Uploads nc <= nc_max cells (host memory) into the context's device
- * buffers.  Replaces the server's H2D (:1335-1349). */
+ * buffers.  Replaces the server's H2D (:1335-1349).  sx and sy both NULL
+ * (new in ABI 5): only the positions are uploaded and the cells keep the
+ * sizes resident from the last call that passed them, which must have
+ * covered at least nc cells (DPEP_ERR_STATE otherwise).  DREAMPlace's cell
+ * sizes do not change between iterations, so a caller that knows this
+ * halves the per-step upload. */
 int dpep_set_cells(dpep_ctx* ctx, const void* px, const void* py,
                    const void* sx, const void* sy, int nc);
 
@@ -173,7 +178,8 @@ int dpep_host_alloc(size_t bytes, void** out);
 int dpep_host_free(void* p);
 
 /* set_cells + compute + get_outputs: one whole step on host buffers, the
- * server loop body (:1326-1815). */
+ * server loop body (:1326-1815).  sx and sy both NULL keep the resident
+ * sizes, as in dpep_set_cells. */
 int dpep_step(dpep_ctx* ctx, const void* px, const void* py, const void* sx,
               const void* sy, int nc, void* field_x, void* field_y,
               void* density, void* potential, void* grad_x, void* grad_y);
@@ -217,7 +223,8 @@ int dpep_get_timings(dpep_ctx* ctx, float* out);
 /* Per-kernel average durations in microseconds over the steps recorded
  * since profiling was enabled (at most `slots` of them), measured with HIP
  * events around each launch on the stream the kernels run on:
- * [0] strip count (with the strip table), [1] strip fill, [2] strip
+ * [0] strip count (with the strip table; a step that sorts in one pass
+ * launches none and adds 0), [1] strip fill, [2] strip
  * accumulate with the row DCT (and the reduction of split strips),
  * [3] column DCT + inverse, [4] row inverse, [5] gather of the partial
  * forces per strip record, [6] forces in cell order, [7] whole step.

@@ -4,7 +4,10 @@ Drives the DREAMPlace adapter (make_forward / make_backward) through the shm
 server on the 1.1M-cell, 2048 x 2048 workload (seed 0), with the last tenth of
 the cells as fillers and 64 fixed terminals between them in pos, float32 as
 DREAMPlace runs, and compares the backward's gradient and the stashed field
-maps with the float64 oracle.  Prints one JSON line of relative errors.
+maps with the float64 oracle.  A second iteration moves the cells: the
+adapter then sends the positions alone (the size tensors are unchanged) and
+its gradient is checked the same way.  Prints one JSON line of relative
+errors.
 
     python adapter_gpu_run.py IPC_DIR
 """
@@ -51,32 +54,42 @@ def main():
                                    ready_timeout=300, step_timeout=120)
     fwd = stc.make_forward(client, keep_field_maps=True).__func__
     bwd = stc.make_backward().__func__
+    steps = []
     try:
-        ctx = F.Ctx()
-        fwd(ctx, *args)
-        grad = bwd(ctx, torch.tensor([0.5], dtype=torch.float32))[0].numpy()
-        print("adapter timing", {k: round(v, 3) for k, v in client._timings[-1].items()
-                                 if isinstance(v, float)}, flush=True)
+        for it in range(2):
+            if it == 1:     # cells move; the size tensors stay as they were
+                args[0].add_(torch.from_numpy(
+                    rng.normal(0, 20, args[0].numel()).astype(np.float32)))
+            ctx = F.Ctx()
+            fwd(ctx, *args)
+            grad = bwd(ctx, torch.tensor([0.5], dtype=torch.float32))[0].numpy()
+            word = int(np.frombuffer(client._mm, np.uint32, 1, stc.S.OFF_OUTPUTS)[0])
+            steps.append((args[0].numpy().copy(), grad, ctx,
+                          bool(word & stc.S.IN_KEEP_SIZES)))
+            print(f"adapter iteration {it} timing",
+                  {k: round(v, 3) for k, v in client._timings[-1].items()
+                   if isinstance(v, float)}, flush=True)
     finally:
         client.stop()
 
     # the cells exactly as the adapter sent them (sizes = clamped + 2 offset
     # in float32)
-    pos = args[0].numpy()
-    half = pos.size // 2
     osx = (args[1] + 2.0 * args[3]).numpy()
     osy = (args[2] + 2.0 * args[4]).numpy()
-    cells = (pos[:half][sel], pos[half:][sel], osx[sel], osy[sel])
-    ref = pyoracle.step(*cells, w.M, w.N, *die, d0n=w.d0n.astype(np.float32))
-    term_idx = np.setdiff1d(np.arange(half), sel)
-    res = {
-        "grad_x": rel_l2(grad[:half][sel], -0.5 * ref["grad_x"]),
-        "grad_y": rel_l2(grad[half:][sel], -0.5 * ref["grad_y"]),
-        "field_x": rel_l2(ctx.field_map_x.numpy(), ref["field_x"]),
-        "field_y": rel_l2(ctx.field_map_y.numpy(), ref["field_y"]),
-        "terminals_zero": bool(np.all(grad[:half][term_idx] == 0) and
-                               np.all(grad[half:][term_idx] == 0)),
-    }
+    res = {}
+    for it, (pos, grad, ctx, kept) in enumerate(steps):
+        half = pos.size // 2
+        cells = (pos[:half][sel], pos[half:][sel], osx[sel], osy[sel])
+        ref = pyoracle.step(*cells, w.M, w.N, *die, d0n=w.d0n.astype(np.float32))
+        term_idx = np.setdiff1d(np.arange(half), sel)
+        sfx = "" if it == 0 else "_moved"
+        res["grad_x" + sfx] = rel_l2(grad[:half][sel], -0.5 * ref["grad_x"])
+        res["grad_y" + sfx] = rel_l2(grad[half:][sel], -0.5 * ref["grad_y"])
+        res["field_x" + sfx] = rel_l2(ctx.field_map_x.numpy(), ref["field_x"])
+        res["field_y" + sfx] = rel_l2(ctx.field_map_y.numpy(), ref["field_y"])
+        res["terminals_zero" + sfx] = bool(np.all(grad[:half][term_idx] == 0) and
+                                           np.all(grad[half:][term_idx] == 0))
+        res["sizes_kept" + sfx] = kept
     print(json.dumps(res), flush=True)
     return 0
 

@@ -7,7 +7,8 @@ Speaks the server side of the protocol in dpep/shm.py: writes ready.flag
 (tmp + rename), polls the state word, answers GO with the float64 oracle's
 step cast to float32 (fields always; density, potential and per-cell forces
 when the file is version 2, as its outputs word asks, fields omitted when
-it says so), QUIT ends it.  CPU_DCT=1 as the real server: the cells' density
+it says so; with the keep-sizes bit, the sizes of its own last step with
+at least nc cells instead of the size slots), QUIT ends it.  CPU_DCT=1 as the real server: the cells' density
 without the initial density in the field_x slot, field_y zero.  LOOPBACK_MODE selects a failure
 for the client's error paths: "exit" (exit 3 before ready), "noready" (never
 write ready.flag), "hang" (never answer GO; QUIT still ends it).  The
@@ -70,6 +71,7 @@ def main():
         os.rename(flag + ".tmp", flag)
 
     steps = 0
+    sizes = None            # the sizes of the last step that sent them
     while True:
         st = struct.unpack_from("<I", mm, S.OFF_STATE)[0]
         if st == S.STATE_QUIT:
@@ -79,11 +81,18 @@ def main():
             continue
         t0 = time.perf_counter()
         nc = min(max(struct.unpack_from("<i", mm, S.OFF_NC)[0], 0), nc_max)
-        cells = [vec(n)[:nc].astype(np.float64) for n in ("px", "py", "sx", "sy")]
+        outs = struct.unpack_from("<I", mm, S.OFF_OUTPUTS)[0] if lay.version >= 2 else 0
+        if outs & S.IN_KEEP_SIZES:
+            if sizes is None or sizes[0].size < nc:
+                print("loopback: sizes kept but none held for these cells", file=sys.stderr)
+                return 1
+        else:
+            sizes = [vec(n)[:nc].astype(np.float64) for n in ("sx", "sy")]
+        cells = [vec(n)[:nc].astype(np.float64) for n in ("px", "py")] + [
+            sz[:nc] for sz in sizes]
         d0n = grid("init_density").astype(np.float64)
         r = pyoracle.step(*cells, M, N, xl, yl, xh, yh, d0n=d0n,
                           gather_forces=lay.version >= 2)
-        outs = struct.unpack_from("<I", mm, S.OFF_OUTPUTS)[0] if lay.version >= 2 else 0
         if cpu_dct:
             grid("field_x")[...] = pyoracle.density(*cells, M, N, xl, yl, xh, yh)
             grid("field_y")[...] = 0.0

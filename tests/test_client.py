@@ -102,6 +102,45 @@ def test_fewer_cells_than_capacity(tmp_path, oracle):
         c.stop()
 
 
+def test_positions_only_steps_keep_the_sizes(tmp_path, oracle):
+    """call(px, py) without sizes sets the keep-sizes bit and leaves the size
+    slots alone; the server steps on the sizes it last received (here the
+    slots are overwritten with garbage to prove they are not re-read).
+    Sizes missing, half given or covering too few cells are refused."""
+    w = _w(6, 500, 16)
+    c = _client(tmp_path, w, nc_max=600)
+    c.start()
+    try:
+        px, py, sx, sy = w.cells(np.float32)
+        with pytest.raises(ValueError, match="sizes kept"):
+            c.call(px, py)
+        with pytest.raises(ValueError, match="both or neither"):
+            c.call(px, py, sx, None)
+        c.call(px, py, sx, sy)
+        word = struct.unpack_from("<I", c._mm, S.OFF_OUTPUTS)[0]
+        assert not word & S.IN_KEEP_SIZES
+        c._views["sx"][:] = -7.0
+        c._views["sy"][:] = np.nan
+        for k in range(2):
+            qx, qy = px + np.float32(3 * k + 1), py - np.float32(k)
+            out = c.call_full(qx, qy)
+            word = struct.unpack_from("<I", c._mm, S.OFF_OUTPUTS)[0]
+            assert word & S.IN_KEEP_SIZES
+            assert np.all(c._views["sx"] == -7.0)          # never rewritten
+            ref = oracle.step(qx, qy, sx, sy, w.M, w.N, w.xl, w.yl, w.xh, w.yh)
+            assert rel_linf(out["density"], ref["density"]) < 1e-6
+            assert rel_l2(out["grad_x"], ref["grad_x"]) < 1e-6
+        # fewer cells keep their sizes too; more than were sent do not
+        out = c.call_full(px[:300], py[:300])
+        ref = oracle.step(px[:300], py[:300], sx[:300], sy[:300], w.M, w.N, w.xl, w.yl,
+                          w.xh, w.yh)
+        assert rel_l2(out["grad_y"], ref["grad_y"]) < 1e-6
+        with pytest.raises(ValueError, match="sizes kept"):
+            c.call(np.zeros(550, np.float32), np.zeros(550, np.float32))
+    finally:
+        c.stop()
+
+
 def test_stale_ready_flag_is_removed(tmp_path):
     w = _w(5, 100, 8)
     ipc = tmp_path / "ipc"
@@ -237,6 +276,43 @@ def test_dreamplace_adapter_fetches_only_the_forces(tmp_path, oracle):
         assert not client._views["field_x"].any()      # never written
         with pytest.raises(RuntimeError, match="needs the fields"):
             client.call(*(np.zeros(4, np.float32),) * 4)
+    finally:
+        client.stop()
+
+
+def test_dreamplace_adapter_sends_the_sizes_once(tmp_path, oracle):
+    """DREAMPlace hands every iteration the same size tensors: after the
+    first call only the positions go to the server (keep-sizes bit set),
+    until a size tensor is modified in place, which sends them again."""
+    torch = pytest.importorskip("torch")
+    from dpep import scatter_ttnn_client as stc
+    import dreamplace_fakes as F
+
+    rng = np.random.default_rng(14)
+    mov, term, fil = _adapter_case(rng)
+    M = N = 16
+    die = (0.0, 0.0, 160.0, 160.0)
+    args, sel = F.forward_args(mov, term, fil, M, N, die, np.zeros((M, N)))
+    client = _client(tmp_path, _w(0, len(sel), M), nc_max=len(sel))
+    fwd = stc.make_forward(client).__func__
+    bwd = stc.make_backward().__func__
+    try:
+        n = args[0].numel() // 2
+        for it in range(4):
+            if it == 3:
+                args[1].mul_(1.5)                   # sizes change in place
+            if it > 0:
+                args[0].add_(torch.from_numpy(rng.uniform(-2, 2, 2 * n)))
+            ctx = F.Ctx()
+            fwd(ctx, *args)
+            word = struct.unpack_from("<I", client._mm, S.OFF_OUTPUTS)[0]
+            assert bool(word & S.IN_KEEP_SIZES) == (it in (1, 2))
+            pos = args[0].numpy()
+            sx, sy = (args[1] + 2 * args[3]).numpy(), (args[2] + 2 * args[4]).numpy()
+            ref = oracle.step(pos[:n][sel], pos[n:][sel], sx[sel], sy[sel], M, N, *die)
+            g = bwd(ctx, torch.tensor([1.0], dtype=torch.float64))[0].numpy()
+            assert rel_l2(g[:n][sel], -ref["grad_x"]) < 1e-5
+            assert rel_l2(g[n:][sel], -ref["grad_y"]) < 1e-5
     finally:
         client.stop()
 

@@ -363,6 +363,40 @@ def test_outputs_are_stale_after_new_cells():
 
 
 @pytest.mark.parametrize("pinned", [False, True])
+def test_positions_only_upload_keeps_the_sizes(pinned):
+    """set_cells(px, py) (NULL sizes in dpep_set_cells) moves the cells and
+    keeps the resident sizes: the step is bitwise the one of a full upload of
+    the same cells, for fewer cells as well; sizes never sent, or sent for
+    fewer cells, are refused (DPEP_ERR_STATE) and leave the context usable."""
+    import dpep
+    from dpep import workloads
+    w = workloads.small(3, seed=13, cells=20000, grid=256)
+    px, py, sx, sy = w.cells(np.float32)
+    rng = np.random.default_rng(3)
+    kw = dict(pinned=pinned)
+    with dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh, **kw) as ctx, \
+            dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh, **kw) as full:
+        for c in (ctx, full):
+            c.set_initial_density(w.d0n.astype(np.float32))
+        with pytest.raises(RuntimeError, match="resident sizes"):
+            ctx.set_cells(px, py)
+        ctx.set_cells(px, py, sx, sy)
+        for n in (w.nc, w.nc, 5000):
+            qx = (px[:n] + rng.normal(0, 3, n)).astype(np.float32)
+            qy = (py[:n] + rng.normal(0, 3, n)).astype(np.float32)
+            a = ctx.step(qx, qy)
+            b = full.step(qx, qy, sx[:n], sy[:n])
+            for k in b:
+                assert np.array_equal(a[k], b[k], equal_nan=True), f"{k} n={n}"
+        ctx.set_cells(px[:100], py[:100], sx[:100], sy[:100])
+        with pytest.raises(RuntimeError, match="resident sizes"):
+            ctx.set_cells(px[:101], py[:101])
+        a = ctx.step(px[:100], py[:100])
+        b = full.step(px[:100], py[:100], sx[:100], sy[:100])
+        assert all(np.array_equal(a[k], b[k]) for k in b)
+
+
+@pytest.mark.parametrize("pinned", [False, True])
 def test_pinned_context_and_scatter_density(oracle, pinned):
     """A pinned context (page-locked staging) gives the same outputs, and
     the scatter density (DPEP_FLAG_SCATTER_DENSITY) is the cells' density

@@ -50,6 +50,22 @@ def test_client_against_oracle(tmp_path, oracle, inprocess):
             ref = oracle.step(pxk, py, sx, sy, w.M, w.N, w.xl, w.yl, w.xh, w.yh,
                               d0n=w.d0n.astype(np.float32))
             _check(out, ref)
+        # positions alone: the sizes stay those of the last call that sent
+        # them (the shm or staging size slots are scribbled over to show they
+        # are not re-read)
+        if inprocess:
+            staged = c._ctx.host_cells()
+            staged["sx"][:] = -7.0
+            staged["sy"][:] = np.nan
+        else:
+            c._views["sx"][:] = -7.0
+            c._views["sy"][:] = np.nan
+        for k in range(2):
+            pxk = (px + rng.normal(0, 2, px.size)).astype(np.float32)
+            out = c.call_full(pxk, py)
+            ref = oracle.step(pxk, py, sx, sy, w.M, w.N, w.xl, w.yl, w.xh, w.yh,
+                              d0n=w.d0n.astype(np.float32))
+            _check(out, ref)
         # fewer cells than before: the tail of the previous step is gone
         n2 = w.nc // 3
         out = c.call_full(px[:n2], py[:n2], sx[:n2], sy[:n2])
@@ -57,7 +73,7 @@ def test_client_against_oracle(tmp_path, oracle, inprocess):
                           w.xh, w.yh, d0n=w.d0n.astype(np.float32))
         _check(out, ref)
         t = c.timing_summary(n_warmup=1)
-        assert t["gather_mode"] == "hip" and t["n_iters"] == 4
+        assert t["gather_mode"] == "hip" and t["n_iters"] == 6
     finally:
         c.stop()
 
@@ -152,6 +168,8 @@ def test_dreamplace_adapter_forces_on_gpu(tmp_path):
     print(r.stdout[-3000:], r.stderr[-3000:], flush=True)
     assert r.returncode == 0
     res = json.loads(r.stdout.strip().splitlines()[-1])
-    assert res["grad_x"] <= 1e-4 and res["grad_y"] <= 1e-4
-    assert res["field_x"] <= 1e-4 and res["field_y"] <= 1e-4
-    assert res["terminals_zero"]
+    for sfx in ("", "_moved"):           # sizes sent, then positions alone
+        assert res["grad_x" + sfx] <= 1e-4 and res["grad_y" + sfx] <= 1e-4
+        assert res["field_x" + sfx] <= 1e-4 and res["field_y" + sfx] <= 1e-4
+        assert res["terminals_zero" + sfx]
+    assert not res["sizes_kept"] and res["sizes_kept_moved"]
