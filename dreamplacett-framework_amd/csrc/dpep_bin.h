@@ -180,6 +180,45 @@ __device__ __forceinline__ void load_cells(const T* __restrict__ px, const T* __
     }
 }
 
+// The cells [c0, cend) of counting workgroup blockIdx.x (K1, the fresh K3:
+// part blockIdx.x % b.sub of one-pass block blockIdx.x / b.sub, see
+// set_count_blocks) and its count slot, the one-pass block's.
+__device__ __forceinline__ int count_cells(const BinArgs& b, int nc, int& c0, int& cend)
+{
+    const int ob = (int)blockIdx.x / b.sub, part = (int)blockIdx.x - ob * b.sub;
+    const int base = ob * b.qcells;
+    c0 = base + part * b.qsub;
+    cend = min(min(c0 + b.qsub, base + b.qcells), nc);
+    if (cend < c0) cend = c0;
+    return ob & (kCountSlots - 1);
+}
+
+// The CPT cells of thread tid in the one-pass block [c0, cend) (cend > c0
+// unless the block is empty; slots past cend hold copies of cell cend - 1,
+// which the caller skips).  Every load is unconditional (clamped index), so
+// no per-cell branch holds the loads back.
+template <typename T, int NT, int CPT>
+__device__ __forceinline__ void load_block_cells(const T* __restrict__ px,
+                                                 const T* __restrict__ py,
+                                                 const T* __restrict__ sx,
+                                                 const T* __restrict__ sy, int c0, int cend,
+                                                 int tid, T* cx, T* cy, T* cw, T* ch)
+{
+    if (cend > c0) {
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int i = min(c0 + tid + j * NT, cend - 1);
+            cx[j] = px[i];
+            cy[j] = py[i];
+            cw[j] = sx[i];
+            ch[j] = sy[i];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) cx[j] = cy[j] = cw[j] = ch[j] = (T)0;
+    }
+}
+
 __device__ __forceinline__ unsigned long long to_fixed(double v, double scale)
 {
     return (unsigned long long)__double2ull_rn(v * scale);
@@ -341,7 +380,8 @@ __device__ __forceinline__ void fresh_offsets(const BinArgs& b, unsigned* cur,
 {
     const int tid = threadIdx.x;
     const int S = b.S;
-    const int x = count_slot((int)blockIdx.x * kCellsPerGroup, b.qcells);
+    int c0, cend;
+    const int x = count_cells(b, 0, c0, cend);
     const unsigned* row = b.cnt + (size_t)blockIdx.x * S;
     const unsigned* xt = counts_of(b, b.par);
     for (int s = tid; s < S; s += kBinThreads) {
@@ -401,7 +441,7 @@ __device__ __forceinline__ void once_offsets(const BinArgs& b, unsigned* start,
 {
     const int tid = threadIdx.x;
     const int S = b.S;
-    const int x = count_slot((int)blockIdx.x * b.qcells, b.qcells);
+    const int x = (int)blockIdx.x & (kCountSlots - 1);     // block b: slot b % 8
     const unsigned* prev = counts_of(b, b.par ^ 1);
     const int per = (S + NT - 1) / NT;
     const int r0 = min(tid * per, S), r1 = min(r0 + per, S);
@@ -514,10 +554,11 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_count(
     const int tid = threadIdx.x;
     for (int s = tid; s < b.S; s += kBinThreads) hist[s] = 0u;
     __syncthreads();
-    const int c0 = blockIdx.x * kCellsPerGroup;
+    int c0, cend;
+    const int x = count_cells(b, nc, c0, cend);
     // all loads of this thread's cells first (independent, in flight together)
     T cx[kCellsPerThread], cy[kCellsPerThread], cw[kCellsPerThread], ch[kCellsPerThread];
-    load_cells(px, py, sx, sy, nc, c0, tid, cx, cy, cw, ch);
+    load_cells(px, py, sx, sy, cend, c0, tid, cx, cy, cw, ch);
 #pragma unroll
     for (int j = 0; j < kCellsPerThread; ++j) {
         CellSpan c;
@@ -535,8 +576,7 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_count(
     // atomics over kCountSlots addresses per strip; the returned old total is
     // the block's base within its slot
     unsigned* row = b.cnt + (size_t)blockIdx.x * b.S;
-    unsigned* slot =
-        counts_of(b, b.par) + (size_t)count_slot((int)blockIdx.x * kCellsPerGroup, b.qcells) * b.S;
+    unsigned* slot = counts_of(b, b.par) + (size_t)x * b.S;
     for (int s = tid; s < b.S; s += kBinThreads) {
         const unsigned h = hist[s];
         row[s] = h ? atomicAdd(&slot[s], h) : 0u;
@@ -561,16 +601,17 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill_direct(
     unsigned* cur = reinterpret_cast<unsigned*>(smem);
     const int tid = threadIdx.x;
     // the cells' loads are issued first: their latency overlaps the offsets
-    const int c0 = blockIdx.x * kCellsPerGroup;
+    int c0, cend;
+    count_cells(b, nc, c0, cend);
     T cx[kCellsPerThread], cy[kCellsPerThread], cw[kCellsPerThread], chh[kCellsPerThread];
-    load_cells(px, py, sx, sy, nc, c0, tid, cx, cy, cw, chh);
+    load_cells(px, py, sx, sy, cend, c0, tid, cx, cy, cw, chh);
     fresh_offsets(b, cur, cur + b.S, cur + 2 * b.S);
     __syncthreads();
     vec4_t<T>* recg = reinterpret_cast<vec4_t<T>*>(b.recg);
     unsigned long long* Bm = reinterpret_cast<unsigned long long*>(b.B);
     for (int j = 0; j < kCellsPerThread; ++j) {
         const int i = c0 + tid + j * kBinThreads;
-        if (i >= nc) break;
+        if (i >= cend) break;
         CellSpan c;
         if (!cell_span((double)cx[j], (double)cy[j], (double)cw[j], (double)chh[j], g, c)) {
             b.pos[i] = pos_pair(kPosNone, kPosNone);
@@ -669,9 +710,10 @@ __global__ __launch_bounds__(kBinThreads, 5) void k_bin_fill_staged(
     unsigned* sm = reinterpret_cast<unsigned*>(sg + kStage);
     const int tid = threadIdx.x;
     // the cells' loads are issued first: their latency overlaps the offsets
-    const int c0 = blockIdx.x * kCellsPerGroup;
+    int c0, cend;
+    count_cells(b, nc, c0, cend);
     T cx[kCellsPerThread], cy[kCellsPerThread], cw[kCellsPerThread], chh[kCellsPerThread];
-    load_cells(px, py, sx, sy, nc, c0, tid, cx, cy, cw, chh);
+    load_cells(px, py, sx, sy, cend, c0, tid, cx, cy, cw, chh);
     fresh_offsets(b, cur, cnt, tmp);
     __syncthreads();
     for (int s = tid; s < S; s += kBinThreads) cnt[s] = 0u;
@@ -687,7 +729,7 @@ __global__ __launch_bounds__(kBinThreads, 5) void k_bin_fill_staged(
     for (int j = 0; j < kCellsPerThread; ++j) {
         s0v[j] = s1v[j] = -1;
         const int i = c0 + tid + j * kBinThreads;
-        if (i >= nc) continue;
+        if (i >= cend) continue;
         CellSpan c;
         if (!cell_span((double)cx[j], (double)cy[j], (double)cw[j], (double)chh[j], g, c)) {
             b.pos[i] = pos_pair(kPosNone, kPosNone);
@@ -827,6 +869,44 @@ __device__ __forceinline__ void record_density(const vec4_t<T>& rg, unsigned rm,
     }
 }
 
+// Threads per team that handles one tall cell (K3's side-map adds, G2's
+// gather).
+constexpr int kTallTeam = 16;
+
+// A tall cell's density added into the side map B by a team of kTallTeam
+// threads (lane: index in the team; every lane calls it for the same cell,
+// its px, py, sx, sy): its bins strided over the team, each the value
+// a single thread's row-by-row loop adds, (ratio / bin area * tx) * ty in
+// fixed point, so the sums are bitwise the same in any order; the lanes
+// also mark the cell's column blocks in each of its strips.  One thread per
+// tall cell held its workgroup ~10 us for a cell of ~50 bins (float64).
+template <typename T>
+__device__ __forceinline__ void scatter_tall_team(const vec4_t<T>& cell, int lane,
+                                                  const Grid& g, const BinArgs& b,
+                                                  unsigned long long* __restrict__ Bm)
+{
+    CellSpan c;
+    if (!cell_span((double)cell.x, (double)cell.y, (double)cell.z, (double)cell.w, g, c))
+        return;
+    int s0, s1;
+    bool tall;
+    cell_strips(c, b.R, b.lgR, s0, s1, tall);
+    const double sc = c.ratio() * g.inv_ba;
+    const int ny1 = c.byh - c.byl + 1;
+    const int nb = (c.bxh - c.bxl + 1) * ny1;
+    for (int e = lane; e < nb; e += kTallTeam) {
+        const int k = c.bxl + e / ny1, q = c.byl + e % ny1;
+        const double tx = overlap_1d(c.x, c.w, g.xl, g.bsx, k);
+        const double ty = overlap_1d(c.y, c.h, g.yl, g.bsy, q);
+        if (tx <= 0.0 || ty <= 0.0) continue;
+        const double stx = sc * tx;
+        atomicAdd(&Bm[(size_t)k * g.N + q], to_fixed(stx * ty, g.fix_scale));
+    }
+    const int CB = side_block(g.N);
+    for (int s = s0 + lane; s <= s1; s += kTallTeam)
+        side_mark(b.bigflag + (size_t)s * kSideWords, c.byl, c.byh, CB);
+}
+
 // ---------------------------------------------------------------------------
 // K3, single pass (no K1): the regions are sized from the previous step's
 // counts (once_offsets).  Workgroup g ranks its records per strip in LDS,
@@ -838,22 +918,42 @@ __device__ __forceinline__ void record_density(const vec4_t<T>& rg, unsigned rm,
 // K4 would add) with the strip's column blocks marked, their gather by G1's
 // pool pass.  Every record is computed as in the fresh fill, so the results
 // do not depend on which records overflow.
+// Tall cells are listed as they are found (their index; the coordinates of
+// the first kTallList too) and added into B by teams of threads at the end
+// (scatter_tall_team), where no per-cell registers are live.
 // LDS: start[S] | room[S] | cnt[S] (the expected strip totals while the plan
-// is made) | tmp[kBinThreads + kChunkCands] | pool count, pool base.
+// is made) | tmp[kOnceThreads + kChunkCands] | pool count, pool base | tall
+// count | tall cells[kOnceThreads * kOnceMaxCpt] | (16-byte aligned) the
+// first kTallList tall cells' px, py, sx, sy.
 // ---------------------------------------------------------------------------
-__host__ __device__ constexpr size_t fill_once_lds(int S)
+constexpr int kTallList = 256;
+
+__host__ __device__ constexpr size_t fill_once_words(int S)
 {
-    return (size_t)(3 * S + kOnceThreads + kChunkCands + 2) * sizeof(unsigned);
+    return ((size_t)(3 * S + kOnceThreads + kChunkCands + 3 + kOnceThreads * kOnceMaxCpt) +
+            3) / 4 * 4;
 }
 
-// NT = kOnceThreads threads, CPT cells each: blocks of QC = NT * CPT cells
-// (b.qcells: counting_block, twice K1's unless that leaves CUs idle), so
-// fewer reservation atomics land on each counter and a block's runs in a
-// strip are longer.  float32: six waves per
-// SIMD, three workgroups per CU, so 1.1 M cells fit the GPU in one round
-// (float64 keeps its registers: it would spill).
+template <typename T>
+__host__ __device__ constexpr size_t fill_once_lds(int S)
+{
+    return fill_once_words(S) * sizeof(unsigned) + (size_t)kTallList * sizeof(vec4_t<T>);
+}
+
+// NT = kOnceThreads threads, up to CPT cells each: one block of b.qcells
+// cells (once_blocks: equal blocks, two per CU when they fit, at least
+// 1024 cells so a block's runs in a strip stay long and few reservation
+// atomics land on each counter).  Six waves per SIMD where the registers
+// allow it (float32 up to 4 cells per thread: three workgroups per CU when
+// the blocks run in rounds), else four (two workgroups per CU).
 template <typename T, int CPT>
-__global__ __launch_bounds__(kOnceThreads, sizeof(T) == 4 ? 6 : 4) void k_bin_fill_once(
+__host__ __device__ constexpr int once_waves()
+{
+    return sizeof(T) == 4 && CPT <= 4 ? 6 : 4;
+}
+
+template <typename T, int CPT>
+__global__ __launch_bounds__(kOnceThreads, (once_waves<T, CPT>())) void k_bin_fill_once(
     const T* __restrict__ px, const T* __restrict__ py,
     const T* __restrict__ sx, const T* __restrict__ sy, int nc, Grid g,
     BinArgs b)
@@ -865,17 +965,26 @@ __global__ __launch_bounds__(kOnceThreads, sizeof(T) == 4 ? 6 : 4) void k_bin_fi
     unsigned* cnt = room + S;                   // this block's records per strip
     unsigned* tmp = cnt + S;
     unsigned* npool = tmp + kOnceThreads + kChunkCands;  // [0] overflow, [1] pool base
+    unsigned* ntall = npool + 2;
+    unsigned* tall_idx = ntall + 1;             // [kOnceThreads * kOnceMaxCpt]
+    vec4_t<T>* tall_cell =                      // [kTallList]
+        reinterpret_cast<vec4_t<T>*>(smem + fill_once_words(S) * sizeof(unsigned));
+    static_assert(CPT <= kOnceMaxCpt, "tall_idx holds kOnceMaxCpt cells per thread");
     const int tid = threadIdx.x;
-    constexpr int NT = kOnceThreads, QC = NT * CPT;
-    const int c0 = (int)blockIdx.x * QC;
-    unsigned* xrow = counts_of(b, b.par) + (size_t)count_slot(c0, QC) * S;
+    constexpr int NT = kOnceThreads;
+    const int c0 = (int)blockIdx.x * b.qcells;
+    const int cend = min(c0 + b.qcells, nc);
+    unsigned* xrow = counts_of(b, b.par) + (size_t)(blockIdx.x & (kCountSlots - 1)) * S;
     // the cells' loads are issued first: their latency overlaps the plan
     T cx[CPT], cy[CPT], cw[CPT], chh[CPT];
-    load_cells<T, NT, CPT>(px, py, sx, sy, nc, c0, tid, cx, cy, cw, chh);
+    load_block_cells<T, NT, CPT>(px, py, sx, sy, c0, cend, tid, cx, cy, cw, chh);
     once_offsets<NT>(b, start, room, cnt, tmp);
     __syncthreads();
     for (int s = tid; s < S; s += NT) cnt[s] = 0u;
-    if (tid == 0) npool[0] = 0u;
+    if (tid == 0) {
+        npool[0] = 0u;
+        *ntall = 0u;
+    }
     __syncthreads();
     vec4_t<T>* recg = reinterpret_cast<vec4_t<T>*>(b.recg);
     unsigned long long* Bm = reinterpret_cast<unsigned long long*>(b.B);
@@ -888,7 +997,7 @@ __global__ __launch_bounds__(kOnceThreads, sizeof(T) == 4 ? 6 : 4) void k_bin_fi
         s0v[j] = s1v[j] = -1;
         p0[j] = p1[j] = kPosNone;
         const int i = c0 + tid + j * NT;
-        if (i >= nc) continue;
+        if (i >= cend) continue;
         CellSpan c;
         if (!cell_span((double)cx[j], (double)cy[j], (double)cw[j], (double)chh[j], g, c))
             continue;
@@ -896,21 +1005,9 @@ __global__ __launch_bounds__(kOnceThreads, sizeof(T) == 4 ? 6 : 4) void k_bin_fi
         bool tall;
         cell_strips(c, b.R, b.lgR, s0, s1, tall);
         if (tall) {
-            const double sc = c.ratio() * g.inv_ba;
-            for (int k = c.bxl; k <= c.bxh; ++k) {
-                const double tx = overlap_1d(c.x, c.w, g.xl, g.bsx, k);
-                if (tx <= 0.0) continue;
-                const double stx = sc * tx;
-                const size_t rowi = (size_t)k * g.N;
-                for (int q = c.byl; q <= c.byh; ++q) {
-                    const double ty = overlap_1d(c.y, c.h, g.yl, g.bsy, q);
-                    if (ty <= 0.0) continue;
-                    atomicAdd(&Bm[rowi + q], to_fixed(stx * ty, g.fix_scale));
-                }
-            }
-            const int CB = side_block(g.N);
-            for (int s = s0; s <= s1; ++s)
-                side_mark(b.bigflag + (size_t)s * kSideWords, c.byl, c.byh, CB);
+            const unsigned t = atomicAdd(ntall, 1u);
+            tall_idx[t] = (unsigned)i;
+            if (t < (unsigned)kTallList) tall_cell[t] = vec4_t<T>{cx[j], cy[j], cw[j], chh[j]};
             p0[j] = kPosTall;
             continue;
         }
@@ -1003,7 +1100,19 @@ __global__ __launch_bounds__(kOnceThreads, sizeof(T) == 4 ? 6 : 4) void k_bin_fi
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
         const int i = c0 + tid + j * NT;
-        if (i < nc) b.pos[i] = pos_pair(p0[j], p1[j]);
+        if (i < cend) b.pos[i] = pos_pair(p0[j], p1[j]);
+    }
+    // the tall cells, by teams of threads, last: the per-cell arrays above
+    // are dead here (earlier, their registers spilled); coordinates past the
+    // first kTallList come from the cell arrays
+    const unsigned nt = *ntall;                 // uniform across the group
+    const int team = tid / kTallTeam, lane = tid % kTallTeam;
+    for (unsigned t = (unsigned)team; t < nt; t += NT / kTallTeam) {
+        const unsigned i = tall_idx[t];
+        const vec4_t<T> cell = t < (unsigned)kTallList
+                                   ? tall_cell[t]
+                                   : vec4_t<T>{px[i], py[i], sx[i], sy[i]};
+        scatter_tall_team<T>(cell, lane, g, b, Bm);
     }
 }
 
@@ -1588,7 +1697,6 @@ __device__ __forceinline__ void gather_tall(int i, const T* __restrict__ px,
 // same cell): the bins strided over the team, float64 partial sums reduced
 // by shuffles within the team in a fixed order.  Returns false (nothing
 // written) for a larger cell, which the whole workgroup then gathers.
-constexpr int kTallTeam = 16;
 constexpr long long kTallTeamBins = 256;
 
 template <typename T>
@@ -1633,9 +1741,9 @@ __device__ __forceinline__ bool gather_tall_team(int i, int lane, const T* __res
     return true;
 }
 
-// One workgroup of NT threads per one-pass K3 block of NT * CPT cells (the
-// same cell-to-thread map): the records of a block sit in one short run per
-// strip, so each run's partials are read whole, by one CU.
+// One workgroup of NT threads per one-pass K3 block of b.qcells <= NT * CPT
+// cells (the same cell-to-thread map): the records of a block sit in one
+// short run per strip, so each run's partials are read whole, by one CU.
 // Tall cells: a team of kTallTeam threads per cell of at most kTallTeamBins
 // bins, larger ones one at a time by the whole workgroup.
 template <typename T, int NT, int CPT>
@@ -1655,13 +1763,15 @@ __global__ __launch_bounds__(NT) void k_gather_out(
     if (threadIdx.x == 0) *ntall = 0u;
     if (threadIdx.x < QC / 32) large[threadIdx.x] = 0u;
     __syncthreads();
-    const int c0 = blockIdx.x * QC + threadIdx.x;
+    const int cb = (int)blockIdx.x * b.qcells;
+    const int cend = min(cb + b.qcells, nc);
+    const int c0 = cb + threadIdx.x;
     const vec2_t<T>* res = reinterpret_cast<const vec2_t<T>*>(b.gtmp);
     unsigned p[CPT], p2[CPT];
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
         const int i = c0 + j * NT;
-        const unsigned long long pp = i < nc ? b.pos[i] : pos_pair(kPosNone, kPosNone);
+        const unsigned long long pp = i < cend ? b.pos[i] : pos_pair(kPosNone, kPosNone);
         p[j] = (unsigned)pp;
         p2[j] = (unsigned)(pp >> 32);
     }
@@ -1674,7 +1784,7 @@ __global__ __launch_bounds__(NT) void k_gather_out(
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
         const int i = c0 + j * NT;
-        if (i >= nc) break;
+        if (i >= cend) break;
         if (p[j] == kPosTall) {
             list[atomicAdd(ntall, 1u)] = (unsigned)i;
             continue;

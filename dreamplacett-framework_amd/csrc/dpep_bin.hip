@@ -8,12 +8,6 @@
 
 namespace dpep {
 
-static unsigned g1_of(int nc)
-{
-    const int g = (nc + kCellsPerGroup - 1) / kCellsPerGroup;
-    return (unsigned)(g > 0 ? g : 1);
-}
-
 // k_strip_acc is instantiated per row length N (its row DCT is templated).
 template <typename T, typename Fn>
 static hipError_t dispatch_n(int N, Fn&& fn)
@@ -42,20 +36,20 @@ hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
                               BinArgs b, const SpectralArgs& a, const T* d0n, T* dens,
                               T* Tt, bool once, hipStream_t s, hipEvent_t* ev)
 {
-    b.G1 = (int)g1_of(nc);
-    b.qcells = counting_block(nc, b.cus);
+    const OnceBlocks ob = once_blocks(nc, b.cus, sizeof(T));
+    set_count_blocks(b, ob);
     if (b.R != strip_rows(g.N)) return hipErrorInvalidValue;   // the kernel's R
     if (once && b.pool_cap < 2u * (unsigned)(nc > 0 ? nc : 0)) return hipErrorInvalidValue;
     hipError_t e;
     if (once) {
         if (ev && (e = hipEventRecord(ev[0], s))) return e;
-        const unsigned grid = (unsigned)(nc > b.qcells ? (nc + b.qcells - 1) / b.qcells : 1);
-        if (b.qcells == kOnceCells)
-            k_bin_fill_once<T, kCellsPerThread><<<grid, kOnceThreads, fill_once_lds(b.S), s>>>(
-                px, py, sx, sy, nc, g, b);
-        else
-            k_bin_fill_once<T, kCellsPerThread / 2><<<grid, kOnceThreads, fill_once_lds(b.S), s>>>(
-                px, py, sx, sy, nc, g, b);
+        if ((e = with_cpt(ob.cpt, [&](auto c) -> hipError_t {
+                 constexpr int CPT = decltype(c)::value;
+                 k_bin_fill_once<T, CPT><<<(unsigned)ob.grid, kOnceThreads,
+                                           fill_once_lds<T>(b.S), s>>>(px, py, sx, sy, nc, g, b);
+                 return hipSuccess;
+             })))
+            return e;
     } else {
         const size_t count_lds = (size_t)b.S * sizeof(unsigned);
         const bool staged = b.S >= kStageMinStrips;
@@ -95,17 +89,18 @@ hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
     hipError_t e = hipGetLastError();
     if (e) return e;
     if (ev && (e = hipEventRecord(ev, s))) return e;
-    // blocks of the one-pass K3's cells
-    const int qc = counting_block(nc, b.cus);
-    const unsigned grid = (unsigned)((nc + qc - 1) / qc);
-    if (qc == kOnceCells)
-        k_gather_out<T, kOnceThreads, kCellsPerThread>
-            <<<grid, kOnceThreads, gather_out_lds<kOnceThreads, kCellsPerThread>(), s>>>(
-                px, py, sx, sy, nc, g, b, fx, fy, gx, gy);
-    else
-        k_gather_out<T, kOnceThreads, kCellsPerThread / 2>
-            <<<grid, kOnceThreads, gather_out_lds<kOnceThreads, kCellsPerThread / 2>(), s>>>(
-                px, py, sx, sy, nc, g, b, fx, fy, gx, gy);
+    // the one-pass K3's cell blocks
+    const OnceBlocks ob = once_blocks(nc, b.cus, sizeof(T));
+    BinArgs bo = b;
+    bo.qcells = ob.q;
+    if ((e = with_cpt(ob.cpt, [&](auto c) -> hipError_t {
+             constexpr int CPT = decltype(c)::value;
+             k_gather_out<T, kOnceThreads, CPT>
+                 <<<(unsigned)ob.grid, kOnceThreads, gather_out_lds<kOnceThreads, CPT>(), s>>>(
+                     px, py, sx, sy, nc, g, bo, fx, fy, gx, gy);
+             return hipSuccess;
+         })))
+        return e;
     return hipGetLastError();
 }
 
@@ -164,14 +159,14 @@ static hipError_t prepare_bin_type()
                                  (int)fill_lds_staged<T>(sizeof(T) == 4 ? 4096 : 1024))))
         return e;
     // the one-pass K3's strip tables: at most 8192 * 8192 bins in 2-row strips
-    if ((e = hipFuncSetAttribute((const void*)k_bin_fill_once<T, kCellsPerThread>,
-                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 (int)fill_once_lds(4096))))
-        return e;
-    if ((e = hipFuncSetAttribute((const void*)k_bin_fill_once<T, kCellsPerThread / 2>,
-                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 (int)fill_once_lds(4096))))
-        return e;
+    for (int cpt = 2; cpt <= kOnceMaxCpt && !e; ++cpt)
+        e = with_cpt(cpt, [&](auto c) -> hipError_t {
+            constexpr int CPT = decltype(c)::value;
+            return hipFuncSetAttribute((const void*)k_bin_fill_once<T, CPT>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)fill_once_lds<T>(4096));
+        });
+    if (e) return e;
     return hipFuncSetAttribute((const void*)k_gather_bin<T>,
                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)kTileBytes);

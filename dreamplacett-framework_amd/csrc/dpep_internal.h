@@ -6,6 +6,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "dpep_device.h"
 
 namespace dpep {
@@ -70,14 +72,6 @@ constexpr int kOnceThreads = 512;      // one-pass K3 workgroup size
 constexpr int kOnceCells = kOnceThreads * kCellsPerThread;   // its largest block
 constexpr int kAccThreads = 1024;      // K4 workgroup size
 constexpr int kCountSlots = 8;         // strip-total counters per strip
-// The count slot of the cells of block [c0, c0 + ...): by blocks of `unit`
-// cells (the step's one-pass block, BinArgs::qcells) in every kernel that
-// counts, so a fresh step's counts size a one-pass step's regions slot by
-// slot.
-__host__ __device__ constexpr int count_slot(int c0, int unit)
-{
-    return (c0 >> __builtin_ctz((unsigned)unit)) & (kCountSlots - 1);   // unit: 2^k
-}
 constexpr int kMaxSpanY = 4095;        // larger y spans take the tall path
 constexpr int kSideBits = 128;         // column blocks tracked per strip in B
 constexpr int kSideWords = kSideBits / 32;
@@ -126,7 +120,10 @@ struct BinArgs {
     int par;                // parity of this step: its set of counts
     int cus;                // CUs of the device
     int qcells;             // cells per one-pass block, the unit of the count
-                            // slots (set per step: counting_block)
+                            // slots (set per step: once_blocks)
+    int sub, qsub;          // counting workgroups per one-pass block, and the
+                            // cells of each but the block's last
+                            // (set_count_blocks)
     unsigned reg_cap;       // records the regions of a plan may hold in total
     unsigned pool0;         // record number of the overflow pool's first entry
     unsigned pool_cap;      // capacity of the overflow pool (0: fresh-only)
@@ -193,6 +190,15 @@ inline size_t region_capacity(size_t cap, int S)
     return cap + cap / 8 + (size_t)kRegionSlack * kCountSlots * (size_t)S;
 }
 
+// Rows of BinArgs::cnt: an upper bound of the counting workgroups
+// (set_count_blocks) of any step of at most nc cells.  With q >= 1024 cells
+// per one-pass block and at most kOnceThreads * kOnceMaxCpt, blocks * parts
+// <= (nc / q + 1) * (q / 1024 + 1) <= 2 * nc / 1024 + 3.5.
+inline int count_grid_max(long long nc)
+{
+    return (int)(2 * ((nc + kCellsPerGroup - 1) / kCellsPerGroup) + 4);
+}
+
 inline BinPlan make_bin_plan(int M, int N, int nc_max, size_t elem_bytes)
 {
     BinPlan p{};
@@ -205,7 +211,7 @@ inline BinPlan make_bin_plan(int M, int N, int nc_max, size_t elem_bytes)
     while ((1 << p.lgR) < R) ++p.lgR;
     p.S = M / R;
     const long long nc = nc_max > 1 ? nc_max : 1;
-    p.G1max = (int)((nc + kCellsPerGroup - 1) / kCellsPerGroup);
+    p.G1max = count_grid_max(nc);
     p.cap = (size_t)(2 * nc);
     p.reg_cap = region_capacity(p.cap, p.S);
     return p;
@@ -237,13 +243,67 @@ inline void set_item_grids(BinArgs& b, int acc_per_cu, int gat_per_cu, int cus)
     b.Wgat = b.Pgat > b.S ? b.Pgat : b.S;
 }
 
-// The cells per counting block of a step with nc cells: kOnceCells when
-// that still gives every CU two blocks, else half of it (at 210 k cells,
-// 103 blocks of 2048 would leave most CUs idle in the one-pass K3).
-inline int counting_block(int nc, int cus)
+// The cell blocks of a step with nc cells, walked by the one-pass K3 and by
+// G2 (one workgroup of kOnceThreads per block), and the unit of the count
+// slots (block b counts in slot b % kCountSlots).  Equal blocks of q cells
+// (a multiple of 64), two per CU, so every CU sorts the same number of cells
+// in one round: 1.1 M cells on 256 CUs make 506 blocks of 2176, where blocks
+// of 2048 left 26 CUs a third block and K3 waited for them.  Blocks stay at
+// kOnceMinCells or more (a block's records in a strip form one run: shorter
+// runs write more partial lines); past 2 * cus * kOnceThreads * kOnceMaxCpt
+// cells they hold kOnceCells and run in rounds.  cpt = ceil(q / kOnceThreads),
+// the cells per thread the kernels are instantiated for: at most
+// kOnceMaxCpt at float32, 4 at float64 (five float64 cells per thread
+// spill K3's registers).
+constexpr int kOnceMaxCpt = 5;
+constexpr int kOnceMinCells = kOnceThreads * 2;
+struct OnceBlocks {
+    int grid;   // blocks (at least one)
+    int q;      // cells per block (the last one may hold fewer)
+    int cpt;    // cells per thread: 2 .. kOnceMaxCpt
+};
+inline OnceBlocks once_blocks(int nc, int cus, size_t elem_bytes)
 {
-    const long long blocks = ((long long)(nc > 0 ? nc : 0) + kOnceCells - 1) / kOnceCells;
-    return blocks >= 2LL * (cus > 0 ? cus : 1) ? kOnceCells : kOnceCells / 2;
+    const long long n = nc > 0 ? nc : 0;
+    const long long per = 2LL * (cus > 0 ? cus : 1);
+    const long long qmax = (long long)kOnceThreads * (elem_bytes == 4 ? kOnceMaxCpt : 4);
+    long long q = (n + per - 1) / per;
+    q = (q + 63) / 64 * 64;
+    if (q < kOnceMinCells) q = kOnceMinCells;
+    if (q > qmax) q = kOnceCells;
+    OnceBlocks o;
+    o.q = (int)q;
+    o.grid = (int)(n > q ? (n + q - 1) / q : 1);
+    o.cpt = (int)((q + kOnceThreads - 1) / kOnceThreads);
+    return o;
+}
+
+// The counting workgroups of a step (K1 and the fresh K3): one-pass block
+// o is split into sub = ceil(q / kCellsPerGroup) parts of qsub cells (the
+// block's last part takes the rest), workgroup w taking part w % sub of
+// block w / sub.  No counting workgroup straddles two one-pass blocks, so
+// the counts a fresh step leaves in each slot are exactly what the next
+// one-pass step reserves there.
+inline void set_count_blocks(BinArgs& b, const OnceBlocks& o)
+{
+    b.qcells = o.q;
+    b.sub = (o.q + kCellsPerGroup - 1) / kCellsPerGroup;
+    b.qsub = ((o.q + b.sub - 1) / b.sub + 63) / 64 * 64;
+    b.G1 = o.grid * b.sub;
+}
+
+// fn(std::integral_constant<int, cpt>{}) for the cells per thread of a
+// one-pass block (once_blocks().cpt); hipErrorInvalidValue for another.
+template <typename Fn>
+inline hipError_t with_cpt(int cpt, Fn&& fn)
+{
+    switch (cpt) {
+    case 2: return fn(std::integral_constant<int, 2>{});
+    case 3: return fn(std::integral_constant<int, 3>{});
+    case 4: return fn(std::integral_constant<int, 4>{});
+    case 5: return fn(std::integral_constant<int, 5>{});
+    default: return hipErrorInvalidValue;
+    }
 }
 
 // Strip-binned scatter (K1 unless `once`, K3, K4; K4 also runs the row DCT,

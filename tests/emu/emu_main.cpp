@@ -154,8 +154,7 @@ static int run(int nc, bool det, bool pot, int ch, bool tall, bool force_stage)
     } else {        // chosen per step, as on the device, for a 2-CU "device"
         set_item_grids(b, 2, 3, 2);
     }
-    b.G1 = (nc + kCellsPerGroup - 1) / kCellsPerGroup;
-    if (b.G1 < 1) b.G1 = 1;
+    b.G1 = count_grid_max(nc);          // rows of cnt; set per step below
     const size_t nslot = (size_t)kCountSlots * p.S;
     b.cnt = exact<unsigned>((size_t)b.G1 * p.S);
     b.xtot = exact<unsigned>(2 * nslot);           // two sets, by step parity
@@ -192,15 +191,15 @@ static int run(int nc, bool det, bool pot, int ch, bool tall, bool force_stage)
     unsigned pool_seen = 0;
     // one step: fresh (K1 + K3) or in one pass on the previous step's counts
     auto step = [&](bool once) -> int {
-        b.qcells = counting_block(nc, b.cus);   // as launch_bin_scatter sets it
+        const OnceBlocks ob = once_blocks(nc, b.cus, sizeof(T));   // as launch_bin_scatter
+        set_count_blocks(b, ob);
         if (once) {
-            const unsigned grid = nc > b.qcells ? (nc + b.qcells - 1) / b.qcells : 1;
-            if (b.qcells == kOnceCells)
-                launch(grid, kOnceThreads, fill_once_lds(p.S),
-                       [&] { k_bin_fill_once<T, kCellsPerThread>(px, py, sx, sy, nc, g, b); });
-            else
-                launch(grid, kOnceThreads, fill_once_lds(p.S),
-                       [&] { k_bin_fill_once<T, kCellsPerThread / 2>(px, py, sx, sy, nc, g, b); });
+            with_cpt(ob.cpt, [&](auto c) -> hipError_t {
+                constexpr int CPT = decltype(c)::value;
+                launch((unsigned)ob.grid, kOnceThreads, fill_once_lds<T>(p.S),
+                       [&] { k_bin_fill_once<T, CPT>(px, py, sx, sy, nc, g, b); });
+                return hipSuccess;
+            });
         } else {
             launch(b.G1, kBinThreads, hist, [&] { k_bin_count<T>(px, py, sx, sy, nc, g, b); });
             if (stage)
@@ -232,18 +231,13 @@ static int run(int nc, bool det, bool pot, int ch, bool tall, bool force_stage)
         if (nc > 0) {
             const size_t glds = (size_t)gather_rows<T>(p.R, N) * N * 2 * sizeof(T);
             launch(b.Wgat, kAccThreads, glds, [&] { k_gather_bin<T>(g, b, fx, fy); });
-            const int qc = counting_block(nc, b.cus);   // as launch_bin_gather
-            const unsigned gg = (unsigned)((nc + qc - 1) / qc);
-            if (qc == kOnceCells)
-                launch(gg, kOnceThreads, gather_out_lds<kOnceThreads, kCellsPerThread>(), [&] {
-                    k_gather_out<T, kOnceThreads, kCellsPerThread>(px, py, sx, sy, nc, g, b, fx,
-                                                                   fy, gx, gy);
+            with_cpt(ob.cpt, [&](auto c) -> hipError_t {   // as launch_bin_gather
+                constexpr int CPT = decltype(c)::value;
+                launch((unsigned)ob.grid, kOnceThreads, gather_out_lds<kOnceThreads, CPT>(), [&] {
+                    k_gather_out<T, kOnceThreads, CPT>(px, py, sx, sy, nc, g, b, fx, fy, gx, gy);
                 });
-            else
-                launch(gg, kOnceThreads, gather_out_lds<kOnceThreads, kCellsPerThread / 2>(), [&] {
-                    k_gather_out<T, kOnceThreads, kCellsPerThread / 2>(px, py, sx, sy, nc, g, b,
-                                                                       fx, fy, gx, gy);
-                });
+                return hipSuccess;
+            });
         }
         // the older set of counts is zero again for the next step
         const unsigned* older = b.xtot + (size_t)(b.par ^ 1) * nslot;

@@ -128,5 +128,7 @@ inline float atomicAdd(float* p, float v) { return unsafeAtomicAdd(p, v); }
 inline double atomicAdd(double* p, double v) { return unsafeAtomicAdd(p, v); }
 
 typedef int hipError_t;
+constexpr hipError_t hipSuccess = 0;
+constexpr hipError_t hipErrorInvalidValue = 1;
 typedef void* hipStream_t;
 typedef void* hipEvent_t;
