@@ -941,11 +941,11 @@ __host__ __device__ constexpr size_t fill_once_lds(int S)
 }
 
 // NT = kOnceThreads threads, up to CPT cells each: one block of b.qcells
-// cells (once_blocks: equal blocks, two per CU when they fit, at least
-// 1024 cells so a block's runs in a strip stay long and few reservation
-// atomics land on each counter).  Six waves per SIMD where the registers
-// allow it (float32 up to 4 cells per thread: three workgroups per CU when
-// the blocks run in rounds), else four (two workgroups per CU).
+// cells (once_blocks: equal blocks, as many per CU as are resident, at
+// least 1024 cells so a block's runs in a strip stay long and few
+// reservation atomics land on each counter).  Six waves per SIMD where the
+// registers allow it (float32 up to 4 cells per thread: three workgroups
+// per CU), else four (two workgroups per CU).
 template <typename T, int CPT>
 __host__ __device__ constexpr int once_waves()
 {

@@ -246,15 +246,17 @@ inline void set_item_grids(BinArgs& b, int acc_per_cu, int gat_per_cu, int cus)
 // The cell blocks of a step with nc cells, walked by the one-pass K3 and by
 // G2 (one workgroup of kOnceThreads per block), and the unit of the count
 // slots (block b counts in slot b % kCountSlots).  Equal blocks of q cells
-// (a multiple of 64), two per CU, so every CU sorts the same number of cells
-// in one round: 1.1 M cells on 256 CUs make 506 blocks of 2176, where blocks
-// of 2048 left 26 CUs a third block and K3 waited for them.  Blocks stay at
-// kOnceMinCells or more (a block's records in a strip form one run: shorter
-// runs write more partial lines); past 2 * cus * kOnceThreads * kOnceMaxCpt
-// cells they hold kOnceCells and run in rounds.  cpt = ceil(q / kOnceThreads),
-// the cells per thread the kernels are instantiated for: at most
-// kOnceMaxCpt at float32, 4 at float64 (five float64 cells per thread
-// spill K3's registers).
+// (a multiple of 64), as many per CU as are resident at once (three at
+// float32, two at float64: registers), so every CU sorts the same number of
+// cells in one round: 1.1 M float32 cells on 256 CUs make 748 blocks of
+// 1472, where blocks of 2048 left 26 CUs a third block and K3 waited for
+// them (two blocks of 2176 per CU measured 1.2 us slower than three).
+// Blocks stay at kOnceMinCells or more (a block's records in a strip form
+// one run: shorter runs write more partial lines); past that many blocks'
+// worth of kOnceThreads * cpt cells they hold kOnceCells and run in rounds.
+// cpt = ceil(q / kOnceThreads), the cells per thread the kernels are
+// instantiated for: at most kOnceMaxCpt at float32, 4 at float64 (five
+// float64 cells per thread spill K3's registers).
 constexpr int kOnceMaxCpt = 5;
 constexpr int kOnceMinCells = kOnceThreads * 2;
 struct OnceBlocks {
@@ -265,7 +267,7 @@ struct OnceBlocks {
 inline OnceBlocks once_blocks(int nc, int cus, size_t elem_bytes)
 {
     const long long n = nc > 0 ? nc : 0;
-    const long long per = 2LL * (cus > 0 ? cus : 1);
+    const long long per = (elem_bytes == 4 ? 3LL : 2LL) * (cus > 0 ? cus : 1);
     const long long qmax = (long long)kOnceThreads * (elem_bytes == 4 ? kOnceMaxCpt : 4);
     long long q = (n + per - 1) / per;
     q = (q + 63) / 64 * 64;
