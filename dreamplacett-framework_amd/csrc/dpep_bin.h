@@ -1462,7 +1462,7 @@ struct FieldRow {
     __device__ __forceinline__ vec2_t<T> operator[](int q) const { return vec2_t<T>{x[q], y[q]}; }
 };
 
-template <typename T>
+template <typename T, bool kGuess>
 __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
     Grid g, BinArgs b, const T* __restrict__ fx, const T* __restrict__ fy)
 {
@@ -1474,12 +1474,20 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
     const vec4_t<T>* recg = reinterpret_cast<const vec4_t<T>*>(b.recg);
     vec2_t<T>* out = reinterpret_cast<vec2_t<T>*>(b.gtmp);
     const T ba = (T)(g.bsx * g.bsy);
+    // kGuess (a grid of one workgroup per strip, b.Wgat == b.S): item w is
+    // strip w unless a strip is split, so the map of strip w is requested
+    // with the item and their loads are in flight together (G1 22.8 -> 21.8
+    // us at 1.1M cells on 2048^2; a run-time choice between the two forms
+    // measured slower than either; in K4 the same measured slower, its map's
+    // latency already overlapping the tile's zeroing).  With more items than
+    // strips (small grids) the guess is mostly wrong: wait for the item.
+    StripMap sm;
+    if constexpr (kGuess) strip_map(b, w, sm);
     if (w < (int)b.nitems[1]) {                 // uniform across the group
         const uint4 item = b.items_g[w];
         const int s = (int)(item.x & 0xFFFFu);
         const int k0 = s * R;
-        StripMap sm;
-        strip_map(b, s, sm);
+        if (!kGuess || s != w) strip_map(b, s, sm);  // uniform across the group
         unsigned e0, e1;                        // this item's records
         item_range(item, sm, e0, e1);
         // both fields of a bin side by side: one 2-element LDS read per bin

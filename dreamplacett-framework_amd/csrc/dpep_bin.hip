@@ -85,7 +85,10 @@ hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
 {
     if (nc <= 0) return ev ? hipEventRecord(ev, s) : hipSuccess;
     const size_t lds = (size_t)gather_rows<T>(b.R, g.N) * g.N * 2 * sizeof(T);
-    k_gather_bin<T><<<b.Wgat, kAccThreads, lds, s>>>(g, b, fx, fy);
+    if (b.Wgat == b.S)      // one workgroup per strip: item w is mostly strip w
+        k_gather_bin<T, true><<<b.Wgat, kAccThreads, lds, s>>>(g, b, fx, fy);
+    else
+        k_gather_bin<T, false><<<b.Wgat, kAccThreads, lds, s>>>(g, b, fx, fy);
     hipError_t e = hipGetLastError();
     if (e) return e;
     if (ev && (e = hipEventRecord(ev, s))) return e;
@@ -137,7 +140,7 @@ hipError_t bin_occupancy(int N, int R, int& acc_per_cu, int& gat_per_cu)
     });
     if (e) return e;
     return hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &gat_per_cu, (const void*)k_gather_bin<T>, kAccThreads,
+        &gat_per_cu, (const void*)k_gather_bin<T, false>, kAccThreads,
         (size_t)gather_rows<T>(R, N) * N * 2 * sizeof(T));
 }
 
@@ -167,7 +170,11 @@ static hipError_t prepare_bin_type()
                                        (int)fill_once_lds<T>(4096));
         });
     if (e) return e;
-    return hipFuncSetAttribute((const void*)k_gather_bin<T>,
+    if ((e = hipFuncSetAttribute((const void*)k_gather_bin<T, true>,
+                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 (int)kTileBytes)))
+        return e;
+    return hipFuncSetAttribute((const void*)k_gather_bin<T, false>,
                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)kTileBytes);
 }

@@ -230,7 +230,10 @@ static int run(int nc, bool det, bool pot, int ch, bool tall, bool force_stage)
         }
         if (nc > 0) {
             const size_t glds = (size_t)gather_rows<T>(p.R, N) * N * 2 * sizeof(T);
-            launch(b.Wgat, kAccThreads, glds, [&] { k_gather_bin<T>(g, b, fx, fy); });
+            if (b.Wgat == b.S)       // as launch_bin_gather
+                launch(b.Wgat, kAccThreads, glds, [&] { k_gather_bin<T, true>(g, b, fx, fy); });
+            else
+                launch(b.Wgat, kAccThreads, glds, [&] { k_gather_bin<T, false>(g, b, fx, fy); });
             with_cpt(ob.cpt, [&](auto c) -> hipError_t {   // as launch_bin_gather
                 constexpr int CPT = decltype(c)::value;
                 launch((unsigned)ob.grid, kOnceThreads, gather_out_lds<kOnceThreads, CPT>(), [&] {
