@@ -3,7 +3,8 @@
 // Every global buffer is malloc'd at its exact size and the LDS tail beyond
 // the launch's dynamic size is poisoned, so any out-of-bounds index aborts
 // with a report.  Results are compared with the float64 oracle.
-// Usage: emu_main <f32|f64> M N ncells [det] [nopot] [ch=<entries>] [tall]
+// Usage: emu_main <f32|f64> M N ncells [det] [nopot] [ch=<entries>] [tall] [stage]
+//        emu_main blocks   (host logic of the cell blocks)
 #include <sanitizer/asan_interface.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -323,8 +324,73 @@ static int dispatch(int M, int N, int nc, bool det, bool pot, int ch, bool tall,
     return 2;
 }
 
+// Host logic of the cell blocks (once_blocks, set_count_blocks, count_cells):
+// every cell in exactly one one-pass block and one counting part, no part
+// straddling two blocks, no empty block, the kernels' limits and the cnt
+// rows (count_grid_max) respected, for many cell counts and CU counts.
+static int check_blocks()
+{
+    using namespace dpep;
+    std::mt19937_64 rng(7);
+    std::vector<long long> ncs = {0, 1, 63, 64, 1023, 1024, 1025, 2047, 2048, 2049, 4096,
+                                  210000, 256000, 1100000, 2000000, 2600000, 1 << 26};
+    const int cuss[] = {1, 2, 80, 256, 304};
+    for (int c : cuss)
+        for (int k = 1; k <= 3; ++k)
+            for (long long q : {2048LL, 2560LL})
+                for (long long d = -70; d <= 70; d += 35)
+                    ncs.push_back(k * c * q + d);
+    for (int r = 0; r < 300; ++r) ncs.push_back((long long)(rng() % 3000000));
+    long long checked = 0;
+    for (int cus : cuss)
+        for (int esz : {4, 8})
+            for (long long ncl : ncs) {
+                if (ncl < 0) continue;
+                const int nc = (int)ncl;
+                const OnceBlocks o = once_blocks(nc, cus, (size_t)esz);
+                const int cmax = esz == 4 ? kOnceMaxCpt : 4;
+                auto fail = [&](const char* what) {
+                    fprintf(stderr, "blocks: %s (nc %d cus %d esz %d: grid %d q %d cpt %d)\n",
+                            what, nc, cus, esz, o.grid, o.q, o.cpt);
+                    return 1;
+                };
+                if (o.q % 64 || o.q < kOnceMinCells) return fail("block size");
+                if (o.cpt < 2 || o.cpt > cmax || o.cpt * kOnceThreads < o.q ||
+                    (o.cpt - 1) * kOnceThreads >= o.q)
+                    return fail("cells per thread");
+                if (o.grid < 1 || (long long)o.grid * o.q < nc ||
+                    (nc > 0 && (long long)(o.grid - 1) * o.q >= nc))
+                    return fail("grid");
+                BinArgs b{};
+                set_count_blocks(b, o);
+                if (b.qsub > kCellsPerGroup || b.qsub % 64 || (b.sub - 1) * b.qsub >= o.q)
+                    return fail("parts");
+                if (b.G1 != o.grid * b.sub || b.G1 > count_grid_max(nc)) return fail("cnt rows");
+                long long next = 0;     // parts in order tile [0, nc) exactly
+                for (int w = 0; w < b.G1; ++w) {
+                    blockIdx = dim3((unsigned)w);
+                    int c0, cend;
+                    const int slot = count_cells(b, nc, c0, cend);
+                    const int ob = w / b.sub;
+                    if (slot != (ob & (kCountSlots - 1))) return fail("slot");
+                    if (cend < c0 || c0 < ob * o.q || (c0 < nc && cend > (ob + 1) * o.q))
+                        return fail("part outside its block");
+                    if (cend > c0) {
+                        if (c0 != next) return fail("parts leave a gap or overlap");
+                        next = cend;
+                    }
+                }
+                if (next != nc) return fail("parts do not cover the cells");
+                ++checked;
+            }
+    blockIdx = dim3(0);
+    printf("blocks ok (%lld cases)\n", checked);
+    return 0;
+}
+
 int main(int argc, char** argv)
 {
+    if (argc == 2 && !strcmp(argv[1], "blocks")) return check_blocks();
     if (argc < 5) { fprintf(stderr, "usage: %s f32|f64 M N nc [det] [nopot]\n", argv[0]); return 2; }
     const bool f64 = !strcmp(argv[1], "f64");
     const int M = atoi(argv[2]), N = atoi(argv[3]), nc = atoi(argv[4]);

@@ -51,6 +51,9 @@ CASES = [
     "f32 8 8192 3000 tall",  # 2-row strips, the largest LDS tile and row FFT
     "f32 64 64 2000 tall stage", "f64 64 64 1500 ch=100 stage",
     "f32 16 128 9000 tall stage",  # blocks beyond the stage: records stored straight
+    # one-pass blocks of 4 and 5 cells per thread (three blocks per "CU" of the
+    # 2-CU emulated device at float32, two at float64)
+    "f32 64 64 10800", "f32 64 64 13200 tall", "f64 64 64 7200",
 ]
 
 
@@ -61,3 +64,12 @@ def test_kernels_in_bounds_and_accurate(emu, case):
                        timeout=600, env=env)
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
     assert "emu " in r.stdout
+
+
+def test_cell_blocks_host_logic(emu):
+    """once_blocks / set_count_blocks / count_cells: every cell in exactly one
+    one-pass block and one counting part, no part straddling two blocks, the
+    kernels' cells-per-thread limits and the cnt rows respected."""
+    r = subprocess.run([emu, "blocks"], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert "blocks ok" in r.stdout

@@ -121,6 +121,21 @@ def test_full_size_configs(oracle, cfg):
     print(f"C{cfg} full: " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
 
 
+@pytest.mark.parametrize("n_mov,dtype", [(600_000, np.float32), (1_400_000, np.float32),
+                                         (1_800_000, np.float32), (900_000, np.float64)])
+def test_one_pass_block_sizes(oracle, n_mov, dtype):
+    """The C3 design at cell counts whose one-pass blocks (once_blocks: three
+    per CU at float32, two at float64, on a 256-CU MI355X) take 2, 4 and 5
+    cells per thread at float32 and 4 at float64 (1.1 M cells, 3 per thread,
+    and 2.0 M cells, blocks in rounds, are the full-size configurations)."""
+    from dpep import workloads
+    w = workloads.config3(seed=3, n_mov=n_mov)
+    errs = check(run_gpu(w, dtype=dtype), run_oracle(oracle, w, dtype=dtype), dtype,
+                 f"{n_mov} cells")
+    print(f"{n_mov} cells {np.dtype(dtype).name}: " +
+          " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
+
+
 def test_float64_mode(oracle):
     from dpep import workloads
     w = workloads.small(5, seed=3, cells=100000, grid=512)
