@@ -13,6 +13,14 @@
 //                 offsets (workgroup 0 publishes the strip table, the
 //                 step's chunk sizes and the K4 / G1 item lists);
 //                 cells -> strip-sorted records; tall cells -> B
+//                 (K1 and this form: the first step, or every step
+//                 with DPEP_FLAG_TWO_PASS; each one-pass block split
+//                 into counting parts of at most 1024 cells)
+//   k_bin_fill_once  the steady state: K3 without K1, on regions   K3
+//                 sized from the previous step's counts; one equal
+//                 block of cells per workgroup (once_blocks); records
+//                 past a region's room -> overflow pool; tall cells
+//                 added to B by 16-thread teams at the block's end
 //   k_strip_acc   one work item = (strip, chunk): LDS accumulate,     K4
 //                 flush rho = D0 + tile (+B); the chunks of a split
 //                 strip add into B and the last one to finish flushes
@@ -20,7 +28,9 @@
 //                 rows staged in LDS, each record's partial force over
 //                 the rows of this strip, in record order
 //   k_gather_out  forces back to cell order: sum of the (one or two)  G2
-//                 partials; tall cells gathered by the whole workgroup
+//                 partials, on the one-pass blocks; tall cells
+//                 gathered by 16-thread teams (larger ones by the
+//                 whole workgroup)
 //
 // Accumulation is fixed point everywhere: round(v * 2^f) added as uint64
 // (LDS, the side map B), with f = fix_exponent_of(nc_max, dtype) so a bin's
