@@ -276,6 +276,28 @@ def test_no_cells_and_shrinking_cell_count(oracle):
             ctx.set_cells(*[np.zeros(w.nc + 1, np.float32)] * 4)
 
 
+def test_cell_count_changes_across_block_shapes(oracle):
+    """One context stepped with 0.3 M, then 1.4 M, then 0.9 M cells: each count
+    cuts the cells into blocks of another size (2, 4, 3 cells per thread on a
+    256-CU MI355X), so each one-pass step plans its regions from counts taken
+    over a different block layout and overflows into the pool where they fall
+    short.  Every step matches the oracle, and stepping the same cells again
+    (regions now from a matching layout) is bitwise the same."""
+    import dpep
+    from dpep import workloads
+    w = workloads.config3(seed=5, n_mov=1_400_000)
+    cells = w.cells(np.float32)
+    with dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh) as ctx:
+        ctx.set_initial_density(w.d0n.astype(np.float32))
+        for n in (300_000, 1_400_000, 900_000):
+            sub = tuple(c[:n] for c in cells)
+            out = ctx.step(*sub)
+            again = ctx.step(*sub)
+            for k in out:
+                assert np.array_equal(out[k], again[k], equal_nan=True), f"{n}: {k}"
+            check(out, run_oracle(oracle, w, cells=sub), np.float32, f"{n} cells")
+
+
 def test_timings_and_kernel_times():
     import dpep
     from dpep import workloads
