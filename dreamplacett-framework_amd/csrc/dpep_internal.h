@@ -255,8 +255,9 @@ inline void set_item_grids(BinArgs& b, int acc_per_cu, int gat_per_cu, int cus)
 // one run: shorter runs write more partial lines); past that many blocks'
 // worth of kOnceThreads * cpt cells they hold kOnceCells and run in rounds.
 // cpt = ceil(q / kOnceThreads), the cells per thread the kernels are
-// instantiated for: at most kOnceMaxCpt at float32, 4 at float64 (five
-// float64 cells per thread spill K3's registers).
+// instantiated for, at most kOnceMaxCpt (five float64 cells per thread spill
+// 48 of K3's registers, and still measured faster than a second round of
+// 2048-cell blocks: 1.1 M float64 cells at 512^2 0.1062 -> 0.1002 ms).
 constexpr int kOnceMaxCpt = 5;
 constexpr int kOnceMinCells = kOnceThreads * 2;
 struct OnceBlocks {
@@ -268,7 +269,7 @@ inline OnceBlocks once_blocks(int nc, int cus, size_t elem_bytes)
 {
     const long long n = nc > 0 ? nc : 0;
     const long long per = (elem_bytes == 4 ? 3LL : 2LL) * (cus > 0 ? cus : 1);
-    const long long qmax = (long long)kOnceThreads * (elem_bytes == 4 ? kOnceMaxCpt : 4);
+    const long long qmax = (long long)kOnceThreads * kOnceMaxCpt;
     long long q = (n + per - 1) / per;
     q = (q + 63) / 64 * 64;
     if (q < kOnceMinCells) q = kOnceMinCells;

@@ -348,7 +348,7 @@ static int check_blocks()
                 if (ncl < 0) continue;
                 const int nc = (int)ncl;
                 const OnceBlocks o = once_blocks(nc, cus, (size_t)esz);
-                const int cmax = esz == 4 ? kOnceMaxCpt : 4;
+                const int cmax = kOnceMaxCpt;
                 auto fail = [&](const char* what) {
                     fprintf(stderr, "blocks: %s (nc %d cus %d esz %d: grid %d q %d cpt %d)\n",
                             what, nc, cus, esz, o.grid, o.q, o.cpt);

@@ -53,7 +53,7 @@ CASES = [
     "f32 16 128 9000 tall stage",  # blocks beyond the stage: records stored straight
     # one-pass blocks of 4 and 5 cells per thread (three blocks per "CU" of the
     # 2-CU emulated device at float32, two at float64)
-    "f32 64 64 10800", "f32 64 64 13200 tall", "f64 64 64 7200",
+    "f32 64 64 10800", "f32 64 64 13200 tall", "f64 64 64 7200", "f64 64 64 8800 tall",
 ]
 
 

@@ -126,8 +126,9 @@ def test_full_size_configs(oracle, cfg):
 def test_one_pass_block_sizes(oracle, n_mov, dtype):
     """The C3 design at cell counts whose one-pass blocks (once_blocks: three
     per CU at float32, two at float64, on a 256-CU MI355X) take 2, 4 and 5
-    cells per thread at float32 and 4 at float64 (1.1 M cells, 3 per thread,
-    and 2.0 M cells, blocks in rounds, are the full-size configurations)."""
+    cells per thread at float32 and 4 at float64 (1.1 M cells, 3 per thread
+    at float32 and 5 at float64, and 2.0 M cells, blocks in rounds, are the
+    full-size configurations)."""
     from dpep import workloads
     w = workloads.config3(seed=3, n_mov=n_mov)
     errs = check(run_gpu(w, dtype=dtype), run_oracle(oracle, w, dtype=dtype), dtype,
