@@ -52,8 +52,10 @@ CASES = [
     "f32 64 64 2000 tall stage", "f64 64 64 1500 ch=100 stage",
     "f32 16 128 9000 tall stage",  # blocks beyond the stage: records stored straight
     # one-pass blocks of 4 and 5 cells per thread (three blocks per "CU" of the
-    # 2-CU emulated device at float32, two at float64)
-    "f32 64 64 10800", "f32 64 64 13200 tall", "f64 64 64 7200", "f64 64 64 8800 tall",
+    # 2-CU emulated device at float32, two at float64), and past 5 cells per
+    # thread the 2048-cell blocks in rounds, with tall cells
+    "f32 64 64 10800", "f32 64 64 13200 tall", "f32 64 64 16800 tall",
+    "f64 64 64 7200", "f64 64 64 8800 tall",
 ]
 
 
