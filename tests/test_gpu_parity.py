@@ -346,6 +346,32 @@ def test_full_step_8192_columns(oracle):
     print(check(out, ref, np.float32, "64x8192"), flush=True)
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_offset_die_with_oblong_bins(oracle, dtype):
+    """A die whose lower-left corner is not the origin, bins 5 x 11.72 (the
+    field weights carry bsx / bsy), 1024 x 256 bins (128 strips of 8 rows of
+    256 columns), cells of all sizes including some past every die edge."""
+    M, N = 1024, 256
+    xl, yl = -1234.5, 777.25
+    xh, yh = xl + 5.0 * M, yl + 3000.0
+    rng = np.random.default_rng(1024 + 256)
+    nc = 60000
+    sx = rng.uniform(0.3, 25.0, nc)
+    sy = rng.uniform(0.3, 60.0, nc)
+    px = rng.uniform(xl - 10.0, xh, nc)
+    py = rng.uniform(yl - 20.0, yh, nc)
+    cells = [a.astype(dtype) for a in (px, py, sx, sy)]
+    d0 = (0.4 * rng.random((M, N))).astype(dtype)
+
+    class W:
+        pass
+    w = W()
+    w.M, w.N, w.xl, w.yl, w.xh, w.yh, w.d0n = M, N, xl, yl, xh, yh, d0
+    errs = check(run_gpu(w, dtype, cells=cells), run_oracle(oracle, w, dtype, cells=cells),
+                 dtype, f"offset die {np.dtype(dtype).name}")
+    print(errs, flush=True)
+
+
 def test_step_device_matches_host_step():
     """dpep_step_device on caller-owned device buffers (allocated through the
     same HIP runtime libdpep links) equals the host-buffer step; afterwards
