@@ -145,6 +145,17 @@ def test_float64_mode(oracle):
               run_oracle(oracle, w, np.float64), np.float64, f"f64 det={det}")
 
 
+def test_float64_4096_grid(oracle):
+    """float64 at 4096 x 4096 (the largest float64 grid): 4-row strips, the
+    gather staging two rows of both field maps at a time, the 4096-point
+    column and row passes; the C4 recipe with 300 K cells."""
+    from dpep import workloads
+    w = workloads.small(4, seed=5, cells=300000, grid=4096)
+    errs = check(run_gpu(w, np.float64), run_oracle(oracle, w, np.float64), np.float64,
+                 "f64 4096")
+    print(errs, flush=True)
+
+
 def test_no_stretch_semantics(oracle):
     """DPEP_FLAG_NO_STRETCH reproduces the TT path's density (original sizes,
     ratio 1: scatter_ttnn_client.py:628-649)."""
