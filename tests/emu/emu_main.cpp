@@ -3,7 +3,7 @@
 // Every global buffer is malloc'd at its exact size and the LDS tail beyond
 // the launch's dynamic size is poisoned, so any out-of-bounds index aborts
 // with a report.  Results are compared with the float64 oracle.
-// Usage: emu_main <f32|f64> M N ncells [det] [nopot] [ch=<entries>] [tall] [stage]
+// Usage: emu_main <f32|f64> M N ncells [det] [nopot] [ch=<entries>] [tall] [stage] [off]
 //        emu_main blocks   (host logic of the cell blocks)
 #include <sanitizer/asan_interface.h>
 #include <stdio.h>
@@ -102,12 +102,14 @@ static std::vector<T> table(int L, bool post)
 }
 
 template <typename T, int LM, int LN>
-static int run(int nc, bool det, bool pot, int ch, bool tall, bool force_stage)
+static int run(int nc, bool det, bool pot, int ch, bool tall, bool force_stage, bool off)
 {
     using namespace dpep;
     const int M = LM, N = LN;
     const size_t mn = (size_t)M * N;
-    const double xl = 0, yl = 0, xh = 100.0 * M / 8, yh = 80.0 * N / 8;
+    // off: a die whose lower-left corner is not the origin
+    const double xl = off ? -1234.5 : 0.0, yl = off ? 777.25 : 0.0;
+    const double xh = xl + 100.0 * M / 8, yh = yl + 80.0 * N / 8;
     Grid g{};
     g.M = M; g.N = N; g.xl = xl; g.yl = yl; g.xh = xh; g.yh = yh;
     g.bsx = (xh - xl) / M; g.bsy = (yh - yl) / N; g.inv_ba = 1.0 / (g.bsx * g.bsy);
@@ -313,9 +315,10 @@ static int run(int nc, bool det, bool pot, int ch, bool tall, bool force_stage)
 }
 
 template <typename T>
-static int dispatch(int M, int N, int nc, bool det, bool pot, int ch, bool tall, bool stage)
+static int dispatch(int M, int N, int nc, bool det, bool pot, int ch, bool tall, bool stage,
+                    bool off)
 {
-#define CASE(a, b) if (M == a && N == b) return run<T, a, b>(nc, det, pot, ch, tall, stage);
+#define CASE(a, b) if (M == a && N == b) return run<T, a, b>(nc, det, pot, ch, tall, stage, off);
     CASE(8, 8) CASE(16, 16) CASE(8, 32) CASE(64, 64) CASE(16, 128) CASE(128, 16)
     CASE(256, 32) CASE(32, 256) CASE(32, 2048) CASE(16, 4096)
     if constexpr (sizeof(T) == 4) { CASE(8, 8192) }
@@ -394,15 +397,16 @@ int main(int argc, char** argv)
     if (argc < 5) { fprintf(stderr, "usage: %s f32|f64 M N nc [det] [nopot]\n", argv[0]); return 2; }
     const bool f64 = !strcmp(argv[1], "f64");
     const int M = atoi(argv[2]), N = atoi(argv[3]), nc = atoi(argv[4]);
-    bool det = false, pot = true, tall = false, stage = false;
+    bool det = false, pot = true, tall = false, stage = false, off = false;
     int ch = 0;
     for (int i = 5; i < argc; ++i) {
         if (!strcmp(argv[i], "det")) det = true;
         if (!strcmp(argv[i], "nopot")) pot = false;
         if (!strcmp(argv[i], "tall")) tall = true;
         if (!strcmp(argv[i], "stage")) stage = true;
+        if (!strcmp(argv[i], "off")) off = true;
         if (!strncmp(argv[i], "ch=", 3)) ch = atoi(argv[i] + 3);
     }
-    return f64 ? dispatch<double>(M, N, nc, det, pot, ch, tall, stage)
-               : dispatch<float>(M, N, nc, det, pot, ch, tall, stage);
+    return f64 ? dispatch<double>(M, N, nc, det, pot, ch, tall, stage, off)
+               : dispatch<float>(M, N, nc, det, pot, ch, tall, stage, off);
 }

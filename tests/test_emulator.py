@@ -38,7 +38,8 @@ def emu(tmp_path_factory):
 
 # ch=<n> forces n entries per strip work item (exercises the split-strip
 # reduce); tall gives a tenth of the cells a span of 3..40 rows (side map B);
-# stage forces K3's staged form (the library picks it from 512 strips on).
+# stage forces K3's staged form (the library picks it from 512 strips on);
+# off moves the die's lower-left corner off the origin.
 CASES = [
     "f32 8 8 50", "f32 16 16 200 tall", "f32 8 32 60 nopot", "f32 16 128 3000 ch=128",
     "f32 128 16 300", "f64 8 8 40", "f64 64 64 1000 ch=100 tall",
@@ -56,6 +57,7 @@ CASES = [
     # thread the 2048-cell blocks in rounds, with tall cells
     "f32 64 64 10800", "f32 64 64 13200 tall", "f32 64 64 16800 tall",
     "f64 64 64 7200", "f64 64 64 8800 tall",
+    "f32 64 64 3000 tall off", "f64 16 128 2000 off",
 ]
 
 
