@@ -36,15 +36,13 @@
 #include <unistd.h>
 
 #include <algorithm>
-#include <atomic>
 #include <chrono>
-#include <condition_variable>
-#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
 
 #include "dpep.h"
+#include "dpep_copy_pool.h"
 
 namespace {
 
@@ -77,87 +75,6 @@ void publish_flag(const std::string& path, const char* content)
     if (rename(part.c_str(), path.c_str()) != 0)
         fprintf(stderr, "[server] cannot rename %s\n", part.c_str());
 }
-
-// A fixed set of worker threads that copy lists of (dst, src, bytes) pieces
-// between the shm file and the page-locked staging buffers; the calling
-// thread takes part.  One memcpy thread moves ~10 GB/s, below the link.
-class CopyPool {
-  public:
-    explicit CopyPool(int workers)
-    {
-        for (int i = 0; i < workers; ++i) threads_.emplace_back([this] { run(); });
-    }
-    ~CopyPool()
-    {
-        {
-            std::lock_guard<std::mutex> g(mu_);
-            quit_ = true;
-        }
-        cv_.notify_all();
-        for (auto& t : threads_) t.join();
-    }
-    struct Job {
-        void* dst;
-        const void* src;
-        size_t bytes;
-    };
-    // Copies every job, split into pieces of about 1 MiB, and returns when
-    // all are done.
-    void copy(const std::vector<Job>& jobs)
-    {
-        constexpr size_t kPiece = 1u << 20;
-        pieces_.clear();
-        for (const Job& j : jobs)
-            for (size_t o = 0; o < j.bytes; o += kPiece)
-                pieces_.push_back({(char*)j.dst + o, (const char*)j.src + o,
-                                   std::min(kPiece, j.bytes - o)});
-        if (pieces_.empty()) return;
-        {
-            std::lock_guard<std::mutex> g(mu_);
-            next_.store(0);
-            left_.store(pieces_.size());
-            ++round_;
-        }
-        cv_.notify_all();
-        work();
-        std::unique_lock<std::mutex> g(mu_);
-        done_cv_.wait(g, [this] { return left_.load() == 0; });
-    }
-
-  private:
-    void work()
-    {
-        for (;;) {
-            const size_t i = next_.fetch_add(1);
-            if (i >= pieces_.size()) return;
-            memcpy(pieces_[i].dst, pieces_[i].src, pieces_[i].bytes);
-            if (left_.fetch_sub(1) == 1) {
-                std::lock_guard<std::mutex> g(mu_);
-                done_cv_.notify_all();
-            }
-        }
-    }
-    void run()
-    {
-        unsigned long seen = 0;
-        for (;;) {
-            {
-                std::unique_lock<std::mutex> g(mu_);
-                cv_.wait(g, [&] { return quit_ || round_ != seen; });
-                if (quit_) return;
-                seen = round_;
-            }
-            work();
-        }
-    }
-    std::vector<std::thread> threads_;
-    std::vector<Job> pieces_;
-    std::mutex mu_;
-    std::condition_variable cv_, done_cv_;
-    std::atomic<size_t> next_{0}, left_{0};
-    unsigned long round_ = 0;
-    bool quit_ = false;
-};
 
 float* host_floats(size_t n)
 {
@@ -313,7 +230,7 @@ int main(int argc, char** argv)
     float* h_sx = h_py + soa;
     float* h_sy = h_sx + soa;
     const unsigned hw = std::thread::hardware_concurrency();
-    CopyPool pool((int)std::min(7u, hw > 1 ? hw - 1 : 1u));
+    dpep::CopyPool pool((int)std::min(7u, hw > 1 ? hw - 1 : 1u));
 
     publish_flag(ready_flag, "READY\n");
     printf("[server] READY -- polling shm state\n");
@@ -373,7 +290,7 @@ int main(int argc, char** argv)
         float t[DPEP_NUM_TIMINGS] = {0};
         dpep_get_timings(ctx, t);
         const double tw0 = now_ms();
-        std::vector<CopyPool::Job> out;
+        std::vector<dpep::CopyPool::Job> out;
         if (cpu_dct) {
             out.push_back({shm_fx, h_raw, map_bytes});
             memset(shm_fy, 0, map_bytes);
