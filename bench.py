@@ -9,7 +9,16 @@ Workload (default): 1.1M movable cells (lognormal widths, height 12), 1300
 macros folded into the fixed density, die 27000 x 27000, 2048 x 2048 bins,
 80 % uniform + 20 % in four Gaussian clusters, seed 0 -- synthetic data of
 the benchmark's shape.  Cell arrays and the fixed density are resident in
-HBM before the timed region; one step = one dpep_compute() on them.
+HBM before the timed region; one step = one dpep_compute() on them.  With
+--config 5 (1.1M cells in 5 % of the die, 512 x 512) a step is one step of
+its stated loop instead: every step's positions (the previous step's plus a
+seeded N(0, 0.5 bin) per cell) are resident before the timed region, and
+the K timed steps walk through them (dpep_step_device).
+
+Besides `value`, the line carries the step with moving cells (`moving`: the
+same drift applied to this workload, and a re-spread between two unrelated
+placements), each with one-pass and counted binning and the overflow-pool
+records per step.
 
 Prints ONE JSON line (the driver's contract).
 """
@@ -248,6 +257,132 @@ def cold_steps(w, dtype, potential, cells, n_ctx=3, steps=60, warmup=6):
     return round(ms, 4)
 
 
+class DeviceSets:
+    """Position sets resident on the device before any timed region (one
+    (px, py) pair per step, the sizes once), and steps of a context through
+    them with dpep_step_device on the context's stream."""
+
+    def __init__(self, sets, sx, sy):
+        import dpep
+        self.lib = dpep.load_library()
+        self.hip = hip_runtime()
+        self.bufs = []
+        self.nc = int(sx.size)
+        self.sx, self.sy = self._up(sx), self._up(sy)
+        self.pos = [(self._up(px), self._up(py)) for px, py in sets]
+
+    def _up(self, a):
+        a = np.ascontiguousarray(a)
+        p = ctypes.c_void_p()
+        assert self.hip.hipMalloc(ctypes.byref(p), max(1, a.nbytes)) == 0
+        self.bufs.append(p)
+        assert self.hip.hipMemcpy(p, a.ctypes.data, a.nbytes, 1) == 0
+        return p
+
+    def step(self, ctx, k):
+        import dpep
+        px, py = self.pos[k]
+        rc = self.lib.dpep_step_device(ctx.handle, px, py, self.sx, self.sy, self.nc,
+                                       None, None, None, None, None, None, None)
+        if rc:
+            raise RuntimeError(dpep.last_error())
+
+    def free(self):
+        for p in self.bufs:
+            self.hip.hipFree(p)
+        self.bufs = []
+
+
+def sequence_run(w, dtype, potential, dev, steps, two_pass=False, stats=False,
+                 profile=False):
+    """One fresh context stepped through dev's position sets 0..steps-1 (its
+    first step counts the cells; every later one sorts in one pass on the
+    plan the step before it made, unless two_pass).  Returns ms per step
+    (host-timed, synchronised on both sides), the per-step binning stats
+    when `stats` (each step then waits for the device: not timed), and the
+    per-kernel event averages when `profile`."""
+    import dpep
+    ctx = dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh, dtype=dtype,
+                       potential=potential, two_pass=two_pass)
+    try:
+        ctx.set_initial_density(w.d0n.astype(dtype))
+        if profile:
+            ctx.set_profiling(steps)
+        ctx.sync()
+        per = []
+        t0 = time.perf_counter()
+        for k in range(steps):
+            dev.step(ctx, k)
+            if stats:
+                per.append(ctx.binning_stats())
+        ctx.sync()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        kt = ctx.kernel_times_us() if profile else None
+    finally:
+        ctx.close()
+    return ms, per, kt
+
+
+def overflow_summary(per):
+    """Overflow-pool records over the one-pass steps of a run."""
+    once = [p for p in per if p["one_pass"]]
+    ov = np.array([p["overflow_records"] for p in once], dtype=np.int64)
+    rec = np.array([p["records"] for p in once], dtype=np.int64)
+    if ov.size == 0:
+        return {"one_pass_steps": 0}
+    return {"one_pass_steps": int(ov.size),
+            "overflow_records_mean": round(float(ov.mean()), 1),
+            "overflow_records_max": int(ov.max()),
+            "steps_with_overflow": int((ov > 0).sum()),
+            "records_mean": round(float(rec.mean()), 1),
+            "overflow_fraction_max": round(float((ov / np.maximum(rec, 1)).max()), 5)}
+
+
+def moving_cells(w, dtype, potential, steps=100):
+    """The step with cells that move between steps, positions resident on the
+    device: (1) the drift of the extreme-hotspot loop applied to this
+    workload's placement (N(0, 0.5 bin) per cell per step, seed = step),
+    `steps` steps; (2) a re-spread: the workload's placement alternating with
+    a uniform placement of the same cells every step, so each step's plan
+    comes from an unrelated placement (the one-pass binning's worst case).
+    Each is timed with one-pass binning and with counting every step, and
+    its overflow-pool records per step are counted in an untimed pass."""
+    from dpep import workloads
+    px0, py0, sx, sy = w.cells(dtype)
+    res = {}
+    sets = [(px.astype(dtype), py.astype(dtype))
+            for _, px, py in workloads.walk(w, steps)]
+    dev = DeviceSets(sets, sx, sy)
+    del sets
+    try:
+        _, per, _ = sequence_run(w, dtype, potential, dev, steps, stats=True)
+        ms1, _, _ = sequence_run(w, dtype, potential, dev, steps)
+        ms2, _, _ = sequence_run(w, dtype, potential, dev, steps, two_pass=True)
+    finally:
+        dev.free()
+    res["drift"] = {"workload": (f"{w.name} placement drifting N(0, 0.5 bin) per cell per "
+                                 f"step (seed = step), {steps} steps"),
+                    "ms_per_step": round(ms1, 4), "two_pass_ms_per_step": round(ms2, 4),
+                    **overflow_summary(per)}
+    rng = np.random.default_rng(12345)
+    ux = (rng.uniform(0.0, 1.0, w.nc) * (w.xh - w.xl - w.sx) + w.xl).astype(dtype)
+    uy = (rng.uniform(0.0, 1.0, w.nc) * (w.yh - w.yl - w.sy) + w.yl).astype(dtype)
+    n_alt = 20
+    dev = DeviceSets([(px0, py0) if k % 2 == 0 else (ux, uy) for k in range(n_alt)],
+                     sx, sy)
+    try:
+        _, per, _ = sequence_run(w, dtype, potential, dev, n_alt, stats=True)
+        ms1, _, _ = sequence_run(w, dtype, potential, dev, n_alt)
+        ms2, _, _ = sequence_run(w, dtype, potential, dev, n_alt, two_pass=True)
+    finally:
+        dev.free()
+    res["respread"] = {"workload": (f"{w.name} placement and a uniform placement of the "
+                                    f"same cells, alternating every step, {n_alt} steps"),
+                       "ms_per_step": round(ms1, 4), "two_pass_ms_per_step": round(ms2, 4),
+                       **overflow_summary(per)}
+    return res
+
+
 def cpu_baseline(w, seconds, max_steps=400):
     import pyoracle
     cb = pyoracle.CpuBaseline(w.M, w.N, w.xl, w.yl, w.xh, w.yh)
@@ -295,6 +430,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true",
                     help="skip the per-kernel event pass (for rocprofv3 runs)")
+    ap.add_argument("--no-moving", action="store_true",
+                    help="skip the moving-cell runs (drift and re-spread)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -315,21 +452,36 @@ def main():
     potential = not args.no_potential
     px, py, sx, sy = w.cells(dtype)
 
+    # the extreme-hotspot configuration is a loop of steps on moving cells:
+    # its positions are resident on the device for every step of the walk
+    walk_dev, walk_stats = None, None
+    if args.config == 5:
+        n_sets = max(args.steps, args.warmup, 1)
+        walk_dev = DeviceSets([(a.astype(dtype), b.astype(dtype)) for _, a, b in
+                               workloads.walk(w, n_sets)], sx, sy)
+
     ctx = dpep.Context(w.M, w.N, w.nc, w.xl, w.yl, w.xh, w.yh, dtype=dtype,
                        deterministic=args.deterministic, potential=potential,
                        two_pass=args.two_pass)
     ctx.set_initial_density(w.d0n.astype(dtype))
     ctx.set_cells(px, py, sx, sy)          # inputs resident in HBM from here
-    for _ in range(args.warmup):
-        ctx.compute()
-    ctx.sync()
-
-    # timed region: exactly K steps, synchronised on both sides
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        ctx.compute()
-    ctx.sync()
-    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    if walk_dev is None:
+        for _ in range(args.warmup):
+            ctx.compute()
+        ctx.sync()
+        # timed region: exactly K steps, synchronised on both sides
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            ctx.compute()
+        ctx.sync()
+        ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    else:
+        # warm-up: W steps of the walk on a context of their own; timed: a
+        # fresh context through K steps of the walk (its first step counts)
+        if args.warmup:
+            sequence_run(w, dtype, potential, walk_dev, args.warmup, two_pass=args.two_pass)
+        ms, _, _ = sequence_run(w, dtype, potential, walk_dev, args.steps,
+                                two_pass=args.two_pass)
 
     # PCIe-inclusive rate (host buffers in and out): never `value`.  The
     # pageable figure is every output to fresh numpy arrays; host_path() the
@@ -347,19 +499,32 @@ def main():
 
     kt = None
     if not args.no_profile:
-        # same K steps again with HIP events between launches on the
-        # context's stream: per-kernel average durations
-        ctx.set_profiling(args.steps)
-        for _ in range(args.steps):
-            ctx.compute()
-        ctx.sync()
-        kt = ctx.kernel_times_us()
-        ctx.set_profiling(0)
+        if walk_dev is None:
+            # same K steps again with HIP events between launches on the
+            # context's stream: per-kernel average durations
+            ctx.set_profiling(args.steps)
+            for _ in range(args.steps):
+                ctx.compute()
+            ctx.sync()
+            kt = ctx.kernel_times_us()
+            ctx.set_profiling(0)
+        else:
+            _, _, kt = sequence_run(w, dtype, potential, walk_dev, args.steps,
+                                    two_pass=args.two_pass, profile=True)
+            _, per, _ = sequence_run(w, dtype, potential, walk_dev, args.steps,
+                                     two_pass=args.two_pass, stats=True)
+            walk_stats = overflow_summary(per)
     ctx.close()
+    if walk_dev is not None:
+        walk_dev.free()
     if host is not None:
         host.update(host_path(w, dtype, potential, px, py, sx, sy))
         # the DREAMPlace adapter's steady state: positions in, forces out
         host_ms = host["forces_positions_only"]["ms"]
+
+    moving = None
+    if not args.no_profile and not args.no_moving and walk_dev is None:
+        moving = moving_cells(w, dtype, potential)
 
     bstep = step_bytes(w.nc, w.M, w.N, esz, potential)
     kb = kernel_bytes(w.nc, w.M, w.N, esz, potential)
@@ -411,7 +576,16 @@ def main():
             "binning": ("two-pass (count, then sort) every step" if args.two_pass else
                         "one pass on the plan the previous step made from its counts "
                         "(the first step counts first)"),
+            "steps_on": ("the walk's positions, one resident set per step: step k adds "
+                         "N(0, 0.5 bin) per cell (seed k) to step k-1's positions"
+                         if walk_dev is not None else
+                         "the same resident positions every step"),
         },
+        "walk_overflow": walk_stats,
+        "moving_ms_per_step": moving["drift"]["ms_per_step"] if moving else None,
+        "overflow_records": (moving["drift"].get("overflow_records_mean")
+                             if moving else None),
+        "moving": moving,
         "hbm_fraction_step": round(bstep / (ms * 1e-3) / HBM_PEAK, 4),
         "step_bytes": bstep,
         "hbm_fraction_3pass_model": round(

@@ -96,6 +96,9 @@ struct dpep_ctx {
     int planned = 0;
     int scrub = 0;
     int par = 0;                 // parity of the next step's set of counts
+    int last_par = 0;            // parity of the last step's set of counts
+    int last_once = 0;           // the last step sorted in one pass
+    hipStream_t last_stream = nullptr;   // the stream the last step ran on
     // which of the context's own output buffers hold the last step's results
     // (kOut* bits): a step on caller-owned outputs leaves the others stale,
     // and new cells uploaded after the step make every output stale
@@ -138,7 +141,7 @@ static void release(dpep_ctx* c)
                     c->d_density, c->d_potential, c->d_fx, c->d_fy, c->d_gx,
                     c->d_gy, c->d_T, c->d_Ux, c->d_Uy, c->d_twM,
                     c->d_postM, c->d_twN, c->d_postN, b.cnt, b.xtot, b.pbase,
-                    b.pcap, b.pool_n, b.pstrip, b.items, b.nitems, b.done, b.recg,
+                    b.pcap, b.pool_n, b.ovst, b.oruns, b.items, b.nitems, b.done, b.recg,
                     b.recm, b.pos, b.gtmp,
                     b.bigflag, b.B, b.chunk, b.items_g, c->d_raw};
     for (void* p : bufs)
@@ -171,7 +174,7 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
         !b.xtot ||
         (nc > 0 && (!px || !py || !sx || !sy)) ||
         (gather && (!gx || !gy)) || !b.cnt || !b.pbase || !b.pcap ||
-        !b.pool_n || !b.pstrip || !b.items || !b.nitems || !b.done || !b.recg ||
+        !b.pool_n || !b.ovst || !b.oruns || !b.items || !b.nitems || !b.done || !b.recg ||
         !b.recm || !b.pos ||
         !b.gtmp || !b.bigflag || !b.B || !b.chunk || !b.items_g)
         return fail(DPEP_ERR_STATE, "internal: a kernel argument is NULL");
@@ -180,6 +183,7 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
     if (c->scrub) {
         HIP_TRY(hipMemsetAsync(b.xtot, 0, 2 * (size_t)kCountSlots * b.S * sizeof(unsigned), s));
         HIP_TRY(hipMemsetAsync(b.pool_n, 0, 2 * sizeof(unsigned), s));
+        HIP_TRY(hipMemsetAsync(b.ovst, 0, 2 * (size_t)b.S * sizeof(unsigned long long), s));
         c->scrub = 0;
     }
     // one pass over the cells when the previous step left its counts
@@ -215,6 +219,9 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
         HIP_TRY(hipEventRecord(pe[6], s));
     c->planned = 1;
     c->scrub = 0;
+    c->last_par = c->par;
+    c->last_once = once ? 1 : 0;
+    c->last_stream = s;
     c->par ^= 1;
     if (prof) HIP_TRY(hipEventRecord(pe[kNumStages], s));
     if (timed) HIP_TRY(hipEventRecord(c->ev[kNumStages], s));
@@ -285,7 +292,7 @@ int dpep_abi_version(void) { return DPEP_ABI_VERSION; }
 
 const char* dpep_build_info(void)
 {
-    return "dpep abi 5; HIP kernels for gfx950; scatter/P1/P2/P3/gather";
+    return "dpep abi 6; HIP kernels for gfx950; scatter/P1/P2/P3/gather";
 }
 
 const char* dpep_last_error(void) { return g_last_error.c_str(); }
@@ -371,7 +378,10 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
         b.pool0 = (unsigned)p.reg_cap;
         b.pool_cap = (unsigned)p.cap;
         const size_t nrec = p.reg_cap + p.cap;
-        HIP_TRY(hipMalloc((void**)&b.pstrip, p.cap * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.ovst, 2 * (size_t)p.S * sizeof(unsigned long long)));
+        HIP_TRY(hipMemset(b.ovst, 0, 2 * (size_t)p.S * sizeof(unsigned long long)));
+        b.rmax = run_capacity(nc_max);
+        HIP_TRY(hipMalloc((void**)&b.oruns, (size_t)p.S * b.rmax * sizeof(uint2)));
         HIP_TRY(hipMalloc((void**)&b.items, (size_t)b.Wacc * sizeof(uint4)));
         HIP_TRY(hipMalloc((void**)&b.items_g, (size_t)b.Wgat * sizeof(uint4)));
         HIP_TRY(hipMalloc((void**)&b.nitems, 2 * sizeof(unsigned)));
@@ -640,6 +650,31 @@ int dpep_get_timings(dpep_ctx* c, float* out)
     out[3] = c->d2h_den_ms;
     out[6] = c->d2h_out_ms;
     out[8] = c->h2d_ms + total + c->d2h_den_ms + c->d2h_out_ms;
+    return DPEP_OK;
+}
+
+int dpep_get_binning_stats(dpep_ctx* c, long long* out, int n)
+{
+    if (int rc = check_ctx(c)) return rc;
+    if (!out || n < 0) return fail(DPEP_ERR_ARG, "bad output buffer");
+    if (!c->stepped) return fail(DPEP_ERR_STATE, "no step has been computed");
+    HIP_TRY(hipStreamSynchronize(c->last_stream ? c->last_stream : c->stream));
+    const BinArgs& b = c->bins;
+    // the last step's set of counts and pool count stay until the next
+    // step's accumulation re-zeroes them
+    std::vector<unsigned> tot((size_t)kCountSlots * b.S);
+    unsigned pool = 0, items[2] = {0, 0}, chunk[2] = {0, 0};
+    HIP_TRY(hipMemcpy(tot.data(), b.xtot + (size_t)(c->last_par & 1) * kCountSlots * b.S,
+                      tot.size() * sizeof(unsigned), hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(&pool, b.pool_n + (c->last_par & 1), sizeof(unsigned),
+                      hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(items, b.nitems, sizeof items, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(chunk, b.chunk, sizeof chunk, hipMemcpyDeviceToHost));
+    long long recs = 0;
+    for (unsigned t : tot) recs += t;
+    const long long v[DPEP_NUM_BIN_STATS] = {c->last_once, recs, c->last_once ? (long long)pool : 0,
+                                             items[0], items[1], chunk[0], chunk[1]};
+    for (int i = 0; i < n; ++i) out[i] = i < DPEP_NUM_BIN_STATS ? v[i] : 0;
     return DPEP_OK;
 }
 

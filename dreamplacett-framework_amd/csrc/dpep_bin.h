@@ -19,8 +19,10 @@
 //   k_bin_fill_once  the steady state: K3 without K1, on regions   K3
 //                 sized from the previous step's counts; one equal
 //                 block of cells per workgroup (once_blocks); records
-//                 past a region's room -> overflow pool; tall cells
-//                 added to B by 16-thread teams at the block's end
+//                 past a region's room -> overflow pool, with their
+//                 strip (K4 and G1 pick their strip's pool records out
+//                 of it); tall cells added to B by 16-thread teams at
+//                 the block's end
 //   k_strip_acc   one work item = (strip, chunk): LDS accumulate,     K4
 //                 flush rho = D0 + tile (+B); the chunks of a split
 //                 strip add into B and the last one to finish flushes
@@ -549,6 +551,55 @@ __device__ __forceinline__ void item_range(const uint4& it, const StripMap& m,
     if (e1 < e0) e1 = e0;
 }
 
+// The per-strip overflow state of the step of parity par: [S] of
+// (runs << 32) | records.
+__device__ __forceinline__ unsigned long long* overflow_state(const BinArgs& b, int par)
+{
+    return b.ovst + (size_t)(par & 1) * b.S;
+}
+
+// Runs of a strip's overflow list that K4 and G1 stage in LDS at once.
+constexpr int kRunBatch = 1024;
+
+// fn(r) for every overflow-pool record r of strip s, by the kAccThreads
+// threads of the strip's first work item (chunk 0; the strip's other chunks
+// call nothing; every thread of the workgroup must call it).  The strip's
+// overflow list is the records a one-pass step found no room for in the
+// strip's regions: one run per K3 block that overflowed there, numbered in
+// the order of the runs' atomics, each run contiguous in the pool.  The run
+// table goes to LDS (lrun[kRunBatch], kRunBatch runs at a time) and each
+// thread takes records e = tid, tid + kAccThreads, ... of the list, finding
+// its run by a binary search of the runs' first numbers: every thread busy,
+// whatever the runs' lengths.  Empty on a counted step and on a placement
+// like the previous step's.
+template <typename Fn>
+__device__ __forceinline__ void for_overflow_records(const BinArgs& b, int s, const uint4& item,
+                                                     int tid, uint2* lrun, Fn&& fn)
+{
+    const unsigned long long st = overflow_state(b, b.par)[s];
+    const unsigned nr = (unsigned)(st >> 32), tot = (unsigned)st;
+    if (tot == 0u || (item.x >> 16) != 0u) return;     // uniform across the group
+    const unsigned nrun = nr < (unsigned)b.rmax ? nr : (unsigned)b.rmax;
+    const uint2* runs = b.oruns + (size_t)s * b.rmax;
+    for (unsigned k0 = 0; k0 < nrun; k0 += kRunBatch) {
+        const unsigned nb = min(nrun - k0, (unsigned)kRunBatch);
+        __syncthreads();                        // the previous batch is read
+        for (unsigned k = (unsigned)tid; k < nb; k += kAccThreads) lrun[k] = runs[k0 + k];
+        __syncthreads();
+        const unsigned v0 = lrun[0].y;
+        const unsigned v1 = k0 + nb < nrun ? runs[k0 + nb].y : tot;
+        for (unsigned e = v0 + (unsigned)tid; e < v1; e += kAccThreads) {
+            unsigned lo = 0u, hi = nb - 1u;     // the last run starting at or before e
+            while (lo < hi) {
+                const unsigned mid = (lo + hi + 1u) >> 1;
+                if (lrun[mid].y <= e) lo = mid;
+                else hi = mid - 1u;
+            }
+            fn(b.pool0 + lrun[lo].x + (e - lrun[lo].y));
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // K1: per-workgroup strip histogram, added into the slot totals.
 // LDS: hist[S].
@@ -924,10 +975,15 @@ __device__ __forceinline__ void scatter_tall_team(const vec4_t<T>& cell, int lan
 // atomic per strip it touches: the total is the next step's count), and
 // stores each record straight to its slot.  Records past the region's
 // capacity -- a strip that gained more than the slack -- go to the overflow
-// pool: their density into the side map B (device-scope atomics, the values
-// K4 would add) with the strip's column blocks marked, their gather by G1's
-// pool pass.  Every record is computed as in the fresh fill, so the results
-// do not depend on which records overflow.
+// pool with their strip number; K4 adds them into the strip's LDS tile and
+// G1 gathers them from the strip's rows in LDS like the strip's other
+// records (for_pool_records).  Every record is computed as in the fresh
+// fill, and each one's partial force is summed in the same order of row
+// groups, so the results do not depend on which records overflow.  (Adding
+// an overflow record's bins into the side map B with device-scope atomics,
+// as an earlier form did, cost 60 us at 1.1M cells when 3.5 % of the
+// records overflowed: those atomics execute beyond the XCD's L2, and the
+// overflow of a changed placement gathers on the strips that grew.)
 // Tall cells are listed as they are found (their index; the coordinates of
 // the first kTallList too) and added into B by teams of threads at the end
 // (scatter_tall_team), where no per-cell registers are live.
@@ -1037,75 +1093,72 @@ __global__ __launch_bounds__(kOnceThreads, (once_waves<T, CPT>())) void k_bin_fi
         }
     }
     __syncthreads();
-    // one run per strip: its place in the region, and how much of it fits
+    // one run per strip: its place in the region, and how much of it fits;
+    // cnt[s] <- the part that does not (ov records)
     for (int s = tid; s < S; s += NT) {
         const unsigned h = cnt[s];
+        unsigned ov = 0u;
         if (h) {
             const unsigned o = atomicAdd(&xrow[s], h);
             start[s] += o;
-            room[s] = room[s] > o ? room[s] - o : 0u;
+            const unsigned rm = room[s] > o ? room[s] - o : 0u;
+            room[s] = rm;
+            ov = h > rm ? h - rm : 0u;
+            if (ov) atomicAdd(&npool[0], ov);
         }
-    }
-    __syncthreads();
-    // records that fit: straight to their slot; the others (bit 2j / 2j + 1
-    // of ovm) take a place in this block's share of the pool: p = their rank
-    // in the block's overflow, resolved below
-    unsigned ovm = 0u;
-#pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-        if (s0v[j] < 0) continue;
-        if (r0[j] < room[s0v[j]]) {
-            p0[j] = start[s0v[j]] + r0[j];
-            recg[p0[j]] = geo[j];
-            b.recm[p0[j]] = m0[j];
-        } else {
-            p0[j] = atomicAdd(&npool[0], 1u);
-            ovm |= 1u << (2 * j);
-        }
-        if (s1v[j] >= 0) {
-            if (r1[j] < room[s1v[j]]) {
-                p1[j] = start[s1v[j]] + r1[j];
-                recg[p1[j]] = geo[j];
-                b.recm[p1[j]] = m1[j];
-            } else {
-                p1[j] = atomicAdd(&npool[0], 1u);
-                ovm |= 1u << (2 * j + 1);
-            }
-        }
+        cnt[s] = ov;
     }
     __syncthreads();
     const unsigned nover = npool[0];            // uniform across the group
     if (nover) {
+        // the block's overflow takes one range of the pool (one atomic),
+        // strip after strip; each strip's part is one run of that strip's
+        // overflow list (one 64-bit atomic gives the run its place in the
+        // list and its first record's number).  cnt[s] <- the pool index of
+        // the run's first record.
         if (tid == 0) npool[1] = atomicAdd(&b.pool_n[b.par & 1], nover);
+        const int per = (S + NT - 1) / NT;
+        const int q0 = min(tid * per, S), q1 = min(q0 + per, S);
+        unsigned run = 0u;
+        for (int s = q0; s < q1; ++s) run += cnt[s];
+        unsigned total;
+        unsigned off = block_exclusive_scan<NT>(run, tmp, total);   // barriers inside
+        off += npool[1];                        // written by thread 0 before them
+        unsigned long long* ost = overflow_state(b, b.par);
+        for (int s = q0; s < q1; ++s) {
+            const unsigned ov = cnt[s];
+            if (!ov) continue;
+            const unsigned long long old = atomicAdd(&ost[s], (1ull << 32) | ov);
+            const unsigned k = (unsigned)(old >> 32);
+            if (k < (unsigned)b.rmax)   // always: one run per block and strip
+                b.oruns[(size_t)s * b.rmax + k] = uint2{off, (unsigned)old};
+            cnt[s] = off;
+            off += ov;
+        }
         __syncthreads();
-        const unsigned pb = npool[1];
-        const T fs = (T)g.fix_scale;
-        const int CB = side_block(g.N);
-        auto place = [&](unsigned& p, int s, unsigned m, const vec4_t<T>& gm) {
-            const unsigned q = pb + p;          // index in the pool
-            if (q >= b.pool_cap) {      // cannot happen: the pool holds 2 nc
+    }
+    // every record to its slot: in its region if it fits, else in its
+    // strip's overflow run (rank past the room)
+    auto place = [&](unsigned& p, int s, unsigned r, unsigned m, const vec4_t<T>& gm) {
+        const unsigned rm = room[s];
+        if (r < rm) {
+            p = start[s] + r;
+        } else {
+            const unsigned q = cnt[s] + (r - rm);
+            if (q >= b.pool_cap) {          // cannot happen: the pool holds 2 nc
                 p = kPosNone;
                 return;
             }
             p = b.pool0 + q;
-            recg[p] = gm;
-            b.recm[p] = m;
-            b.pstrip[q] = (unsigned)s;
-            const int k0 = s << b.lgR;
-            record_density<T>(gm, m, k0, k0 + b.R - 1, g.stretch, fs,
-                              [&](int k, int col, unsigned long long v) {
-                                  atomicAdd(&Bm[(size_t)k * g.N + col], v);
-                              });
-            const SpanBox sb = span_of(m, k0);
-            side_mark(b.bigflag + (size_t)s * kSideWords, sb.byl, sb.byl + sb.ny, CB);
-        };
-        if (ovm) {
-#pragma unroll
-            for (int j = 0; j < CPT; ++j) {
-                if ((ovm >> (2 * j)) & 1u) place(p0[j], s0v[j], m0[j], geo[j]);
-                if ((ovm >> (2 * j + 1)) & 1u) place(p1[j], s1v[j], m1[j], geo[j]);
-            }
         }
+        recg[p] = gm;
+        b.recm[p] = m;
+    };
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        if (s0v[j] < 0) continue;
+        place(p0[j], s0v[j], r0[j], m0[j], geo[j]);
+        if (s1v[j] >= 0) place(p1[j], s1v[j], r1[j], m1[j], geo[j]);
     }
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
@@ -1213,7 +1266,9 @@ template <typename T, int L>
 __host__ __device__ constexpr size_t acc_lds_bytes()
 {
     constexpr int R = strip_rows(L);
-    const size_t tile = (size_t)R * L * sizeof(unsigned long long) + 16;
+    // the tile, the split-strip flag (16 bytes), the overflow run table
+    const size_t tile = (size_t)R * L * sizeof(unsigned long long) + 16 +
+                        (size_t)kRunBatch * sizeof(uint2);
     const size_t fft = (size_t)(R / 2) * lds_len(L) * sizeof(vec2_t<T>);
     return tile > fft ? tile : fft;
 }
@@ -1235,6 +1290,8 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     if (w == 0) {   // K3 has read the previous step's counts: zero them
         unsigned* old = counts_of(b, b.par ^ 1);
         for (int e = tid; e < kCountSlots * b.S; e += kAccThreads) old[e] = 0u;
+        unsigned long long* ost = overflow_state(b, b.par ^ 1);
+        for (int e = tid; e < b.S; e += kAccThreads) ost[e] = 0ull;
         if (tid == 0) b.pool_n[(b.par ^ 1) & 1] = 0u;
     }
     if (w >= (int)b.nitems[0]) return;          // uniform across the group
@@ -1273,6 +1330,15 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
         record_density<T>(rg, rm, k0, k1, g.stretch, fs,
                           [&](int k, int q, A v) { atomicAdd(&tile[(k - k0) * N + q], v); });
     }
+    // the strip's overflow list (records past their region's room), by the
+    // strip's first chunk, added into the tile like the others
+    for_overflow_records(b, s, item, tid, reinterpret_cast<uint2*>(tile + RN + 2),
+                         [&](unsigned r) {
+                             record_density<T>(recg[r], b.recm[r], k0, k1, g.stretch, fs,
+                                               [&](int k, int q, A v) {
+                                                   atomicAdd(&tile[(k - k0) * N + q], v);
+                                               });
+                         });
     __syncthreads();
 
     const size_t gbase = (size_t)k0 * N;
@@ -1463,14 +1529,17 @@ __host__ __device__ constexpr int gather_rows(int R, int N)
     return rg;
 }
 
-// A row of the two field maps from some column on, indexed like G1's LDS
-// pairs.
+// G1's LDS: the staged rows of both field maps, then the overflow run table.
 template <typename T>
-struct FieldRow {
-    const T* x;
-    const T* y;
-    __device__ __forceinline__ vec2_t<T> operator[](int q) const { return vec2_t<T>{x[q], y[q]}; }
-};
+__host__ __device__ constexpr size_t gather_lds_fields(int R, int N)
+{
+    return (size_t)gather_rows<T>(R, N) * N * 2 * sizeof(T);
+}
+template <typename T>
+__host__ __device__ constexpr size_t gather_lds(int R, int N)
+{
+    return gather_lds_fields<T>(R, N) + (size_t)kRunBatch * sizeof(uint2);
+}
 
 template <typename T, bool kGuess>
 __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
@@ -1500,8 +1569,10 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
         if (!kGuess || s != w) strip_map(b, s, sm);  // uniform across the group
         unsigned e0, e1;                        // this item's records
         item_range(item, sm, e0, e1);
-        // both fields of a bin side by side: one 2-element LDS read per bin
+        // both fields of a bin side by side: one 2-element LDS read per bin;
+        // then the overflow run table
         vec2_t<T>* lf = reinterpret_cast<vec2_t<T>*>(smem);
+        uint2* lrun = reinterpret_cast<uint2*>(smem + gather_lds_fields<T>(R, N));
         vec4_t<T> rg0{};
         unsigned rm0 = 0u, rn0 = 0u;
         if (e0 + tid < e1) {                    // the first record, before the rows
@@ -1574,33 +1645,20 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
                 }
                 out[r] = v;
             }
+            // the strip's overflow list, by the strip's first chunk, from
+            // the same rows in LDS and in the same order of row groups
+            for_overflow_records(b, s, item, tid, lrun, [&](unsigned r) {
+                vec2_t<T> v = record_partial<T>(
+                    recg[r], b.recm[r], k0, kg0, kg1, g.stretch, ba,
+                    [&](int k, int c) { return lf + (k - kg0) * N + c; });
+                if (!first) {
+                    const vec2_t<T> o = out[r];
+                    v.x += o.x;
+                    v.y += o.y;
+                }
+                out[r] = v;
+            });
         }
-    }
-    // the overflow pool (records past their region's capacity, rare): each
-    // record's partial over its strip's row groups straight from the field
-    // maps, in G1's order, grid-strided over every workgroup
-    const unsigned np = b.pool_n[b.par & 1];
-    for (unsigned p = (unsigned)w * kAccThreads + tid; p < np;
-         p += gridDim.x * kAccThreads) {
-        if (p >= b.pool_cap) break;
-        const unsigned r = b.pool0 + p;
-        const int k0 = (int)b.pstrip[p] * R;
-        const vec4_t<T> rg = recg[r];
-        const unsigned rm = b.recm[r];
-        vec2_t<T> v{};
-        for (int kg0 = k0; kg0 < k0 + R; kg0 += RG) {
-            vec2_t<T> u = record_partial<T>(
-                rg, rm, k0, kg0, kg0 + RG - 1, g.stretch, ba, [&](int k, int c) {
-                    const size_t o = (size_t)k * N + c;
-                    return FieldRow<T>{fx + o, fy + o};
-                });
-            if (kg0 != k0) {
-                u.x += v.x;
-                u.y += v.y;
-            }
-            v = u;
-        }
-        out[r] = v;
     }
 }
 

@@ -39,7 +39,10 @@ hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
     const OnceBlocks ob = once_blocks(nc, b.cus, sizeof(T));
     set_count_blocks(b, ob);
     if (b.R != strip_rows(g.N)) return hipErrorInvalidValue;   // the kernel's R
-    if (once && b.pool_cap < 2u * (unsigned)(nc > 0 ? nc : 0)) return hipErrorInvalidValue;
+    // a one-pass step needs an overflow pool for all its records and room in
+    // every strip's run table for one run per block
+    if (once && (b.pool_cap < 2u * (unsigned)(nc > 0 ? nc : 0) || ob.grid > b.rmax))
+        return hipErrorInvalidValue;
     hipError_t e;
     if (once) {
         if (ev && (e = hipEventRecord(ev[0], s))) return e;
@@ -84,7 +87,7 @@ hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
                              T* gx, T* gy, hipStream_t s, hipEvent_t ev)
 {
     if (nc <= 0) return ev ? hipEventRecord(ev, s) : hipSuccess;
-    const size_t lds = (size_t)gather_rows<T>(b.R, g.N) * g.N * 2 * sizeof(T);
+    const size_t lds = gather_lds<T>(b.R, g.N);
     if (b.Wgat == b.S)      // one workgroup per strip: item w is mostly strip w
         k_gather_bin<T, true><<<b.Wgat, kAccThreads, lds, s>>>(g, b, fx, fy);
     else
@@ -140,8 +143,7 @@ hipError_t bin_occupancy(int N, int R, int& acc_per_cu, int& gat_per_cu)
     });
     if (e) return e;
     return hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &gat_per_cu, (const void*)k_gather_bin<T, false>, kAccThreads,
-        (size_t)gather_rows<T>(R, N) * N * 2 * sizeof(T));
+        &gat_per_cu, (const void*)k_gather_bin<T, false>, kAccThreads, gather_lds<T>(R, N));
 }
 
 template <typename T>
@@ -170,13 +172,12 @@ static hipError_t prepare_bin_type()
                                        (int)fill_once_lds<T>(4096));
         });
     if (e) return e;
+    const int glds = (int)(kTileBytes + (size_t)kRunBatch * sizeof(uint2));
     if ((e = hipFuncSetAttribute((const void*)k_gather_bin<T, true>,
-                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 (int)kTileBytes)))
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, glds)))
         return e;
     return hipFuncSetAttribute((const void*)k_gather_bin<T, false>,
-                               hipFuncAttributeMaxDynamicSharedMemorySize,
-                               (int)kTileBytes);
+                               hipFuncAttributeMaxDynamicSharedMemorySize, glds);
 }
 
 hipError_t bin_prepare()

@@ -104,8 +104,10 @@ constexpr unsigned kRegionSlack = 16;
 //          exactly (none overflows);
 //   once   K3 alone: each region sized from the previous step's count of it
 //          plus slack; K3 reserves in the regions as it sorts, and records
-//          past a region's capacity go to the overflow pool (their density
-//          through the side map B).
+//          past a region's capacity go to the overflow pool: a block's part
+//          of a strip that does not fit is one run of that strip's overflow
+//          list (ovst, oruns), which K4 and G1 walk after the strip's
+//          regions.
 // The counts of a step stay for the next one: two sets, by step parity.
 // K4's workgroup 0 re-zeroes the older set (and its pool count) once K3 has
 // read it.
@@ -138,7 +140,15 @@ struct BinArgs {
     unsigned* nitems;       // [2] K4, G1 item counts
     uint4* items_g;         // [Wgat] G1 items (same layout)
     unsigned* pool_n;       // [2] overflow records of the step of each parity
-    unsigned* pstrip;       // [pool_cap] strip of each overflow record
+    unsigned long long* ovst;  // [2][S] per strip, the step of each parity:
+                               // (overflow runs << 32) | overflow records
+                               // (the older set zero again after K4)
+    uint2* oruns;           // [S][rmax] a strip's overflow runs, in the order
+                            // of its ovst atomics: {pool index of the run's
+                            // first record, that record's number in the
+                            // strip's overflow list}
+    int rmax;               // runs a strip's list holds: one per one-pass
+                            // block (run_capacity)
     unsigned* done;         // [S] K4 chunks done per strip (zero between steps)
     void* recg;             // [pool0 + pool_cap] record geometry, vec4 of T
     unsigned* recm;         // [pool0 + pool_cap] record span word
@@ -260,6 +270,15 @@ inline void set_item_grids(BinArgs& b, int acc_per_cu, int gat_per_cu, int cus)
 // 2048-cell blocks: 1.1 M float64 cells at 512^2 0.1062 -> 0.1002 ms).
 constexpr int kOnceMaxCpt = 5;
 constexpr int kOnceMinCells = kOnceThreads * 2;
+
+// Overflow runs a strip's list can hold: each one-pass block adds at most
+// one per strip, and a step of at most nc cells has at most
+// ceil(nc / kOnceMinCells) blocks (once_blocks).
+inline int run_capacity(long long nc_max)
+{
+    const long long nc = nc_max > 0 ? nc_max : 0;
+    return (int)(nc / kOnceMinCells + 2);
+}
 struct OnceBlocks {
     int grid;   // blocks (at least one)
     int q;      // cells per block (the last one may hold fewer)

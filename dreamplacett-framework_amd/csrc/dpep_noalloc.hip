@@ -70,14 +70,14 @@ struct Carve {
 };
 
 // The scratch layout of one call.  The regions that must start at zero (slot
-// totals, the overflow count, chunk tickets, side-map marks, the side map,
+// totals, the overflow counts, chunk tickets, side-map marks, the side map,
 // and the zero initial density when the caller passes none) come first, in
 // one run.  Every call counts before it sorts (no counts survive between
 // calls), so the records need no overflow pool.
 struct Layout {
-    size_t xtot, pool_n, done, bigflag, B, d0zero, zero_end;
+    size_t xtot, pool_n, ovst, done, bigflag, B, d0zero, zero_end;
     size_t twM, postM, twN, postN, T, Ux, Uy;
-    size_t cnt, pbase, pcap, pstrip, items, items_g, nitems, chunk;
+    size_t cnt, pbase, pcap, oruns, items, items_g, nitems, chunk;
     size_t recg, recm, pos, gtmp;
     size_t total;
 };
@@ -91,6 +91,7 @@ Layout plan_layout(int M, int N, int nc, size_t esz, const BinPlan& p, const Bin
     Layout l{};
     l.xtot = c.take(2 * (size_t)kCountSlots * p.S * sizeof(unsigned));
     l.pool_n = c.take(2 * sizeof(unsigned));
+    l.ovst = c.take(2 * (size_t)p.S * sizeof(unsigned long long));
     l.done = c.take((size_t)p.S * sizeof(unsigned));
     l.bigflag = c.take((size_t)kSideWords * p.S * sizeof(unsigned));
     l.B = c.take(mn * sizeof(unsigned long long));
@@ -106,7 +107,7 @@ Layout plan_layout(int M, int N, int nc, size_t esz, const BinPlan& p, const Bin
     l.cnt = c.take((size_t)p.G1max * p.S * sizeof(unsigned));
     l.pbase = c.take((size_t)kCountSlots * p.S * sizeof(unsigned));
     l.pcap = c.take((size_t)kCountSlots * p.S * sizeof(unsigned));
-    l.pstrip = c.take(sizeof(unsigned));
+    l.oruns = c.take(sizeof(uint2));
     l.items = c.take((size_t)b.Wacc * sizeof(uint4));
     l.items_g = c.take((size_t)b.Wgat * sizeof(uint4));
     l.nitems = c.take(2 * sizeof(unsigned));
@@ -179,7 +180,9 @@ int run(int M, int N, const Grid& g, int dtype, bool potential, bool gather, int
     b.pool_n = (unsigned*)(sc + l.pool_n);
     b.pbase = (unsigned*)(sc + l.pbase);
     b.pcap = (unsigned*)(sc + l.pcap);
-    b.pstrip = (unsigned*)(sc + l.pstrip);
+    b.ovst = (unsigned long long*)(sc + l.ovst);
+    b.oruns = (uint2*)(sc + l.oruns);
+    b.rmax = 1;
     b.reg_cap = (unsigned)p.cap;
     b.pool0 = (unsigned)p.cap;
     b.pool_cap = 0u;

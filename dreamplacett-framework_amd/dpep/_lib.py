@@ -38,6 +38,8 @@ OUTPUT_NAMES = ("density", "potential", "field_x", "field_y", "grad_x", "grad_y"
 NUM_TIMINGS = 9
 TIMING_KEYS = ("h2d", "scatter", "gather", "d2h_den", "upload", "compute",
                "download", "fw", "total")
+BIN_STATS_KEYS = ("one_pass", "records", "overflow_records", "acc_items", "gather_items",
+                  "acc_chunk", "gather_chunk")
 KERNEL_KEYS = ("bin_count", "bin_fill", "strip_acc", "col_pass", "row_inv",
                "gather_bin", "gather_out", "step")
 
@@ -69,6 +71,8 @@ _SIGNATURES = {
                                              ctypes.POINTER(ctypes.c_float),
                                              ctypes.c_int]),
     "dpep_set_profiling": (ctypes.c_int, [_vp, ctypes.c_int]),
+    "dpep_get_binning_stats": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_longlong),
+                                              ctypes.c_int]),
     "dpep_get_scatter_density": (ctypes.c_int, [_vp, _vp]),
     "dpep_host_alloc": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(_vp)]),
     "dpep_host_free": (ctypes.c_int, [_vp]),
@@ -90,7 +94,7 @@ class DpepError(RuntimeError):
 
 
 # DPEP_ABI_VERSION of include/dpep.h this binding is written against
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 def load_library(path: Optional[str] = None) -> ctypes.CDLL:
@@ -391,6 +395,16 @@ class Context:
         _check(self._lib.dpep_get_kernel_times(self.handle, buf, len(KERNEL_KEYS)),
                "dpep_get_kernel_times", self._lib)
         return dict(zip(KERNEL_KEYS, [float(v) for v in buf]))
+
+    def binning_stats(self) -> Dict[str, int]:
+        """How the last step binned its cells (waits for it): one_pass (1 if
+        it sorted on the previous step's plan), records, overflow_records
+        (records that went to the overflow pool), acc_items / gather_items
+        and acc_chunk / gather_chunk (work items and records per item)."""
+        buf = (ctypes.c_longlong * len(BIN_STATS_KEYS))()
+        _check(self._lib.dpep_get_binning_stats(self.handle, buf, len(BIN_STATS_KEYS)),
+               "dpep_get_binning_stats", self._lib)
+        return dict(zip(BIN_STATS_KEYS, [int(v) for v in buf]))
 
     def close(self) -> None:
         if self._h is not None:

@@ -241,6 +241,19 @@ def c5_displace(w: Workload, px: np.ndarray, py: np.ndarray, step: int):
     return nx.astype(np.float32), ny.astype(np.float32)
 
 
+def walk(w: Workload, steps: int, first: int = 0):
+    """Positions of `steps` consecutive steps of the seeded drift: step k's
+    positions are step k-1's (the placement's, for the first) plus
+    c5_displace with seed first + k.  Yields (step, px, py), float32.  The
+    100-step loop of the extreme-hotspot configuration is walk(config5(),
+    100); the same drift applied to another placement gives it cells that
+    move a fraction of a bin per step, as early placement iterations do."""
+    px, py = w.px, w.py
+    for k in range(steps):
+        px, py = c5_displace(w, px, py, first + k)
+        yield first + k, px, py
+
+
 CONFIGS = {1: config1, 2: config2, 3: config3, 4: config4, 5: config5}
 
 

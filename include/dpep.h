@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define DPEP_ABI_VERSION 5
+#define DPEP_ABI_VERSION 6
 
 /* status codes */
 #define DPEP_OK 0
@@ -231,6 +231,22 @@ int dpep_get_timings(dpep_ctx* ctx, float* out);
  * n = floats in out.  (ABI version 1 had one gather slot at [5] and the
  * step at [6].) */
 int dpep_get_kernel_times(dpep_ctx* ctx, float* out, int n);
+
+/* How the last step binned its cells (waits for it): n long longs of
+ * [0] 1 if it sorted in one pass on the plan the step before it made from
+ *     its counts, 0 if it counted first;
+ * [1] strip records of the step (a cell that is not taller than a strip
+ *     makes one record per strip it touches: one or two);
+ * [2] of them, records that found no room in their region and went to the
+ *     overflow pool (their density through device atomics; always 0 on a
+ *     counted step);
+ * [3] [4] work items of the strip accumulation and of the per-strip gather;
+ * [5] [6] records per work item of each (a strip above that is split).
+ * No counterpart in the reference (its routing dropped records past a page's
+ * capacity, kernels/v11_scatter_dm.cpp:235-246, and counted nothing); it
+ * shows what the one-pass binning costs when cells move between steps. */
+#define DPEP_NUM_BIN_STATS 7
+int dpep_get_binning_stats(dpep_ctx* ctx, long long* out, int n);
 
 /* slots > 0 enables per-kernel event timing for a ring of `slots` steps
  * (adds one event between launches); 0 disables (the default). */

@@ -169,7 +169,10 @@ static int run(int nc, bool det, bool pot, int ch, bool tall, bool force_stage, 
     b.reg_cap = (unsigned)p.reg_cap;
     b.pool0 = (unsigned)p.reg_cap;
     b.pool_cap = (unsigned)p.cap;
-    b.pstrip = exact<unsigned>(p.cap);
+    b.ovst = exact<unsigned long long>(2 * (size_t)p.S);
+    memset(b.ovst, 0, 2 * (size_t)p.S * sizeof(unsigned long long));
+    b.rmax = run_capacity(nc);
+    b.oruns = exact<uint2>((size_t)p.S * b.rmax);
     const size_t nrec = p.reg_cap + p.cap;
     b.items = exact<uint4>(b.Wacc);
     b.items_g = exact<uint4>(b.Wgat);
@@ -232,7 +235,7 @@ static int run(int nc, bool det, bool pot, int ch, bool tall, bool force_stage, 
             launch(grid, row_threads<T>(LN), shm, [&] { k_row_inv<T, LN, F>(a, Ux, Uy, fx, fy, phi); });
         }
         if (nc > 0) {
-            const size_t glds = (size_t)gather_rows<T>(p.R, N) * N * 2 * sizeof(T);
+            const size_t glds = gather_lds<T>(p.R, N);
             if (b.Wgat == b.S)       // as launch_bin_gather
                 launch(b.Wgat, kAccThreads, glds, [&] { k_gather_bin<T, true>(g, b, fx, fy); });
             else
@@ -250,6 +253,8 @@ static int run(int nc, bool det, bool pot, int ch, bool tall, bool force_stage, 
         for (size_t s2 = 0; s2 < nslot; ++s2)
             if (older[s2]) { fprintf(stderr, "previous counts left set\n"); return 4; }
         if (b.pool_n[b.par ^ 1]) { fprintf(stderr, "previous overflow count left set\n"); return 4; }
+        for (int s2 = 0; s2 < p.S; ++s2)
+            if (b.ovst[(size_t)(b.par ^ 1) * p.S + s2]) { fprintf(stderr, "previous overflow runs left set\n"); return 4; }
         b.par ^= 1;
         const unsigned char* Bb = (const unsigned char*)b.B;
         for (size_t i = 0; i < mn * 8; ++i)

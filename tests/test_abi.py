@@ -39,8 +39,8 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_info():
     import dpep
     lib = dpep.load_library()
-    assert lib.dpep_abi_version() == 5
-    assert b"abi 5" in lib.dpep_build_info()
+    assert lib.dpep_abi_version() == 6
+    assert b"abi 6" in lib.dpep_build_info()
     assert b"gfx950" in lib.dpep_build_info()
 
 

@@ -1,9 +1,10 @@
 """GPU: dpep_step_device_noalloc (the entry point that allocates nothing,
 its scratch in one device array of the library) against dpep_step_device on
 the same device buffers: two calls in a row, the second with fewer cells,
-float32 and float64; the density must match bit for bit (integer
-accumulation) and the fields, potential and forces to 1e-6 relative (the
-same kernels on the same inputs).  Also: a problem too large for the array
+float32 and float64; every output must match bit for bit: both run the
+same kernels on the same inputs, with the same device-built tables, and
+integer accumulation makes the density independent of the order records
+are placed in.  Also: a problem too large for the array
 is refused with its size, and a NULL initial density means zero."""
 import numpy as np
 import pytest
@@ -57,12 +58,11 @@ def test_noalloc_matches_step_device(oracle, dtype):
                 assert rc == 0, dpep.last_error()
                 db.sync()
                 a, b = fetch(oa, nc), fetch(ob, nc)
-                assert np.array_equal(a["density"], b["density"]), f"call {call}"
                 for k in OUTS:
-                    e = rel_l2(b[k], a[k])
-                    print(f"call {call} nc={nc} {k}: rel L2 vs step_device {e:.2e}",
+                    d = float(np.abs(b[k].astype(np.float64) - a[k]).max()) if nc else 0.0
+                    print(f"call {call} nc={nc} {k}: max |noalloc - step_device| {d:.3e}",
                           flush=True)
-                    assert e <= 1e-6, (call, k, e)
+                    assert np.array_equal(a[k], b[k]), (call, k, d)
                 if call == 1:
                     c = [np.asarray(v[:nc]) + (shift if i < 2 else 0)
                          for i, v in enumerate((px, py, sx, sy))]
