@@ -1094,7 +1094,9 @@ __global__ __launch_bounds__(kOnceThreads, (once_waves<T, CPT>())) void k_bin_fi
     }
     __syncthreads();
     // one run per strip: its place in the region, and how much of it fits;
-    // cnt[s] <- the part that does not (ov records)
+    // the part that does not (ov records) takes a block-local place in the
+    // block's overflow (an LDS atomic): cnt[s] <- that place << 16 | ov
+    // (both below 2 * kOnceThreads * kOnceMaxCpt < 2^16)
     for (int s = tid; s < S; s += NT) {
         const unsigned h = cnt[s];
         unsigned ov = 0u;
@@ -1104,36 +1106,31 @@ __global__ __launch_bounds__(kOnceThreads, (once_waves<T, CPT>())) void k_bin_fi
             const unsigned rm = room[s] > o ? room[s] - o : 0u;
             room[s] = rm;
             ov = h > rm ? h - rm : 0u;
-            if (ov) atomicAdd(&npool[0], ov);
         }
-        cnt[s] = ov;
+        cnt[s] = ov ? (atomicAdd(&npool[0], ov) << 16) | ov : 0u;
     }
     __syncthreads();
     const unsigned nover = npool[0];            // uniform across the group
     if (nover) {
-        // the block's overflow takes one range of the pool (one atomic),
-        // strip after strip; each strip's part is one run of that strip's
-        // overflow list (one 64-bit atomic gives the run its place in the
-        // list and its first record's number).  cnt[s] <- the pool index of
-        // the run's first record.
+        // the block's overflow takes one range of the pool (one atomic);
+        // each strip's part is one run of that strip's overflow list (one
+        // 64-bit atomic gives the run its place in the list and its first
+        // record's number).  cnt[s] <- the pool index of the run's first
+        // record.
         if (tid == 0) npool[1] = atomicAdd(&b.pool_n[b.par & 1], nover);
-        const int per = (S + NT - 1) / NT;
-        const int q0 = min(tid * per, S), q1 = min(q0 + per, S);
-        unsigned run = 0u;
-        for (int s = q0; s < q1; ++s) run += cnt[s];
-        unsigned total;
-        unsigned off = block_exclusive_scan<NT>(run, tmp, total);   // barriers inside
-        off += npool[1];                        // written by thread 0 before them
+        __syncthreads();
+        const unsigned pb = npool[1];
         unsigned long long* ost = overflow_state(b, b.par);
-        for (int s = q0; s < q1; ++s) {
-            const unsigned ov = cnt[s];
+        for (int s = tid; s < S; s += NT) {
+            const unsigned c = cnt[s];
+            const unsigned ov = c & 0xFFFFu;
             if (!ov) continue;
+            const unsigned q = pb + (c >> 16);
             const unsigned long long old = atomicAdd(&ost[s], (1ull << 32) | ov);
             const unsigned k = (unsigned)(old >> 32);
             if (k < (unsigned)b.rmax)   // always: one run per block and strip
-                b.oruns[(size_t)s * b.rmax + k] = uint2{off, (unsigned)old};
-            cnt[s] = off;
-            off += ov;
+                b.oruns[(size_t)s * b.rmax + k] = uint2{q, (unsigned)old};
+            cnt[s] = q;
         }
         __syncthreads();
     }

@@ -46,6 +46,18 @@ class PositionDump:
 
 
 def read_positions(path: str) -> PositionDump:
+    """A position dump: the servers' EXPORT_POS_PATH binary format, or a
+    DENSITY_AUDIT pos_iter####.npz (keys px, py, sx, sy, M, N, xl, yl, xh, yh,
+    as the reference's audit writes them, integration/scatter_ttnn_client.py
+    :136-140)."""
+    if path.endswith(".npz"):
+        with np.load(path, allow_pickle=False) as z:
+            px, py, sx, sy = (np.ascontiguousarray(z[k], np.float32)
+                              for k in ("px", "py", "sx", "sy"))
+            if not (px.size == py.size == sx.size == sy.size):
+                raise ValueError(f"{path}: cell arrays of different lengths")
+            return PositionDump(int(z["M"]), int(z["N"]), float(z["xl"]), float(z["yl"]),
+                                float(z["xh"]), float(z["yh"]), px, py, sx, sy)
     with open(path, "rb") as f:
         head = f.read(_HEAD.size)
         if len(head) != _HEAD.size:

@@ -244,6 +244,7 @@ class ScatterTTNNClient:
         if self.M and self.N and d.size != self.M * self.N:
             raise ValueError(f"initial density has {d.size} elements, expected "
                              f"{self.M * self.N}")
+        self._d0_sum = float(d.sum(dtype=np.float64))      # for DENSITY_AUDIT
         if self._ctx is not None:
             self._ctx.set_initial_density(d)
         elif self._mm is not None:
@@ -544,7 +545,7 @@ def make_forward(client: ScatterTTNNClient, keep_field_maps: bool = False,
             ctx.dpep_grad_x = out["grad_x"]
             ctx.dpep_grad_y = out["grad_y"]
         if "density" in out:
-            _density_audit(out["density"], sx, sy, client, iteration[0])
+            _density_audit(out["density"], px, py, sx, sy, client, iteration[0] - 1)
         ctx.pos = pos
         ctx.node_size_x_clamped = node_size_x_clamped
         ctx.node_size_y_clamped = node_size_y_clamped
@@ -611,26 +612,66 @@ def make_backward(original_backward=None):
     return staticmethod(_backward)
 
 
-def _density_audit(density, sx, sy, client, iteration) -> None:
-    """DENSITY_AUDIT=1: one CSV row per iteration with the GPU density's
-    integral (cells plus initial density, in area units), the cells' total
-    area beside it, and the density's peak, in DENSITY_AUDIT_DIR (default
-    <ipc_dir>/density_audit).  Positions are not dumped (EXPORT_POS_PATH
-    does that).  The reference's audit (:42-149) compared its TT density with
-    a CPU scatter of the same cells; this build's scatter is checked against
-    its float64 oracle by the tests instead, and the audit keeps to figures
-    the GPU output alone yields."""
+def _in_die_mass(px, py, sx, sy, xl, yl, xh, yh, bsx, bsy) -> float:
+    """The cells' density integral the step must produce when it is exact:
+    per cell, ratio * (area of its stretched rectangle inside the die), with
+    DREAMPlace's stretch to sqrt2 * bin (a closed form per cell, not a
+    density map)."""
+    px, py, sx, sy = (np.asarray(a, np.float64) for a in (px, py, sx, sy))
+    ok = np.isfinite(px) & np.isfinite(py) & np.isfinite(sx) & np.isfinite(sy) & \
+        (sx > 0) & (sy > 0)
+    w = np.maximum(sx, np.sqrt(2.0) * bsx)
+    h = np.maximum(sy, np.sqrt(2.0) * bsy)
+    x = px + 0.5 * (sx - w)
+    y = py + 0.5 * (sy - h)
+    ox = np.clip(np.minimum(x + w, xh) - np.maximum(x, xl), 0.0, None)
+    oy = np.clip(np.minimum(y + h, yh) - np.maximum(y, yl), 0.0, None)
+    with np.errstate(invalid="ignore"):
+        m = (sx * sy) / (w * h) * ox * oy
+    return float(np.sum(np.where(ok, m, 0.0)))
+
+
+def _density_audit(density, px, py, sx, sy, client, iteration) -> None:
+    """DENSITY_AUDIT=1: one CSV row per iteration in DENSITY_AUDIT_DIR
+    (default <ipc_dir>/density_audit): the cells' density integral (the GPU
+    density minus the initial density, in area units) against the in-die
+    mass of the cells computed in closed form from the same positions
+    (mass_deficit_pct), the density's sum and peak and the number of real
+    cells; and the positions of the first DENSITY_AUDIT_MAX_ITERS
+    iterations (default 700) as pos_iter####.npz with the reference's keys
+    (px, py, sx, sy, M, N, xl, yl, xh, yh), which dpep.replay reads.  The
+    reference's audit (integration/scatter_ttnn_client.py:42-149) also
+    scattered the cells on the CPU to compare maps; here the map is checked
+    against the float64 oracle by the tests (offline, on these dumps too),
+    and the library never computes a density on the CPU."""
     d = os.environ.get("DENSITY_AUDIT_DIR", os.path.join(client.ipc_dir, "density_audit"))
+    try:
+        max_iters = int(os.environ.get("DENSITY_AUDIT_MAX_ITERS", "700"))
+    except ValueError:
+        max_iters = 700
     os.makedirs(d, exist_ok=True)
     path = os.path.join(d, "density_audit.csv")
-    bin_area = ((client.xh - client.xl) / client.M) * ((client.yh - client.yl) / client.N)
-    mass = float(np.asarray(density, np.float64).sum() * bin_area)
-    cells = float(np.sum(np.asarray(sx, np.float64) * np.asarray(sy, np.float64)))
+    bsx = (client.xh - client.xl) / client.M
+    bsy = (client.yh - client.yl) / client.N
+    dens = np.asarray(density, np.float64)
+    cells_mass = float((dens.sum() - getattr(client, "_d0_sum", 0.0)) * bsx * bsy)
+    expect = _in_die_mass(px, py, sx, sy, client.xl, client.yl, client.xh, client.yh,
+                          bsx, bsy)
+    deficit = (1.0 - cells_mass / expect) * 100.0 if expect > 0 else 0.0
+    n_real = int(np.count_nonzero((np.asarray(sx) > 0) & (np.asarray(sy) > 0)))
     new = not os.path.exists(path)
     with open(path, "a") as f:
         if new:
-            f.write("iter,density_mass,cell_area,density_max\n")
-        f.write(f"{iteration},{mass:.9e},{cells:.9e},{float(np.max(density)):.6e}\n")
+            f.write("iter,mass_deficit_pct,cells_mass,in_die_mass,density_sum,"
+                    "density_max,n_real\n")
+        f.write(f"{iteration},{deficit:.6e},{cells_mass:.9e},{expect:.9e},"
+                f"{dens.sum():.9e},{dens.max():.6e},{n_real}\n")
+    if iteration < max_iters:
+        np.savez_compressed(os.path.join(d, f"pos_iter{iteration:04d}.npz"),
+                            px=np.asarray(px, np.float32), py=np.asarray(py, np.float32),
+                            sx=np.asarray(sx, np.float32), sy=np.asarray(sy, np.float32),
+                            M=client.M, N=client.N, xl=client.xl, yl=client.yl,
+                            xh=client.xh, yh=client.yh)
 
 
 def patch_dreamplace(container: str = "", ipc_dir: str = "/dev/shm/dpep_ipc",

@@ -317,6 +317,60 @@ def test_dreamplace_adapter_sends_the_sizes_once(tmp_path, oracle):
         client.stop()
 
 
+def test_density_audit_rows_and_position_dumps(tmp_path, oracle, monkeypatch):
+    """DENSITY_AUDIT=1 (reference :42-149): one CSV row per iteration whose
+    mass deficit is zero for an exact density (the loopback returns the
+    oracle's), with cells that stick out of the die counted by their in-die
+    part of the stretched rectangle; the first DENSITY_AUDIT_MAX_ITERS
+    iterations' positions as pos_iter####.npz, which dpep.replay reads back
+    bitwise."""
+    torch = pytest.importorskip("torch")
+    from dpep import replay
+    from dpep import scatter_ttnn_client as stc
+    import dreamplace_fakes as F
+
+    audit = tmp_path / "audit"
+    monkeypatch.setenv("DENSITY_AUDIT", "1")
+    monkeypatch.setenv("DENSITY_AUDIT_DIR", str(audit))
+    monkeypatch.setenv("DENSITY_AUDIT_MAX_ITERS", "1")
+    rng = np.random.default_rng(17)
+    mov, term, fil = _adapter_case(rng)
+    M = N = 16
+    die = (0.0, 0.0, 160.0, 160.0)
+    d0n = rng.uniform(0, 0.5, (M, N))
+    args, sel = F.forward_args(mov, term, fil, M, N, die, d0n)
+    client = _client(tmp_path, _w(0, len(sel), M), nc_max=len(sel))
+    fwd = stc.make_forward(client).__func__
+    n = args[0].numel() // 2
+    sent = []
+    try:
+        for it in range(2):
+            if it:
+                args[0].add_(torch.from_numpy(rng.uniform(-3, 3, 2 * n)))
+            pos = args[0].numpy().copy()
+            sent.append((pos[:n][sel], pos[n:][sel]))
+            fwd(F.Ctx(), *args)
+    finally:
+        client.stop()
+    sx, sy = (args[1] + 2 * args[3]).numpy()[sel], (args[2] + 2 * args[4]).numpy()[sel]
+    rows = open(audit / "density_audit.csv").read().strip().splitlines()
+    head = rows[0].split(",")
+    assert head[:2] == ["iter", "mass_deficit_pct"] and len(rows) == 3
+    for k, row in enumerate(rows[1:]):
+        v = dict(zip(head, row.split(",")))
+        assert int(v["iter"]) == k
+        assert abs(float(v["mass_deficit_pct"])) < 1e-3, v
+        # the closed-form in-die mass is the oracle density's integral
+        px, py = sent[k]
+        raw = oracle.density(px, py, sx, sy, M, N, *die)
+        assert float(v["in_die_mass"]) == pytest.approx(raw.sum() * 100.0, rel=1e-9)
+    assert sorted(p.name for p in audit.glob("pos_iter*.npz")) == ["pos_iter0000.npz"]
+    d = replay.read_positions(str(audit / "pos_iter0000.npz"))
+    assert (d.M, d.N, d.xh) == (M, N, 160.0)
+    assert np.array_equal(d.px, sent[0][0].astype(np.float32))
+    assert np.array_equal(d.sy, sy.astype(np.float32))
+
+
 def test_cpu_dct_mode(tmp_path, oracle, monkeypatch):
     """CPU_DCT=1 as in the reference (:804-829 client, :1757-1788 server):
     call() returns the cells' density without the initial density in
