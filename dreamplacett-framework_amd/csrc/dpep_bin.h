@@ -572,13 +572,22 @@ constexpr int kRunBatch = 1024;
 // its run by a binary search of the runs' first numbers: every thread busy,
 // whatever the runs' lengths.  Empty on a counted step and on a placement
 // like the previous step's.
+// The step's pool count is read first, after the strip's own records: one
+// word every workgroup reads (an L2 hit after the first), zero unless the
+// step overflowed; only then the strip's overflow_state entry.  (Each
+// workgroup reading its strip's entry on every step, an address K3's
+// device-scope atomics leave outside the L2, cost G1 1.3 us at 2M cells on
+// 4096 x 4096; loaded with the work item and held across the record loop,
+// 9 us; a flag derived from the strip map instead, 8 us: it changed how the
+// compiler schedules G1's first loads.)
 template <typename Fn>
 __device__ __forceinline__ void for_overflow_records(const BinArgs& b, int s, const uint4& item,
                                                      int tid, uint2* lrun, Fn&& fn)
 {
+    if (b.pool_n[b.par & 1] == 0u || (item.x >> 16) != 0u) return;   // uniform
     const unsigned long long st = overflow_state(b, b.par)[s];
     const unsigned nr = (unsigned)(st >> 32), tot = (unsigned)st;
-    if (tot == 0u || (item.x >> 16) != 0u) return;     // uniform across the group
+    if (tot == 0u) return;                              // uniform across the group
     const unsigned nrun = nr < (unsigned)b.rmax ? nr : (unsigned)b.rmax;
     const uint2* runs = b.oruns + (size_t)s * b.rmax;
     for (unsigned k0 = 0; k0 < nrun; k0 += kRunBatch) {
@@ -977,7 +986,7 @@ __device__ __forceinline__ void scatter_tall_team(const vec4_t<T>& cell, int lan
 // capacity -- a strip that gained more than the slack -- go to the overflow
 // pool with their strip number; K4 adds them into the strip's LDS tile and
 // G1 gathers them from the strip's rows in LDS like the strip's other
-// records (for_pool_records).  Every record is computed as in the fresh
+// records (for_overflow_records).  Every record is computed as in the fresh
 // fill, and each one's partial force is summed in the same order of row
 // groups, so the results do not depend on which records overflow.  (Adding
 // an overflow record's bins into the side map B with device-scope atomics,
@@ -1110,13 +1119,40 @@ __global__ __launch_bounds__(kOnceThreads, (once_waves<T, CPT>())) void k_bin_fi
         cnt[s] = ov ? (atomicAdd(&npool[0], ov) << 16) | ov : 0u;
     }
     __syncthreads();
+    // records that fit: straight to their slot; the others (bit 2j / 2j + 1
+    // of ovm) are placed below, once the block's overflow has its range
+    unsigned ovm = 0u;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        if (s0v[j] < 0) continue;
+        if (r0[j] < room[s0v[j]]) {
+            p0[j] = start[s0v[j]] + r0[j];
+            recg[p0[j]] = geo[j];
+            b.recm[p0[j]] = m0[j];
+        } else {
+            p0[j] = r0[j] - room[s0v[j]];       // its place in the strip's run
+            ovm |= 1u << (2 * j);
+        }
+        if (s1v[j] >= 0) {
+            if (r1[j] < room[s1v[j]]) {
+                p1[j] = start[s1v[j]] + r1[j];
+                recg[p1[j]] = geo[j];
+                b.recm[p1[j]] = m1[j];
+            } else {
+                p1[j] = r1[j] - room[s1v[j]];
+                ovm |= 1u << (2 * j + 1);
+            }
+        }
+    }
+    __syncthreads();
     const unsigned nover = npool[0];            // uniform across the group
     if (nover) {
         // the block's overflow takes one range of the pool (one atomic);
         // each strip's part is one run of that strip's overflow list (one
         // 64-bit atomic gives the run its place in the list and its first
         // record's number).  cnt[s] <- the pool index of the run's first
-        // record.
+        // record; a record's place in its run (in p0 / p1) is its rank past
+        // the room.
         if (tid == 0) npool[1] = atomicAdd(&b.pool_n[b.par & 1], nover);
         __syncthreads();
         const unsigned pb = npool[1];
@@ -1133,29 +1169,23 @@ __global__ __launch_bounds__(kOnceThreads, (once_waves<T, CPT>())) void k_bin_fi
             cnt[s] = q;
         }
         __syncthreads();
-    }
-    // every record to its slot: in its region if it fits, else in its
-    // strip's overflow run (rank past the room)
-    auto place = [&](unsigned& p, int s, unsigned r, unsigned m, const vec4_t<T>& gm) {
-        const unsigned rm = room[s];
-        if (r < rm) {
-            p = start[s] + r;
-        } else {
-            const unsigned q = cnt[s] + (r - rm);
-            if (q >= b.pool_cap) {          // cannot happen: the pool holds 2 nc
+        auto place = [&](unsigned& p, int s, unsigned m, const vec4_t<T>& gm) {
+            const unsigned q = cnt[s] + p;
+            if (q >= b.pool_cap) {      // cannot happen: the pool holds 2 nc
                 p = kPosNone;
                 return;
             }
             p = b.pool0 + q;
-        }
-        recg[p] = gm;
-        b.recm[p] = m;
-    };
+            recg[p] = gm;
+            b.recm[p] = m;
+        };
+        if (ovm) {
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-        if (s0v[j] < 0) continue;
-        place(p0[j], s0v[j], r0[j], m0[j], geo[j]);
-        if (s1v[j] >= 0) place(p1[j], s1v[j], r1[j], m1[j], geo[j]);
+            for (int j = 0; j < CPT; ++j) {
+                if ((ovm >> (2 * j)) & 1u) place(p0[j], s0v[j], m0[j], geo[j]);
+                if ((ovm >> (2 * j + 1)) & 1u) place(p1[j], s1v[j], m1[j], geo[j]);
+            }
+        }
     }
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
