@@ -663,17 +663,22 @@ int dpep_get_binning_stats(dpep_ctx* c, long long* out, int n)
     // the last step's set of counts and pool count stay until the next
     // step's accumulation re-zeroes them
     std::vector<unsigned> tot((size_t)kCountSlots * b.S);
+    std::vector<unsigned long long> ost((size_t)b.S);
     unsigned pool = 0, items[2] = {0, 0}, chunk[2] = {0, 0};
     HIP_TRY(hipMemcpy(tot.data(), b.xtot + (size_t)(c->last_par & 1) * kCountSlots * b.S,
                       tot.size() * sizeof(unsigned), hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(ost.data(), b.ovst + (size_t)(c->last_par & 1) * b.S,
+                      ost.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost));
     HIP_TRY(hipMemcpy(&pool, b.pool_n + (c->last_par & 1), sizeof(unsigned),
                       hipMemcpyDeviceToHost));
     HIP_TRY(hipMemcpy(items, b.nitems, sizeof items, hipMemcpyDeviceToHost));
     HIP_TRY(hipMemcpy(chunk, b.chunk, sizeof chunk, hipMemcpyDeviceToHost));
-    long long recs = 0;
+    long long recs = 0, runs = 0;
     for (unsigned t : tot) recs += t;
+    for (unsigned long long o : ost) runs = (long long)(o >> 32) > runs ? (long long)(o >> 32) : runs;
     const long long v[DPEP_NUM_BIN_STATS] = {c->last_once, recs, c->last_once ? (long long)pool : 0,
-                                             items[0], items[1], chunk[0], chunk[1]};
+                                             items[0], items[1], chunk[0], chunk[1],
+                                             c->last_once ? runs : 0};
     for (int i = 0; i < n; ++i) out[i] = i < DPEP_NUM_BIN_STATS ? v[i] : 0;
     return DPEP_OK;
 }

@@ -39,7 +39,7 @@ NUM_TIMINGS = 9
 TIMING_KEYS = ("h2d", "scatter", "gather", "d2h_den", "upload", "compute",
                "download", "fw", "total")
 BIN_STATS_KEYS = ("one_pass", "records", "overflow_records", "acc_items", "gather_items",
-                  "acc_chunk", "gather_chunk")
+                  "acc_chunk", "gather_chunk", "overflow_runs_max")
 KERNEL_KEYS = ("bin_count", "bin_fill", "strip_acc", "col_pass", "row_inv",
                "gather_bin", "gather_out", "step")
 
@@ -400,7 +400,8 @@ class Context:
         """How the last step binned its cells (waits for it): one_pass (1 if
         it sorted on the previous step's plan), records, overflow_records
         (records that went to the overflow pool), acc_items / gather_items
-        and acc_chunk / gather_chunk (work items and records per item)."""
+        and acc_chunk / gather_chunk (work items and records per item),
+        overflow_runs_max (the most overflow runs one strip received)."""
         buf = (ctypes.c_longlong * len(BIN_STATS_KEYS))()
         _check(self._lib.dpep_get_binning_stats(self.handle, buf, len(BIN_STATS_KEYS)),
                "dpep_get_binning_stats", self._lib)

@@ -241,11 +241,13 @@ int dpep_get_kernel_times(dpep_ctx* ctx, float* out, int n);
  *     overflow pool (their density through device atomics; always 0 on a
  *     counted step);
  * [3] [4] work items of the strip accumulation and of the per-strip gather;
- * [5] [6] records per work item of each (a strip above that is split).
+ * [5] [6] records per work item of each (a strip above that is split);
+ * [7] the most overflow runs one strip received (one per block of cells
+ *     that overflowed there).
  * No counterpart in the reference (its routing dropped records past a page's
  * capacity, kernels/v11_scatter_dm.cpp:235-246, and counted nothing); it
  * shows what the one-pass binning costs when cells move between steps. */
-#define DPEP_NUM_BIN_STATS 7
+#define DPEP_NUM_BIN_STATS 8
 int dpep_get_binning_stats(dpep_ctx* ctx, long long* out, int n);
 
 /* slots > 0 enables per-kernel event timing for a ring of `slots` steps

@@ -188,11 +188,11 @@ def test_one_pass_overflow_matches_counted_step(oracle, grid, dtype):
     """A context stepped on one placement, then on a very different one:
     the one-pass sort of the second placement runs out of room in most
     strips (the room was planned for the first), so most of its records go
-    through the overflow pool (their density by device atomics into the side
-    map, their gather from the field maps).  Its outputs must equal, bitwise,
-    those of a context that counts first (DPEP_FLAG_TWO_PASS), and the
-    oracle's; a third step (planned from the second's counts) overflows no
-    more and gives the same again."""
+    to their strips' overflow lists (added into the strip tiles and gathered
+    from the staged field rows after the strips' own records).  Its outputs
+    must equal, bitwise, those of a context that counts first
+    (DPEP_FLAG_TWO_PASS), and the oracle's; a third step (planned from the
+    second's counts) overflows no more and gives the same again."""
     import dpep
     from dpep import workloads
     b = workloads.small(5, seed=22, cells=60000, grid=grid)     # one hot square
@@ -204,7 +204,10 @@ def test_one_pass_overflow_matches_counted_step(oracle, grid, dtype):
         ctx.set_initial_density(b.d0n.astype(dtype))
         ctx.step(*ca)
         over = ctx.step(*cb)
+        st = ctx.binning_stats()
         again = ctx.step(*cb)
+        assert ctx.binning_stats()["overflow_records"] == 0
+    assert st["one_pass"] == 1 and st["overflow_records"] > st["records"] // 4, st
     with dpep.Context(b.M, b.N, b.nc, b.xl, b.yl, b.xh, b.yh, dtype=dtype,
                       two_pass=True) as ctx:
         ctx.set_initial_density(b.d0n.astype(dtype))
