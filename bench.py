@@ -388,7 +388,8 @@ def cpu_baseline(w, seconds, max_steps=400):
     cb = pyoracle.CpuBaseline(w.M, w.N, w.xl, w.yl, w.xh, w.yh)
     px, py, sx, sy = w.cells(np.float32)
     d0 = w.d0n.astype(np.float32)
-    cb.step(px, py, sx, sy, d0)                     # warm-up
+    for _ in range(3):                              # warm-up steps
+        cb.step(px, py, sx, sy, d0)
     times, stages = [], []
     t_start = time.perf_counter()
     while len(times) < max_steps and (time.perf_counter() - t_start) < seconds:
@@ -405,7 +406,7 @@ def cpu_baseline(w, seconds, max_steps=400):
         "cores": pyoracle.CpuBaseline.threads(),
         "kind": "port",
         "sample": (f"{len(times)} full steps of the same workload "
-                   f"({w.nc} cells, {w.M}x{w.N}) after 1 warm-up, median; "
+                   f"({w.nc} cells, {w.M}x{w.N}) after 3 warm-ups, median; "
                    f"float32 OpenMP scatter + FFT DCT + gather"),
         "stage_ms": {k: round(v, 3) for k, v in st.items()},
     }
