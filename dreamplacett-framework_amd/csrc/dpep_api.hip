@@ -389,7 +389,7 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
         HIP_TRY(hipMalloc((void**)&b.done, (size_t)p.S * sizeof(unsigned)));
         HIP_TRY(hipMemset(b.done, 0, (size_t)p.S * sizeof(unsigned)));
         HIP_TRY(hipMalloc(&b.recg, nrec * p.geo_bytes));
-        HIP_TRY(hipMalloc((void**)&b.recm, nrec * sizeof(unsigned)));
+        HIP_TRY(hipMalloc((void**)&b.recm, (p.span_bytes ? nrec : 1) * sizeof(unsigned)));
         HIP_TRY(hipMalloc((void**)&b.pos, (size_t)(nc_max > 0 ? nc_max : 1) * sizeof(unsigned long long)));
         HIP_TRY(hipMalloc(&b.gtmp, nrec * 2 * c->esz));
         HIP_TRY(hipMalloc((void**)&b.bigflag, (size_t)kSideWords * p.S * sizeof(unsigned)));

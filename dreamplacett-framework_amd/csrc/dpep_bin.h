@@ -42,10 +42,11 @@
 // runs about seven times faster than ds_add_f32.)
 //
 // K3 evaluates each cell's stretch and span once, in float64, and stores a
-// 20-byte record (structure of arrays): geometry in bin units relative to
-// the edges of its first bin (offsets dx, dy of the stretched corner, in
-// [0, 1), and the cell's original extents w, h, from which K4 and G1 re-derive
-// the stretched extents and the area ratio), and one span word.  Short
+// record: geometry in bin units relative to the edges of its first bin
+// (offsets dx, dy of the stretched corner, in [0, 1), and the cell's
+// original extents w, h, from which K4 and G1 re-derive the stretched
+// extents and the area ratio) and its first row and column (16 bytes in
+// one word at float32, rec_geo; a double4 plus a span word at float64).  Short
 // arithmetic on small numbers, which float32 carries to ~1e-7 of a bin
 // (absolute die coordinates would not).  K3 also writes pos[i] (both slots),
 // the records of cell i (in cell order, coalesced), so G2 can write the
@@ -114,6 +115,124 @@ __device__ __forceinline__ void stretch_of(const vec4_t<T>& r, int stretch, T& x
     yr = r.y + hc;
 }
 
+// ---------------------------------------------------------------------------
+// Stored records.  float64: the geometry (dx, dy, w, h) as a double4 in recg
+// and the span word in recm.  float32: one 16-byte word per record in recg
+// (recm unused).  dx and dy, the offsets of the stretched corner from its
+// first bin's edges in [0, 1), are kept as the 23-bit mantissas of the
+// floats 1 + dx and 1 + dy, whose sign and exponent bits are always the same
+// and so carry the rest: the row offset rel (4 bits) and byl (13 bits, 5 in
+// the dx word and 8 in the dy word); w and h are plain float32.  Decoding an
+// offset is one AND-OR and one subtraction (precision 2^-23 of a bin); the
+// row and column counts are derived from the geometry (rec_view).  One
+// aligned 16-byte store per record in K3 and one load in K4 and G1, where
+// the 20-byte form took two of each into two arrays.  A cell whose stretched
+// corner lies below the die's lower x or y edge (a negative offset) takes
+// the tall path instead (cell_strips).
+// ---------------------------------------------------------------------------
+constexpr unsigned kOffMant = 0x007FFFFFu;     // mantissa bits of 1 + offset
+constexpr unsigned kOne = 0x3F800000u;         // the bits of 1.0f
+
+template <typename T>
+__device__ __forceinline__ vec4_t<T> rec_geo(double ex, double ey, double wb, double hb, int byl)
+{
+    if constexpr (sizeof(T) == 4) {
+        auto mant = [](double e) -> unsigned {
+            const double v = e * 8388608.0 + 0.5;
+            return v <= 0.0 ? 0u : (v >= 8388607.0 ? kOffMant : (unsigned)v);
+        };
+        const unsigned ub = (unsigned)byl;
+        float4 r;
+        r.x = __uint_as_float(mant(ex) | ((ub & 0x1Fu) << 27));
+        r.y = __uint_as_float(mant(ey) | (((ub >> 5) & 0xFFu) << 23));
+        r.z = (float)wb;
+        r.w = (float)hb;
+        return r;
+    } else {
+        return vec4_t<T>{(T)ex, (T)ey, (T)wb, (T)hb};
+    }
+}
+
+// The per-record part of a record in strip s (rel = bxl - s * R): the span
+// word (float64), or rel in 4 bits (float32), merged by rec_put.
+template <typename T>
+__device__ __forceinline__ unsigned rec_span(int rel, int nx, int ny, int byl)
+{
+    if constexpr (sizeof(T) == 4) return (unsigned)rel & 0xFu;
+    else return span_word(rel, nx, ny, byl);
+}
+
+template <typename T>
+__device__ __forceinline__ void rec_put(const BinArgs& b, vec4_t<T>* recg, unsigned p,
+                                        const vec4_t<T>& geo, unsigned m)
+{
+    if constexpr (sizeof(T) == 4) {
+        float4 r = geo;
+        r.x = __uint_as_float(__float_as_uint(r.x) | (m << 23));
+        recg[p] = r;
+    } else {
+        recg[p] = geo;
+        b.recm[p] = m;
+    }
+}
+
+// The span word of record r (float64; float32 records carry it in recg).
+template <typename T>
+__device__ __forceinline__ unsigned rec_m(const BinArgs& b, unsigned r)
+{
+    if constexpr (sizeof(T) == 4) return 0u;
+    else return b.recm[r];
+}
+
+// A record in the frame of its strip (first row k0): offsets dx, dy, far
+// edges xr = dx + stretched w and yr, area ratio, first row and column,
+// rows and columns past them (nx not clamped to the strip: callers clamp
+// to their rows; ny clamped to the grid's N columns).
+template <typename T>
+struct RecView {
+    T dx, dy, xr, yr, rat;
+    int bxl, nx, byl, ny;
+};
+
+template <typename T>
+__device__ __forceinline__ RecView<T> rec_view(const vec4_t<T>& rg, unsigned rm, int k0,
+                                               int stretch, int N)
+{
+    RecView<T> v;
+    if constexpr (sizeof(T) == 4) {
+        const unsigned ux = __float_as_uint(rg.x), uy = __float_as_uint(rg.y);
+        v.dx = __uint_as_float((ux & kOffMant) | kOne) - 1.f;
+        v.dy = __uint_as_float((uy & kOffMant) | kOne) - 1.f;
+        v.bxl = k0 + (((int)(ux << 5)) >> 28);
+        v.byl = (int)((ux >> 27) | (((uy >> 23) & 0xFFu) << 5));
+        const float w = rg.z, h = rg.w;
+        float wc = w, hc = h;
+        v.rat = 1.f;
+        if (stretch) {
+            const float m = 1.41421356237309504880f;
+            wc = w > m ? w : m;
+            hc = h > m ? h : m;
+            v.rat = (w * h) * fast_rcp(wc * hc);
+        }
+        v.xr = v.dx + wc;
+        v.yr = v.dy + hc;
+        // a row or column past the cell's far edge adds nothing (its overlap
+        // is not positive), so counting from the rounded edge is safe
+        v.nx = (int)v.xr;
+        v.ny = min((int)v.yr, N - 1 - v.byl);
+    } else {
+        const SpanBox sb = span_of(rm, k0);
+        stretch_of<T>(rg, stretch, v.xr, v.yr, v.rat);
+        v.dx = rg.x;
+        v.dy = rg.y;
+        v.bxl = sb.bxl;
+        v.nx = sb.nx;
+        v.byl = sb.byl;
+        v.ny = sb.ny;
+    }
+    return v;
+}
+
 constexpr unsigned kPosTall = 0xFFFFFFFFu;     // record slot: tall cell (side map)
 constexpr unsigned kPosNone = 0xFFFFFFFEu;     // record slot: none
 
@@ -143,11 +262,16 @@ __device__ __forceinline__ unsigned long long pos_pair(unsigned p0, unsigned p1)
     return (unsigned long long)p0 | ((unsigned long long)p1 << 32);
 }
 
-// Strips [s0, s1] a cell occupies and whether it takes the tall path.
-__device__ __forceinline__ void cell_strips(const CellSpan& c, int R, int lgR,
+// Strips [s0, s1] a cell occupies and whether it takes the tall path: more
+// rows than a strip, more than kMaxSpanY + 1 columns, or (float32 records,
+// which hold non-negative offsets only) a stretched corner below the die's
+// lower x or y edge.
+template <typename T>
+__device__ __forceinline__ void cell_strips(const CellSpan& c, const Grid& g, int R, int lgR,
                                             int& s0, int& s1, bool& tall)
 {
     tall = (c.bxh - c.bxl + 1) > R || (c.byh - c.byl) > kMaxSpanY;
+    if constexpr (sizeof(T) == 4) tall = tall || c.x < g.xl || c.y < g.yl;
     s0 = c.bxl >> lgR;
     s1 = c.bxh >> lgR;
 }
@@ -636,7 +760,7 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_count(
             continue;
         int s0, s1;
         bool tall;
-        cell_strips(c, b.R, b.lgR, s0, s1, tall);
+        cell_strips<T>(c, g, b.R, b.lgR, s0, s1, tall);
         if (tall) continue;
         atomicAdd(&hist[s0], 1u);
         if (s1 != s0) atomicAdd(&hist[s1], 1u);
@@ -689,7 +813,7 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill_direct(
         }
         int s0, s1;
         bool tall;
-        cell_strips(c, b.R, b.lgR, s0, s1, tall);
+        cell_strips<T>(c, g, b.R, b.lgR, s0, s1, tall);
         if (tall) {
             const double sc = c.ratio() * g.inv_ba;
             for (int k = c.bxl; k <= c.bxh; ++k) {
@@ -713,17 +837,15 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill_direct(
         // strip-relative record, evaluated in float64 and rounded once
         const double ex = (c.x - (g.xl + c.bxl * g.bsx)) * g.inv_bsx;
         const double ey = (c.y - (g.yl + c.byl * g.bsy)) * g.inv_bsy;
-        const vec4_t<T> geo = {(T)ex, (T)ey, (T)((double)cw[j] * g.inv_bsx),
-                               (T)((double)chh[j] * g.inv_bsy)};
+        const vec4_t<T> geo = rec_geo<T>(ex, ey, (double)cw[j] * g.inv_bsx,
+                                         (double)chh[j] * g.inv_bsy, c.byl);
         const int nx = c.bxh - c.bxl, ny = c.byh - c.byl;
         const unsigned p0 = atomicAdd(&cur[s0], 1u);
-        recg[p0] = geo;
-        b.recm[p0] = span_word(c.bxl - (s0 << b.lgR), nx, ny, c.byl);
+        rec_put<T>(b, recg, p0, geo, rec_span<T>(c.bxl - (s0 << b.lgR), nx, ny, c.byl));
         unsigned p1 = kPosNone;
         if (s1 != s0) {
             p1 = atomicAdd(&cur[s1], 1u);
-            recg[p1] = geo;
-            b.recm[p1] = span_word(c.bxl - (s1 << b.lgR), nx, ny, c.byl);
+            rec_put<T>(b, recg, p1, geo, rec_span<T>(c.bxl - (s1 << b.lgR), nx, ny, c.byl));
         }
         b.pos[i] = pos_pair(p0, p1);
     }
@@ -807,7 +929,7 @@ __global__ __launch_bounds__(kBinThreads, 5) void k_bin_fill_staged(
         }
         int s0, s1;
         bool tall;
-        cell_strips(c, b.R, b.lgR, s0, s1, tall);
+        cell_strips<T>(c, g, b.R, b.lgR, s0, s1, tall);
         if (tall) {
             const double sc = c.ratio() * g.inv_ba;
             for (int k = c.bxl; k <= c.bxh; ++k) {
@@ -831,15 +953,15 @@ __global__ __launch_bounds__(kBinThreads, 5) void k_bin_fill_staged(
         // strip-relative record, evaluated in float64 and rounded once
         const double ex = (c.x - (g.xl + c.bxl * g.bsx)) * g.inv_bsx;
         const double ey = (c.y - (g.yl + c.byl * g.bsy)) * g.inv_bsy;
-        geo[j] = {(T)ex, (T)ey, (T)((double)cw[j] * g.inv_bsx),
-                  (T)((double)chh[j] * g.inv_bsy)};
+        geo[j] = rec_geo<T>(ex, ey, (double)cw[j] * g.inv_bsx, (double)chh[j] * g.inv_bsy,
+                            c.byl);
         const int nx = c.bxh - c.bxl, ny = c.byh - c.byl;
         s0v[j] = s0;
-        m0[j] = span_word(c.bxl - (s0 << b.lgR), nx, ny, c.byl);
+        m0[j] = rec_span<T>(c.bxl - (s0 << b.lgR), nx, ny, c.byl);
         r0[j] = atomicAdd(&cnt[s0], 1u);
         if (s1 != s0) {
             s1v[j] = s1;
-            m1[j] = span_word(c.bxl - (s1 << b.lgR), nx, ny, c.byl);
+            m1[j] = rec_span<T>(c.bxl - (s1 << b.lgR), nx, ny, c.byl);
             r1[j] = atomicAdd(&cnt[s1], 1u);
         }
     }
@@ -868,8 +990,7 @@ __global__ __launch_bounds__(kBinThreads, 5) void k_bin_fill_staged(
             sg[k0] = geo[j];
             sm[k0] = m0[j];
         } else {
-            recg[d0] = geo[j];
-            b.recm[d0] = m0[j];
+            rec_put<T>(b, recg, d0, geo[j], m0[j]);
         }
         unsigned d1 = kPosNone;
         if (s1v[j] >= 0) {
@@ -879,8 +1000,7 @@ __global__ __launch_bounds__(kBinThreads, 5) void k_bin_fill_staged(
                 sg[k1] = geo[j];
                 sm[k1] = m1[j];
             } else {
-                recg[d1] = geo[j];
-                b.recm[d1] = m1[j];
+                rec_put<T>(b, recg, d1, geo[j], m1[j]);
             }
         }
         b.pos[i] = pos_pair(d0, d1);
@@ -900,8 +1020,7 @@ __global__ __launch_bounds__(kBinThreads, 5) void k_bin_fill_staged(
             else if (mid > lo) hi = mid;
         }
         const unsigned d = cur[lo] + (k - off[lo]);
-        recg[d] = sg[k];
-        b.recm[d] = sm[k];
+        rec_put<T>(b, recg, d, sg[k], sm[k]);
     }
 }
 
@@ -911,30 +1030,28 @@ __global__ __launch_bounds__(kBinThreads, 5) void k_bin_fill_staged(
 // values in either place.
 template <typename T, typename Add>
 __device__ __forceinline__ void record_density(const vec4_t<T>& rg, unsigned rm, int k0,
-                                               int k1, int stretch, T fs, Add&& add)
+                                               int k1, int N, int stretch, T fs, Add&& add)
 {
-    const SpanBox sb = span_of(rm, k0);
-    T xr, yr, rat;
-    stretch_of<T>(rg, stretch, xr, yr, rat);
-    const T dx = rg.x, dy = rg.y;
-    const int ka = max(sb.bxl, k0), kb = min(sb.bxl + sb.nx, k1);
+    const RecView<T> rv = rec_view<T>(rg, rm, k0, stretch, N);
+    const T xr = rv.xr, yr = rv.yr, rat = rv.rat, dx = rv.dx, dy = rv.dy;
+    const int ka = max(rv.bxl, k0), kb = min(rv.bxl + rv.nx, k1);
     // y overlaps of the (usual) first 4 columns, shared by the rows
     T tyv[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-        tyv[q] = q <= sb.ny ? min(yr, (T)(q + 1)) - max(dy, (T)q) : (T)0;
+        tyv[q] = q <= rv.ny ? min(yr, (T)(q + 1)) - max(dy, (T)q) : (T)0;
     for (int k = ka; k <= kb; ++k) {
-        const T jx = (T)(k - sb.bxl);
+        const T jx = (T)(k - rv.bxl);
         const T tx = min(xr, jx + (T)1) - max(dx, jx);
         if (!(tx > (T)0)) continue;
         const T rtx = rat * tx;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            if (tyv[q] > (T)0) add(k, sb.byl + q, to_fixed(rtx * tyv[q], fs));
-        for (int q = 4; q <= sb.ny; ++q) {
+            if (tyv[q] > (T)0) add(k, rv.byl + q, to_fixed(rtx * tyv[q], fs));
+        for (int q = 4; q <= rv.ny; ++q) {
             const T ty = min(yr, (T)(q + 1)) - max(dy, (T)q);
             if (!(ty > (T)0)) continue;
-            add(k, sb.byl + q, to_fixed(rtx * ty, fs));
+            add(k, rv.byl + q, to_fixed(rtx * ty, fs));
         }
     }
 }
@@ -960,7 +1077,7 @@ __device__ __forceinline__ void scatter_tall_team(const vec4_t<T>& cell, int lan
         return;
     int s0, s1;
     bool tall;
-    cell_strips(c, b.R, b.lgR, s0, s1, tall);
+    cell_strips<T>(c, g, b.R, b.lgR, s0, s1, tall);
     const double sc = c.ratio() * g.inv_ba;
     const int ny1 = c.byh - c.byl + 1;
     const int nb = (c.bxh - c.bxl + 1) * ny1;
@@ -1078,7 +1195,7 @@ __global__ __launch_bounds__(kOnceThreads, (once_waves<T, CPT>())) void k_bin_fi
             continue;
         int s0, s1;
         bool tall;
-        cell_strips(c, b.R, b.lgR, s0, s1, tall);
+        cell_strips<T>(c, g, b.R, b.lgR, s0, s1, tall);
         if (tall) {
             const unsigned t = atomicAdd(ntall, 1u);
             tall_idx[t] = (unsigned)i;
@@ -1089,15 +1206,15 @@ __global__ __launch_bounds__(kOnceThreads, (once_waves<T, CPT>())) void k_bin_fi
         // strip-relative record, evaluated in float64 and rounded once
         const double ex = (c.x - (g.xl + c.bxl * g.bsx)) * g.inv_bsx;
         const double ey = (c.y - (g.yl + c.byl * g.bsy)) * g.inv_bsy;
-        geo[j] = {(T)ex, (T)ey, (T)((double)cw[j] * g.inv_bsx),
-                  (T)((double)chh[j] * g.inv_bsy)};
+        geo[j] = rec_geo<T>(ex, ey, (double)cw[j] * g.inv_bsx, (double)chh[j] * g.inv_bsy,
+                            c.byl);
         const int nx = c.bxh - c.bxl, ny = c.byh - c.byl;
         s0v[j] = s0;
-        m0[j] = span_word(c.bxl - (s0 << b.lgR), nx, ny, c.byl);
+        m0[j] = rec_span<T>(c.bxl - (s0 << b.lgR), nx, ny, c.byl);
         r0[j] = atomicAdd(&cnt[s0], 1u);
         if (s1 != s0) {
             s1v[j] = s1;
-            m1[j] = span_word(c.bxl - (s1 << b.lgR), nx, ny, c.byl);
+            m1[j] = rec_span<T>(c.bxl - (s1 << b.lgR), nx, ny, c.byl);
             r1[j] = atomicAdd(&cnt[s1], 1u);
         }
     }
@@ -1127,8 +1244,7 @@ __global__ __launch_bounds__(kOnceThreads, (once_waves<T, CPT>())) void k_bin_fi
         if (s0v[j] < 0) continue;
         if (r0[j] < room[s0v[j]]) {
             p0[j] = start[s0v[j]] + r0[j];
-            recg[p0[j]] = geo[j];
-            b.recm[p0[j]] = m0[j];
+            rec_put<T>(b, recg, p0[j], geo[j], m0[j]);
         } else {
             p0[j] = r0[j] - room[s0v[j]];       // its place in the strip's run
             ovm |= 1u << (2 * j);
@@ -1136,8 +1252,7 @@ __global__ __launch_bounds__(kOnceThreads, (once_waves<T, CPT>())) void k_bin_fi
         if (s1v[j] >= 0) {
             if (r1[j] < room[s1v[j]]) {
                 p1[j] = start[s1v[j]] + r1[j];
-                recg[p1[j]] = geo[j];
-                b.recm[p1[j]] = m1[j];
+                rec_put<T>(b, recg, p1[j], geo[j], m1[j]);
             } else {
                 p1[j] = r1[j] - room[s1v[j]];
                 ovm |= 1u << (2 * j + 1);
@@ -1176,8 +1291,7 @@ __global__ __launch_bounds__(kOnceThreads, (once_waves<T, CPT>())) void k_bin_fi
                 return;
             }
             p = b.pool0 + q;
-            recg[p] = gm;
-            b.recm[p] = m;
+            rec_put<T>(b, recg, p, gm, m);
         };
         if (ovm) {
 #pragma unroll
@@ -1214,25 +1328,23 @@ __global__ __launch_bounds__(kOnceThreads, (once_waves<T, CPT>())) void k_bin_fi
 // the same partial.
 template <typename T, typename Row>
 __device__ __forceinline__ vec2_t<T> record_partial(const vec4_t<T>& rg, unsigned rm, int k0,
-                                                    int kg0, int kg1, int stretch, T ba,
+                                                    int kg0, int kg1, int N, int stretch, T ba,
                                                     Row&& row)
 {
-    const SpanBox sb = span_of(rm, k0);
-    T xr, yr, rat;
-    stretch_of<T>(rg, stretch, xr, yr, rat);
-    const T dx = rg.x, dy = rg.y;
-    const int ka = max(sb.bxl, kg0), kb = min(sb.bxl + sb.nx, kg1);
+    const RecView<T> rv = rec_view<T>(rg, rm, k0, stretch, N);
+    const T xr = rv.xr, yr = rv.yr, dx = rv.dx, dy = rv.dy;
+    const int ka = max(rv.bxl, kg0), kb = min(rv.bxl + rv.nx, kg1);
     // y overlaps of the (usual) first 4 columns, shared by the rows
     T tyv[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-        tyv[q] = q <= sb.ny ? min(yr, (T)(q + 1)) - max(dy, (T)q) : (T)0;
+        tyv[q] = q <= rv.ny ? min(yr, (T)(q + 1)) - max(dy, (T)q) : (T)0;
     T ax = (T)0, ay = (T)0;
     for (int k = ka; k <= kb; ++k) {
-        const T jx = (T)(k - sb.bxl);
+        const T jx = (T)(k - rv.bxl);
         const T tx = min(xr, jx + (T)1) - max(dx, jx);
         if (!(tx > (T)0)) continue;
-        const auto rf = row(k, sb.byl);
+        const auto rf = row(k, rv.byl);
         T sx_ = (T)0, sy_ = (T)0;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -1241,7 +1353,7 @@ __device__ __forceinline__ vec2_t<T> record_partial(const vec4_t<T>& rg, unsigne
                 sx_ += tyv[q] * f.x;
                 sy_ += tyv[q] * f.y;
             }
-        for (int q = 4; q <= sb.ny; ++q) {
+        for (int q = 4; q <= rv.ny; ++q) {
             const T ty = min(yr, (T)(q + 1)) - max(dy, (T)q);
             if (!(ty > (T)0)) continue;
             const vec2_t<T> f = rf[q];
@@ -1251,7 +1363,7 @@ __device__ __forceinline__ vec2_t<T> record_partial(const vec4_t<T>& rg, unsigne
         ax += tx * sx_;
         ay += tx * sy_;
     }
-    const T sc = rat * ba;
+    const T sc = rv.rat * ba;
     return vec2_t<T>{sc * ax, sc * ay};
 }
 
@@ -1343,7 +1455,7 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     if (e0 + tid < e1) {
         const unsigned r = map_record(sm, e0 + tid);
         rgn = recg[r];
-        rmn = b.recm[r];
+        rmn = rec_m<T>(b, r);
     }
     __syncthreads();
     for (unsigned eb = e0 + tid; eb < e1; eb += kAccThreads) {
@@ -1352,16 +1464,16 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
         if (eb + kAccThreads < e1) {     // the next record, in flight meanwhile
             const unsigned r = map_record(sm, eb + kAccThreads);
             rgn = recg[r];
-            rmn = b.recm[r];
+            rmn = rec_m<T>(b, r);
         }
-        record_density<T>(rg, rm, k0, k1, g.stretch, fs,
+        record_density<T>(rg, rm, k0, k1, N, g.stretch, fs,
                           [&](int k, int q, A v) { atomicAdd(&tile[(k - k0) * N + q], v); });
     }
     // the strip's overflow list (records past their region's room), by the
     // strip's first chunk, added into the tile like the others
     for_overflow_records(b, s, item, tid, reinterpret_cast<uint2*>(tile + RN + 2),
                          [&](unsigned r) {
-                             record_density<T>(recg[r], b.recm[r], k0, k1, g.stretch, fs,
+                             record_density<T>(recg[r], rec_m<T>(b, r), k0, k1, N, g.stretch, fs,
                                                [&](int k, int q, A v) {
                                                    atomicAdd(&tile[(k - k0) * N + q], v);
                                                });
@@ -1605,7 +1717,7 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
         if (e0 + tid < e1) {                    // the first record, before the rows
             rn0 = map_record(sm, e0 + tid);
             rg0 = recg[rn0];
-            rm0 = b.recm[rn0];
+            rm0 = rec_m<T>(b, rn0);
         }
         for (int kg0 = k0; kg0 < k0 + R; kg0 += RG) {
             const int kg1 = kg0 + RG - 1;
@@ -1652,7 +1764,7 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
             if (kg0 != k0 && e0 + tid < e1) {
                 rn = map_record(sm, e0 + tid);
                 rgn = recg[rn];
-                rmn = b.recm[rn];
+                rmn = rec_m<T>(b, rn);
             }
             for (unsigned eb = e0 + tid; eb < e1; eb += kAccThreads) {
                 const vec4_t<T> rg = rgn;
@@ -1660,10 +1772,10 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
                 if (eb + kAccThreads < e1) {
                     rn = map_record(sm, eb + kAccThreads);
                     rgn = recg[rn];
-                    rmn = b.recm[rn];
+                    rmn = rec_m<T>(b, rn);
                 }
                 vec2_t<T> v = record_partial<T>(
-                    rg, rm, k0, kg0, kg1, g.stretch, ba,
+                    rg, rm, k0, kg0, kg1, N, g.stretch, ba,
                     [&](int k, int c) { return lf + (k - kg0) * N + c; });
                 if (!first) {
                     const vec2_t<T> o = out[r];
@@ -1676,7 +1788,7 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
             // the same rows in LDS and in the same order of row groups
             for_overflow_records(b, s, item, tid, lrun, [&](unsigned r) {
                 vec2_t<T> v = record_partial<T>(
-                    recg[r], b.recm[r], k0, kg0, kg1, g.stretch, ba,
+                    recg[r], rec_m<T>(b, r), k0, kg0, kg1, N, g.stretch, ba,
                     [&](int k, int c) { return lf + (k - kg0) * N + c; });
                 if (!first) {
                     const vec2_t<T> o = out[r];

@@ -151,7 +151,7 @@ struct BinArgs {
                             // block (run_capacity)
     unsigned* done;         // [S] K4 chunks done per strip (zero between steps)
     void* recg;             // [pool0 + pool_cap] record geometry, vec4 of T
-    unsigned* recm;         // [pool0 + pool_cap] record span word
+    unsigned* recm;         // [pool0 + pool_cap] record span word (float64)
     unsigned long long* pos;   // [nc_max] records of cell i: first strip (or
                                // kPosTall / kPosNone) | second strip << 32
     void* gtmp;             // [pool0 + pool_cap] vec2 forces by record
@@ -191,6 +191,8 @@ struct BinPlan {
     size_t cap;             // records (2 per cell)
     size_t reg_cap;         // region capacity of a planned step (>= cap)
     size_t geo_bytes;       // bytes of one record's geometry (4 elements)
+    size_t span_bytes;      // bytes of its span word in recm (float64 only;
+                            // float32 records carry it in the geometry)
 };
 
 // Records all (slot, strip) regions of a plan hold at most: every region's
@@ -213,6 +215,7 @@ inline BinPlan make_bin_plan(int M, int N, int nc_max, size_t elem_bytes)
 {
     BinPlan p{};
     p.geo_bytes = 4 * elem_bytes;
+    p.span_bytes = elem_bytes == 4 ? 0 : sizeof(unsigned);
     int R = 8;
     while (R > 1 && (size_t)R * N * 8 > kTileBytes) R >>= 1;
     if (R > M) R = M;

@@ -113,7 +113,7 @@ Layout plan_layout(int M, int N, int nc, size_t esz, const BinPlan& p, const Bin
     l.nitems = c.take(2 * sizeof(unsigned));
     l.chunk = c.take(2 * sizeof(unsigned));
     l.recg = c.take(p.cap * p.geo_bytes);
-    l.recm = c.take(p.cap * sizeof(unsigned));
+    l.recm = c.take((p.span_bytes ? p.cap : 1) * sizeof(unsigned));
     l.pos = c.take(ncs * sizeof(unsigned long long));
     l.gtmp = c.take(p.cap * 2 * esz);
     l.total = c.end;
