@@ -326,7 +326,7 @@ static int dispatch(int M, int N, int nc, bool det, bool pot, int ch, bool tall,
 #define CASE(a, b) if (M == a && N == b) return run<T, a, b>(nc, det, pot, ch, tall, stage, off);
     CASE(8, 8) CASE(16, 16) CASE(8, 32) CASE(64, 64) CASE(16, 128) CASE(128, 16)
     CASE(256, 32) CASE(32, 256) CASE(32, 2048) CASE(16, 4096)
-    if constexpr (sizeof(T) == 4) { CASE(8, 8192) }
+    if constexpr (sizeof(T) == 4) { CASE(8, 8192) CASE(2048, 16) CASE(4096, 64) }
 #undef CASE
     fprintf(stderr, "unsupported shape\n");
     return 2;

@@ -58,6 +58,9 @@ CASES = [
     "f32 64 64 10800", "f32 64 64 13200 tall", "f32 64 64 16800 tall",
     "f64 64 64 7200", "f64 64 64 8800 tall",
     "f32 64 64 3000 tall off", "f64 16 128 2000 off",
+    # the column pass at 2048 and 4096 rows (two FFTs of 16 elements per
+    # thread, 256- and 512-thread workgroups), 256 and 512 strips
+    "f32 2048 16 3000", "f32 4096 64 5000 tall",
 ]
 
 
