@@ -119,22 +119,31 @@ __device__ __forceinline__ void stretch_of(const vec4_t<T>& r, int stretch, T& x
 // Stored records.  float64: the geometry (dx, dy, w, h) as a double4 in recg
 // and the span word in recm.  float32: one 16-byte word per record in recg
 // (recm unused).  dx and dy, the offsets of the stretched corner from its
-// first bin's edges in [0, 1), are kept as the 23-bit mantissas of the
-// floats 1 + dx and 1 + dy, whose sign and exponent bits are always the same
-// and so carry the rest: the row offset rel (4 bits) and byl (13 bits, 5 in
-// the dx word and 8 in the dy word); w and h are plain float32.  Decoding an
-// offset is one AND-OR and one subtraction (precision 2^-23 of a bin); the
-// row and column counts are derived from the geometry (rec_view).  One
-// aligned 16-byte store per record in K3 and one load in K4 and G1, where
-// the 20-byte form took two of each into two arrays.  A cell whose stretched
-// corner lies below the die's lower x or y edge (a negative offset) takes
-// the tall path instead (cell_strips).
+// first bin's edges, are kept as the 23-bit mantissas of the floats 1 + dx
+// and 1 + dy, whose sign and exponent bits are always the same and so carry
+// the rest: the row offset rel (4 bits) and byl (13 bits, 5 in the dx word
+// and 8 in the dy word); w and h are plain float32.  An offset is in [0, 1)
+// except where the stretch moves a cell's corner past the die's lower edge
+// (its first bin clamped to 0), in [-1, 0) then: along x the record starts
+// one row earlier (rel - 1, at row -1, which every row loop clamps away) with
+// dx + 1; along y it keeps dy + 1 and sets bit 31 of the dy word, and the
+// decode subtracts 2 instead of 1.  Decoding an offset is an AND-OR and a
+// subtraction (precision 2^-23 of a bin); the row and column counts are
+// derived from the geometry (rec_view).  One aligned 16-byte store per record
+// in K3 and one load in K4 and G1, where the 20-byte form took two of each
+// into two arrays.  A cell whose corner lies more than a bin below the lower
+// edge (placed outside the die) takes the tall path instead (cell_strips).
 // ---------------------------------------------------------------------------
 constexpr unsigned kOffMant = 0x007FFFFFu;     // mantissa bits of 1 + offset
 constexpr unsigned kOne = 0x3F800000u;         // the bits of 1.0f
+constexpr unsigned kSign = 0x80000000u;
 
+// rel: the first row's offset in the cell's first strip, in [0, R).  A cell
+// whose stretched corner is below the lower x edge starts at row 0 (rel 0)
+// and spans one strip only (a cell spanning more than R rows is tall).
 template <typename T>
-__device__ __forceinline__ vec4_t<T> rec_geo(double ex, double ey, double wb, double hb, int byl)
+__device__ __forceinline__ vec4_t<T> rec_geo(double ex, double ey, double wb, double hb, int byl,
+                                             int rel)
 {
     if constexpr (sizeof(T) == 4) {
         auto mant = [](double e) -> unsigned {
@@ -142,9 +151,12 @@ __device__ __forceinline__ vec4_t<T> rec_geo(double ex, double ey, double wb, do
             return v <= 0.0 ? 0u : (v >= 8388607.0 ? kOffMant : (unsigned)v);
         };
         const unsigned ub = (unsigned)byl;
+        const bool lx = ex < 0.0, ly = ey < 0.0;
         float4 r;
-        r.x = __uint_as_float(mant(ex) | ((ub & 0x1Fu) << 27));
-        r.y = __uint_as_float(mant(ey) | (((ub >> 5) & 0xFFu) << 23));
+        r.x = __uint_as_float(mant(lx ? ex + 1.0 : ex) | (((unsigned)(rel - lx) & 0xFu) << 23) |
+                              ((ub & 0x1Fu) << 27));
+        r.y = __uint_as_float(mant(ly ? ey + 1.0 : ey) | (((ub >> 5) & 0xFFu) << 23) |
+                              (ly ? kSign : 0u));
         r.z = (float)wb;
         r.w = (float)hb;
         return r;
@@ -154,11 +166,14 @@ __device__ __forceinline__ vec4_t<T> rec_geo(double ex, double ey, double wb, do
 }
 
 // The per-record part of a record in strip s (rel = bxl - s * R): the span
-// word (float64), or rel in 4 bits (float32), merged by rec_put.
+// word (float64), or at float32 whether s is the cell's second strip (the
+// geometry word carries the first strip's rel, in [0, R), and the second
+// strip's is R less: the same 4-bit field plus 16 - R, no carry), a constant
+// at every call, so K3 keeps nothing per record for it.
 template <typename T>
-__device__ __forceinline__ unsigned rec_span(int rel, int nx, int ny, int byl)
+__device__ __forceinline__ unsigned rec_span(int rel, int nx, int ny, int byl, bool second)
 {
-    if constexpr (sizeof(T) == 4) return (unsigned)rel & 0xFu;
+    if constexpr (sizeof(T) == 4) return second ? 1u : 0u;
     else return span_word(rel, nx, ny, byl);
 }
 
@@ -168,7 +183,7 @@ __device__ __forceinline__ void rec_put(const BinArgs& b, vec4_t<T>* recg, unsig
 {
     if constexpr (sizeof(T) == 4) {
         float4 r = geo;
-        r.x = __uint_as_float(__float_as_uint(r.x) | (m << 23));
+        if (m) r.x = __uint_as_float(__float_as_uint(r.x) + ((16u - (unsigned)b.R) << 23));
         recg[p] = r;
     } else {
         recg[p] = geo;
@@ -201,8 +216,9 @@ __device__ __forceinline__ RecView<T> rec_view(const vec4_t<T>& rg, unsigned rm,
     RecView<T> v;
     if constexpr (sizeof(T) == 4) {
         const unsigned ux = __float_as_uint(rg.x), uy = __float_as_uint(rg.y);
+        // 1 + offset minus 1; dy minus 2 where bit 31 of its word is set
         v.dx = __uint_as_float((ux & kOffMant) | kOne) - 1.f;
-        v.dy = __uint_as_float((uy & kOffMant) | kOne) - 1.f;
+        v.dy = __uint_as_float((uy & kOffMant) | kOne) - __uint_as_float(kOne + ((uy >> 31) << 23));
         v.bxl = k0 + (((int)(ux << 5)) >> 28);
         v.byl = (int)((ux >> 27) | (((uy >> 23) & 0xFFu) << 5));
         const float w = rg.z, h = rg.w;
@@ -271,7 +287,8 @@ __device__ __forceinline__ void cell_strips(const CellSpan& c, const Grid& g, in
                                             int& s0, int& s1, bool& tall)
 {
     tall = (c.bxh - c.bxl + 1) > R || (c.byh - c.byl) > kMaxSpanY;
-    if constexpr (sizeof(T) == 4) tall = tall || c.x < g.xl || c.y < g.yl;
+    // a float32 record holds offsets down to -1 bin (rec_geo)
+    if constexpr (sizeof(T) == 4) tall = tall || c.x < g.xl - g.bsx || c.y < g.yl - g.bsy;
     s0 = c.bxl >> lgR;
     s1 = c.bxh >> lgR;
 }
@@ -838,14 +855,14 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill_direct(
         const double ex = (c.x - (g.xl + c.bxl * g.bsx)) * g.inv_bsx;
         const double ey = (c.y - (g.yl + c.byl * g.bsy)) * g.inv_bsy;
         const vec4_t<T> geo = rec_geo<T>(ex, ey, (double)cw[j] * g.inv_bsx,
-                                         (double)chh[j] * g.inv_bsy, c.byl);
+                                         (double)chh[j] * g.inv_bsy, c.byl, c.bxl - (s0 << b.lgR));
         const int nx = c.bxh - c.bxl, ny = c.byh - c.byl;
         const unsigned p0 = atomicAdd(&cur[s0], 1u);
-        rec_put<T>(b, recg, p0, geo, rec_span<T>(c.bxl - (s0 << b.lgR), nx, ny, c.byl));
+        rec_put<T>(b, recg, p0, geo, rec_span<T>(c.bxl - (s0 << b.lgR), nx, ny, c.byl, false));
         unsigned p1 = kPosNone;
         if (s1 != s0) {
             p1 = atomicAdd(&cur[s1], 1u);
-            rec_put<T>(b, recg, p1, geo, rec_span<T>(c.bxl - (s1 << b.lgR), nx, ny, c.byl));
+            rec_put<T>(b, recg, p1, geo, rec_span<T>(c.bxl - (s1 << b.lgR), nx, ny, c.byl, true));
         }
         b.pos[i] = pos_pair(p0, p1);
     }
@@ -954,14 +971,14 @@ __global__ __launch_bounds__(kBinThreads, 5) void k_bin_fill_staged(
         const double ex = (c.x - (g.xl + c.bxl * g.bsx)) * g.inv_bsx;
         const double ey = (c.y - (g.yl + c.byl * g.bsy)) * g.inv_bsy;
         geo[j] = rec_geo<T>(ex, ey, (double)cw[j] * g.inv_bsx, (double)chh[j] * g.inv_bsy,
-                            c.byl);
+                            c.byl, c.bxl - (s0 << b.lgR));
         const int nx = c.bxh - c.bxl, ny = c.byh - c.byl;
         s0v[j] = s0;
-        m0[j] = rec_span<T>(c.bxl - (s0 << b.lgR), nx, ny, c.byl);
+        m0[j] = rec_span<T>(c.bxl - (s0 << b.lgR), nx, ny, c.byl, false);
         r0[j] = atomicAdd(&cnt[s0], 1u);
         if (s1 != s0) {
             s1v[j] = s1;
-            m1[j] = rec_span<T>(c.bxl - (s1 << b.lgR), nx, ny, c.byl);
+            m1[j] = rec_span<T>(c.bxl - (s1 << b.lgR), nx, ny, c.byl, true);
             r1[j] = atomicAdd(&cnt[s1], 1u);
         }
     }
@@ -1207,14 +1224,14 @@ __global__ __launch_bounds__(kOnceThreads, (once_waves<T, CPT>())) void k_bin_fi
         const double ex = (c.x - (g.xl + c.bxl * g.bsx)) * g.inv_bsx;
         const double ey = (c.y - (g.yl + c.byl * g.bsy)) * g.inv_bsy;
         geo[j] = rec_geo<T>(ex, ey, (double)cw[j] * g.inv_bsx, (double)chh[j] * g.inv_bsy,
-                            c.byl);
+                            c.byl, c.bxl - (s0 << b.lgR));
         const int nx = c.bxh - c.bxl, ny = c.byh - c.byl;
         s0v[j] = s0;
-        m0[j] = rec_span<T>(c.bxl - (s0 << b.lgR), nx, ny, c.byl);
+        m0[j] = rec_span<T>(c.bxl - (s0 << b.lgR), nx, ny, c.byl, false);
         r0[j] = atomicAdd(&cnt[s0], 1u);
         if (s1 != s0) {
             s1v[j] = s1;
-            m1[j] = rec_span<T>(c.bxl - (s1 << b.lgR), nx, ny, c.byl);
+            m1[j] = rec_span<T>(c.bxl - (s1 << b.lgR), nx, ny, c.byl, true);
             r1[j] = atomicAdd(&cnt[s1], 1u);
         }
     }
