@@ -876,10 +876,11 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill_direct(
 // (its base from fresh_offsets).  They are ranked per strip (LDS atomics),
 // staged in LDS in strip order (the block's counting sort) and copied out
 // with consecutive threads on consecutive slots, so a wave's stores cover
-// whole runs instead of one scattered 16- and 4-byte store per record: the
+// whole runs instead of one scattered store per record: the
 // lines of a run are written whole, by one workgroup, at once.  A staged
 // slot's strip is found again by a binary search of the strip offsets, so
-// the stage holds only the records (20 bytes each at float32) and five
+// the stage holds only the records (geometry and per-record word, 20 bytes
+// each at float32) and five
 // workgroups fit a CU: one round at 1.1 M cells.  Records past kStage
 // slots go straight to their place.
 // LDS: cur[S] | cnt[S] | tmp[kBinThreads + kChunkCands] | off[S + 1] |
@@ -929,7 +930,8 @@ __global__ __launch_bounds__(kBinThreads, 5) void k_bin_fill_staged(
     __syncthreads();
     vec4_t<T>* recg = reinterpret_cast<vec4_t<T>*>(b.recg);
     unsigned long long* Bm = reinterpret_cast<unsigned long long*>(b.B);
-    // per cell: its record geometry, span words, strips and ranks in them
+    // per cell: its record geometry, the per-record parts (rec_span), strips
+    // and ranks in them
     vec4_t<T> geo[kCellsPerThread];
     unsigned m0[kCellsPerThread], m1[kCellsPerThread], r0[kCellsPerThread],
         r1[kCellsPerThread];
