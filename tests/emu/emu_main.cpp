@@ -396,9 +396,80 @@ static int check_blocks()
     return 0;
 }
 
+// The float32 record word (rec_geo / rec_put / rec_view): for random cells,
+// including those whose stretched corner lies below the die's lower x or y
+// edge (offset in [-1, 0), first row or column 0) and the second-strip copy
+// of a cell that spans two strips, the decoded record gives the encoded
+// geometry: the same absolute first row, offsets within 2^-23 of a bin, the
+// same first column, extents and area ratio, and row / column counts that
+// reach the far edge.
+static int check_records()
+{
+    using namespace dpep;
+    std::mt19937_64 rng(11);
+    std::uniform_real_distribution<double> u01(0.0, 1.0);
+    const int Rs[] = {1, 2, 4, 8};
+    const int N = 8192;
+    long long checked = 0;
+    for (int it = 0; it < 400000; ++it) {
+        const int R = Rs[it % 4];
+        const int s0 = (int)(rng() % 64);
+        const int k0 = s0 * R;
+        const bool xedge = (it % 7) == 0, yedge = (it % 5) == 0;
+        const int rel0 = xedge ? 0 : (int)(rng() % R);
+        const int byl = yedge ? 0 : (int)(rng() % N);
+        const double ex = xedge ? -u01(rng) : u01(rng) * (1.0 - 1e-9);
+        const double ey = yedge ? -u01(rng) : u01(rng) * (1.0 - 1e-9);
+        const int stretch = (int)(rng() & 1);
+        // extents in bins; an edge cell is stretched (its corner moved left)
+        const double wb = (xedge || stretch) ? u01(rng) * 1.4 + 1e-3 : u01(rng) * 3.0 + 1e-3;
+        const double hb = (yedge || stretch) ? u01(rng) * 1.4 + 1e-3 : u01(rng) * 3.0 + 1e-3;
+        const int st = (xedge || yedge) ? 1 : stretch;
+        BinArgs b{};
+        b.R = R;
+        float4 rec[2];
+        const float4 geo = rec_geo<float>(ex, ey, wb, hb, byl, rel0);
+        rec_put<float>(b, rec, 0u, geo, rec_span<float>(rel0, 0, 0, byl, false));
+        // a cell starting in strip s0 that reaches strip s0 + 1 (never an
+        // x-edge cell: it would span more than R rows)
+        const bool second = !xedge && R > 1;
+        if (second) rec_put<float>(b, rec, 1u, geo, rec_span<float>(rel0 - R, 0, 0, byl, true));
+        for (int copy = 0; copy < (second ? 2 : 1); ++copy) {
+            const int kc = copy ? k0 + R : k0;       // the strip the copy is in
+            const RecView<float> v = rec_view<float>(rec[copy], 0u, kc, st, N);
+            const double x_abs = (double)v.bxl + (double)v.dx;
+            const double x_want = (double)(k0 + rel0) + ex;
+            const double tol = 1.2e-7;
+            bool ok = fabs(x_abs - x_want) <= tol && fabs((double)v.dy - ey) <= tol &&
+                      v.byl == byl && v.bxl == k0 + rel0 - (xedge ? 1 : 0);
+            const float w = (float)wb, h = (float)hb;
+            float wc = w, hc = h, rat = 1.f;
+            if (st) {
+                const float m = 1.41421356237309504880f;
+                wc = w > m ? w : m;
+                hc = h > m ? h : m;
+                rat = (w * h) * fast_rcp(wc * hc);
+            }
+            ok = ok && v.rat == rat && v.xr == v.dx + wc && v.yr == v.dy + hc;
+            ok = ok && v.nx == (int)v.xr && v.ny == std::min((int)v.yr, N - 1 - byl) &&
+                 v.bxl + v.nx + 1 > x_want + wc - 1e-6 && v.ny >= 0;
+            if (!ok) {
+                fprintf(stderr, "record mismatch it=%d R=%d copy=%d ex=%.9f ey=%.9f byl=%d rel0=%d: "
+                        "bxl %d dx %.9f dy %.9f byl %d nx %d ny %d\n", it, R, copy, ex, ey, byl,
+                        rel0, v.bxl, v.dx, v.dy, v.byl, v.nx, v.ny);
+                return 1;
+            }
+            ++checked;
+        }
+    }
+    printf("records ok (%lld records)\n", checked);
+    return 0;
+}
+
 int main(int argc, char** argv)
 {
     if (argc == 2 && !strcmp(argv[1], "blocks")) return check_blocks();
+    if (argc == 2 && !strcmp(argv[1], "records")) return check_records();
     if (argc < 5) { fprintf(stderr, "usage: %s f32|f64 M N nc [det] [nopot]\n", argv[0]); return 2; }
     const bool f64 = !strcmp(argv[1], "f64");
     const int M = atoi(argv[2]), N = atoi(argv[3]), nc = atoi(argv[4]);

@@ -73,6 +73,17 @@ def test_kernels_in_bounds_and_accurate(emu, case):
     assert "emu " in r.stdout
 
 
+def test_float32_record_word(emu):
+    """rec_geo / rec_put / rec_view round trip: random cells, the second-strip
+    copy of a cell spanning two strips, and cells whose stretched corner lies
+    below the die's lower x or y edge decode to the encoded geometry (first
+    row and column, offsets within 2^-23 of a bin, extents, area ratio, row
+    and column counts reaching the far edge)."""
+    r = subprocess.run([emu, "records"], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert "records ok" in r.stdout
+
+
 def test_cell_blocks_host_logic(emu):
     """once_blocks / set_count_blocks / count_cells: every cell in exactly one
     one-pass block and one counting part, no part straddling two blocks, the

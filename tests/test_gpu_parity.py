@@ -386,6 +386,45 @@ def test_offset_die_with_oblong_bins(oracle, dtype):
     print(errs, flush=True)
 
 
+@pytest.mark.parametrize("stretch", [True, False])
+def test_cells_at_the_lower_die_edges(oracle, stretch):
+    """Small cells whose (stretched) corner lies below the die's lower x edge,
+    its lower y edge, or both, by up to 1.3 bins, on a die whose corner is not
+    the origin.  A float32 record keeps such a cell within a bin of the edge
+    (offset + 1: one row early along x, a flag bit along y); one further out
+    goes to the side map.  Two steps on one context (counted, then one pass)
+    are bitwise equal, and both match the float64 oracle within tolerance."""
+    M, N = 256, 512
+    bsx, bsy = 4.0, 3.0
+    xl, yl = 311.5, -97.25
+    xh, yh = xl + bsx * M, yl + bsy * N
+    rng = np.random.default_rng(77 + int(stretch))
+    nc = 40000
+    sx = rng.uniform(0.05, 1.3, nc) * bsx
+    sy = rng.uniform(0.05, 1.3, nc) * bsy
+    px = rng.uniform(xl, xh - 2 * bsx, nc)
+    py = rng.uniform(yl, yh - 2 * bsy, nc)
+    q = nc // 4
+    # a quarter along the lower x edge, one along the lower y edge, one at
+    # the corner; the rest anywhere
+    px[:q] = xl + rng.uniform(-1.3, 0.5, q) * bsx
+    py[q:2 * q] = yl + rng.uniform(-1.3, 0.5, q) * bsy
+    px[2 * q:3 * q] = xl + rng.uniform(-1.3, 0.5, q) * bsx
+    py[2 * q:3 * q] = yl + rng.uniform(-1.3, 0.5, q) * bsy
+    cells = [a.astype(np.float32) for a in (px, py, sx, sy)]
+
+    class W:
+        pass
+    w = W()
+    w.M, w.N, w.xl, w.yl, w.xh, w.yh = M, N, xl, yl, xh, yh
+    w.d0n = (0.3 * rng.random((M, N))).astype(np.float32)
+    print(f"lower edges, stretch={stretch}", flush=True)
+    errs = check(run_gpu(w, cells=cells, stretch=stretch),
+                 run_oracle(oracle, w, cells=cells, stretch=stretch),
+                 np.float32, f"lower edges stretch={stretch}")
+    print(errs, flush=True)
+
+
 def test_step_device_matches_host_step():
     """dpep_step_device on caller-owned device buffers (allocated through the
     same HIP runtime libdpep links) equals the host-buffer step; afterwards
