@@ -336,7 +336,10 @@ int dpep_create(int M, int N, int nc_max, double xl, double yl, double xh,
     auto step = [&]() -> int {
         HIP_TRY(hipGetDevice(&c->device));
         HIP_TRY(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
-        for (auto& e : c->ev) HIP_TRY(hipEventCreate(&e));
+        // timing only (read after a stream synchronisation): no system-scope
+        // fence when recorded, which would write back and invalidate the
+        // caches between the kernels it brackets
+        for (auto& e : c->ev) HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
         HIP_TRY(hipEventCreate(&c->ev_x0));
         HIP_TRY(hipEventCreate(&c->ev_x1));
         const size_t mnb = (size_t)M * N * c->esz;
@@ -721,7 +724,8 @@ int dpep_set_profiling(dpep_ctx* c, int slots)
     if (slots == 0) return DPEP_OK;
     c->prof_ev.assign((size_t)slots * (kNumStages + 1), nullptr);
     c->prof_once.assign((size_t)slots, 0);
-    for (auto& e : c->prof_ev) HIP_TRY(hipEventCreate(&e));
+    for (auto& e : c->prof_ev)      // timing only, as the step's events
+        HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
     c->prof_slots = slots;
     c->profiling = 1;
     return DPEP_OK;
