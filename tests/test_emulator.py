@@ -58,9 +58,6 @@ CASES = [
     "f32 64 64 10800", "f32 64 64 13200 tall", "f32 64 64 16800 tall",
     "f64 64 64 7200", "f64 64 64 8800 tall",
     "f32 64 64 3000 tall off", "f64 16 128 2000 off",
-    # the column pass at 2048 and 4096 rows (two FFTs of 16 elements per
-    # thread, 256- and 512-thread workgroups), 256 and 512 strips
-    "f32 2048 16 3000", "f32 4096 64 5000 tall",
 ]
 
 
@@ -71,6 +68,23 @@ def test_kernels_in_bounds_and_accurate(emu, case):
                        timeout=600, env=env)
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
     assert "emu " in r.stdout
+
+
+# The spectral passes alone at every FFT length from 8 to 8192 on either axis
+# (the column pass at 2048 and 4096 rows holds 210-229 VGPRs' worth of state,
+# 8192 the largest LDS use), against the oracle's FFT solve of the same density.
+SPECTRAL = ["f32 2048 16", "f32 4096 32", "f32 16 2048", "f32 32 4096", "f32 8192 8",
+            "f32 8 8192", "f32 1024 64", "f64 2048 16", "f64 4096 32", "f64 1024 64",
+            "f64 16 2048", "f64 32 4096"]
+
+
+@pytest.mark.parametrize("case", SPECTRAL)
+def test_spectral_passes_in_bounds_and_accurate(emu, case):
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=1")
+    r = subprocess.run([emu, "spectral"] + case.split(), capture_output=True, text=True,
+                       timeout=600, env=env)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+    assert "emu spectral " in r.stdout
 
 
 def test_float32_record_word(emu):
