@@ -80,9 +80,10 @@ struct dpep_ctx {
     hipStream_t stream = nullptr;
     hipEvent_t ev[kNumStages + 1] = {};
     hipEvent_t ev_x0 = nullptr, ev_x1 = nullptr;
-    // per-kernel profiling: a ring of `prof_slots` event sets, one per step
-    std::vector<hipEvent_t> prof_ev;   // prof_slots * (kNumStages + 1)
-    std::vector<unsigned char> prof_once;   // per slot: that step ran no count kernel
+    // per-kernel profiling: a ring of `prof_slots` event sets, one per step,
+    // a (start, end) pair per kernel stamped by its own dispatch
+    std::vector<hipEvent_t> prof_ev;   // prof_slots * 2 * kNumStages
+    std::vector<unsigned char> prof_mask;   // per slot: the stages that step launched
     int profiling = 0;
     int prof_slots = 0;
     long prof_steps = 0;               // steps recorded since enabling
@@ -192,38 +193,33 @@ static int run_step(dpep_ctx* c, const T* px, const T* py, const T* sx,
     c->planned = 0;
     c->scrub = 1;                 // until the step's last launch succeeds
 
-    // with profiling on, this step's stage boundaries go to one ring slot
-    hipEvent_t* pe = prof ? &c->prof_ev[(size_t)(c->prof_steps % c->prof_slots) *
-                                         (kNumStages + 1)]
-                          : nullptr;
-    // a recorded event costs GPU time (measured ~3.5 us each on MI355X):
-    // only when the caller asked for per-step timings
+    // with profiling on, each kernel's dispatch stamps its (start, end) pair
+    // in one ring slot; the mask says which kernels this step launched
+    const size_t slot = prof ? (size_t)(c->prof_steps % c->prof_slots) : 0;
+    const hipEvent_t* pe = prof ? &c->prof_ev[slot * 2 * kNumStages] : nullptr;
+    if (prof)
+        c->prof_mask[slot] = (unsigned char)((once ? 0u : 1u) | 0x1Eu |
+                                             (gather && nc > 0 ? 0x60u : 0u));
+    // a recorded event costs GPU time (a few us per step on MI355X): only
+    // when the caller asked for per-step timings
     const bool timed = (c->flags & DPEP_FLAG_STEP_TIMINGS) != 0;
     if (timed) HIP_TRY(hipEventRecord(c->ev[0], s));
-    if (prof) {
-        c->prof_once[(size_t)(c->prof_steps % c->prof_slots)] = once ? 1 : 0;
-        HIP_TRY(hipEventRecord(pe[0], s));
-    }
     HIP_TRY(launch_bin_scatter<T>(px, py, sx, sy, nc, c->grid, c->bins, c->sargs, d0n,
-                                  dens, (T*)c->d_T, once, s, prof ? pe + 1 : nullptr));
+                                  dens, (T*)c->d_T, once, s, pe));
 
-    HIP_TRY(launch_col_pass<T>(c->sargs, (T*)c->d_T, (T*)c->d_Ux, (T*)c->d_Uy, s));
-    if (prof) HIP_TRY(hipEventRecord(pe[4], s));
+    HIP_TRY(launch_col_pass<T>(c->sargs, (T*)c->d_T, (T*)c->d_Ux, (T*)c->d_Uy, s,
+                               pe ? pe + 6 : nullptr));
     HIP_TRY(launch_row_inv<T>(c->sargs, (const T*)c->d_Ux, (const T*)c->d_Uy, fx, fy,
-                              phi, s));
-    if (prof) HIP_TRY(hipEventRecord(pe[5], s));
+                              phi, s, pe ? pe + 8 : nullptr));
     if (gather)
         HIP_TRY(launch_bin_gather<T>(px, py, sx, sy, nc, c->grid, c->bins, fx, fy,
-                                     gx, gy, s, prof ? pe[6] : nullptr));
-    else if (prof)
-        HIP_TRY(hipEventRecord(pe[6], s));
+                                     gx, gy, s, pe ? pe + 10 : nullptr));
     c->planned = 1;
     c->scrub = 0;
     c->last_par = c->par;
     c->last_once = once ? 1 : 0;
     c->last_stream = s;
     c->par ^= 1;
-    if (prof) HIP_TRY(hipEventRecord(pe[kNumStages], s));
     if (timed) HIP_TRY(hipEventRecord(c->ev[kNumStages], s));
     if (prof) c->prof_steps++;
     c->last_nc = nc;
@@ -642,11 +638,13 @@ int dpep_get_timings(dpep_ctx* c, float* out)
                             ? elapsed(c->ev[0], c->ev[kNumStages]) : 0.f;
     out[0] = c->h2d_ms;
     if (c->profiling && c->prof_steps > 0) {
-        const hipEvent_t* pe = &c->prof_ev[(size_t)((c->prof_steps - 1) % c->prof_slots) *
-                                           (kNumStages + 1)];
-        out[1] = elapsed(pe[0], pe[3]);              // binning, accumulation, P1
-        out[5] = elapsed(pe[3], pe[5]);              // P2 + P3
-        out[2] = elapsed(pe[5], pe[kNumStages]);     // gather
+        const size_t slot = (size_t)((c->prof_steps - 1) % c->prof_slots);
+        const hipEvent_t* pe = &c->prof_ev[slot * 2 * kNumStages];
+        const unsigned mask = c->prof_mask[slot];
+        // binning (from K1, or K3 on a one-pass step), accumulation and P1
+        out[1] = elapsed(pe[(mask & 1u) ? 0 : 2], pe[5]);
+        out[5] = elapsed(pe[6], pe[9]);              // P2 + P3
+        out[2] = (mask & 0x60u) ? elapsed(pe[10], pe[13]) : 0.f;   // gather
     } else {
         out[5] = total;
     }
@@ -698,12 +696,19 @@ int dpep_get_kernel_times(dpep_ctx* c, float* out, int n)
     for (int i = 0; i < n; ++i) out[i] = 0.f;
     const long steps = c->prof_steps < c->prof_slots ? c->prof_steps : c->prof_slots;
     for (long k = 0; k < steps; ++k) {
-        const hipEvent_t* pe = &c->prof_ev[(size_t)k * (kNumStages + 1)];
-        // a one-pass step launches no count kernel: its [0] interval is the
-        // two events' own cost, not a kernel's
-        for (int i = c->prof_once[(size_t)k] ? 1 : 0; i < kNumStages && i < n; ++i)
-            out[i] += 1000.f * elapsed(pe[i], pe[i + 1]);
-        if (n > kNumStages) out[kNumStages] += 1000.f * elapsed(pe[0], pe[kNumStages]);
+        const hipEvent_t* pe = &c->prof_ev[(size_t)k * 2 * kNumStages];
+        const unsigned mask = c->prof_mask[(size_t)k];
+        // each kernel's own (start, end); a kernel the step did not launch
+        // (K1 on a one-pass step, the gather when off) adds nothing
+        int first = -1, last = -1;
+        for (int i = 0; i < kNumStages; ++i) {
+            if (!((mask >> i) & 1u)) continue;
+            if (first < 0) first = i;
+            last = i;
+            if (i < n) out[i] += 1000.f * elapsed(pe[2 * i], pe[2 * i + 1]);
+        }
+        if (n > kNumStages && first >= 0)
+            out[kNumStages] += 1000.f * elapsed(pe[2 * first], pe[2 * last + 1]);
     }
     for (int i = 0; i < n && i <= kNumStages; ++i) out[i] /= (float)steps;
     return DPEP_OK;
@@ -722,8 +727,8 @@ int dpep_set_profiling(dpep_ctx* c, int slots)
     c->prof_slots = 0;
     c->prof_steps = 0;
     if (slots == 0) return DPEP_OK;
-    c->prof_ev.assign((size_t)slots * (kNumStages + 1), nullptr);
-    c->prof_once.assign((size_t)slots, 0);
+    c->prof_ev.assign((size_t)slots * 2 * kNumStages, nullptr);
+    c->prof_mask.assign((size_t)slots, 0);
     for (auto& e : c->prof_ev)      // timing only, as the step's events
         HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
     c->prof_slots = slots;

@@ -34,7 +34,7 @@ template <typename T>
 hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
                               const T* sy, int nc, const Grid& g,
                               BinArgs b, const SpectralArgs& a, const T* d0n, T* dens,
-                              T* Tt, bool once, hipStream_t s, hipEvent_t* ev)
+                              T* Tt, bool once, hipStream_t s, const hipEvent_t* ev)
 {
     const OnceBlocks ob = once_blocks(nc, b.cus, sizeof(T));
     set_count_blocks(b, ob);
@@ -44,12 +44,14 @@ hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
     if (once && (b.pool_cap < 2u * (unsigned)(nc > 0 ? nc : 0) || ob.grid > b.rmax))
         return hipErrorInvalidValue;
     hipError_t e;
+    const hipEvent_t* ev1 = ev ? ev + 0 : nullptr;     // K1
+    const hipEvent_t* ev3 = ev ? ev + 2 : nullptr;     // K3
+    const hipEvent_t* ev4 = ev ? ev + 4 : nullptr;     // K4
     if (once) {
-        if (ev && (e = hipEventRecord(ev[0], s))) return e;
         if ((e = with_cpt(ob.cpt, [&](auto c) -> hipError_t {
                  constexpr int CPT = decltype(c)::value;
-                 k_bin_fill_once<T, CPT><<<(unsigned)ob.grid, kOnceThreads,
-                                           fill_once_lds<T>(b.S), s>>>(px, py, sx, sy, nc, g, b);
+                 DPEP_LAUNCH(ev3, (k_bin_fill_once<T, CPT>), (unsigned)ob.grid, kOnceThreads,
+                             fill_once_lds<T>(b.S), s, px, py, sx, sy, nc, g, b);
                  return hipSuccess;
              })))
             return e;
@@ -59,51 +61,50 @@ hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
         const size_t fill_lds =
             staged ? fill_lds_staged<T>(b.S)
                    : (size_t)(2 * b.S + kBinThreads + kChunkCands) * sizeof(unsigned);
-        k_bin_count<T><<<b.G1, kBinThreads, count_lds, s>>>(px, py, sx, sy, nc, g, b);
+        DPEP_LAUNCH(ev1, (k_bin_count<T>), b.G1, kBinThreads, count_lds, s, px, py, sx, sy,
+                    nc, g, b);
         if ((e = hipGetLastError())) return e;
-        if (ev && (e = hipEventRecord(ev[0], s))) return e;
         if (staged)
-            k_bin_fill_staged<T><<<b.G1, kBinThreads, fill_lds, s>>>(px, py, sx, sy, nc, g, b);
+            DPEP_LAUNCH(ev3, (k_bin_fill_staged<T>), b.G1, kBinThreads, fill_lds, s, px, py, sx,
+                        sy, nc, g, b);
         else
-            k_bin_fill_direct<T><<<b.G1, kBinThreads, fill_lds, s>>>(px, py, sx, sy, nc, g, b);
+            DPEP_LAUNCH(ev3, (k_bin_fill_direct<T>), b.G1, kBinThreads, fill_lds, s, px, py, sx,
+                        sy, nc, g, b);
     }
     if ((e = hipGetLastError())) return e;
-    if (ev && (e = hipEventRecord(ev[1], s))) return e;
-    e = dispatch_n<T>(g.N, [&](auto lc) -> hipError_t {
+    return dispatch_n<T>(g.N, [&](auto lc) -> hipError_t {
         constexpr int L = decltype(lc)::value;
-        k_strip_acc<T, L><<<b.Wacc, kAccThreads, acc_lds_bytes<T, L>(), s>>>(g, b, a, d0n,
-                                                                             dens, Tt);
+        DPEP_LAUNCH(ev4, (k_strip_acc<T, L>), b.Wacc, kAccThreads, (acc_lds_bytes<T, L>()), s, g,
+                    b, a, d0n, dens, Tt);
         return hipGetLastError();
     });
-    if (e) return e;
-    if (ev && (e = hipEventRecord(ev[2], s))) return e;
-    return hipSuccess;
 }
 
 template <typename T>
 hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
                              const T* sy, int nc, const Grid& g,
                              const BinArgs& b, const T* fx, const T* fy,
-                             T* gx, T* gy, hipStream_t s, hipEvent_t ev)
+                             T* gx, T* gy, hipStream_t s, const hipEvent_t* ev)
 {
-    if (nc <= 0) return ev ? hipEventRecord(ev, s) : hipSuccess;
+    if (nc <= 0) return hipSuccess;
     const size_t lds = gather_lds<T>(b.R, g.N);
+    const hipEvent_t* evg1 = ev ? ev + 0 : nullptr;
+    const hipEvent_t* evg2 = ev ? ev + 2 : nullptr;
     if (b.Wgat == b.S)      // one workgroup per strip: item w is mostly strip w
-        k_gather_bin<T, true><<<b.Wgat, kAccThreads, lds, s>>>(g, b, fx, fy);
+        DPEP_LAUNCH(evg1, (k_gather_bin<T, true>), b.Wgat, kAccThreads, lds, s, g, b, fx, fy);
     else
-        k_gather_bin<T, false><<<b.Wgat, kAccThreads, lds, s>>>(g, b, fx, fy);
+        DPEP_LAUNCH(evg1, (k_gather_bin<T, false>), b.Wgat, kAccThreads, lds, s, g, b, fx, fy);
     hipError_t e = hipGetLastError();
     if (e) return e;
-    if (ev && (e = hipEventRecord(ev, s))) return e;
     // the one-pass K3's cell blocks
     const OnceBlocks ob = once_blocks(nc, b.cus, sizeof(T));
     BinArgs bo = b;
     bo.qcells = ob.q;
     if ((e = with_cpt(ob.cpt, [&](auto c) -> hipError_t {
              constexpr int CPT = decltype(c)::value;
-             k_gather_out<T, kOnceThreads, CPT>
-                 <<<(unsigned)ob.grid, kOnceThreads, gather_out_lds<kOnceThreads, CPT>(), s>>>(
-                     px, py, sx, sy, nc, g, bo, fx, fy, gx, gy);
+             DPEP_LAUNCH(evg2, (k_gather_out<T, kOnceThreads, CPT>), (unsigned)ob.grid,
+                         kOnceThreads, (gather_out_lds<kOnceThreads, CPT>()), s, px, py, sx, sy,
+                         nc, g, bo, fx, fy, gx, gy);
              return hipSuccess;
          })))
         return e;
@@ -190,12 +191,12 @@ hipError_t bin_prepare()
 template hipError_t launch_bin_scatter<float>(const float*, const float*, const float*,
                                               const float*, int, const Grid&, BinArgs,
                                               const SpectralArgs&, const float*, float*,
-                                              float*, bool, hipStream_t, hipEvent_t*);
+                                              float*, bool, hipStream_t, const hipEvent_t*);
 template hipError_t launch_bin_scatter<double>(const double*, const double*,
                                                const double*, const double*, int,
                                                const Grid&, BinArgs, const SpectralArgs&,
                                                const double*, double*, double*, bool,
-                                               hipStream_t, hipEvent_t*);
+                                               hipStream_t, const hipEvent_t*);
 template hipError_t bin_occupancy<float>(int, int, int&, int&);
 template hipError_t bin_occupancy<double>(int, int, int&, int&);
 template hipError_t launch_fixed_density<float>(const float*, const float*, const float*,
@@ -208,11 +209,11 @@ template hipError_t launch_fixed_density<double>(const double*, const double*,
 template hipError_t launch_bin_gather<float>(const float*, const float*, const float*,
                                              const float*, int, const Grid&,
                                              const BinArgs&, const float*, const float*,
-                                             float*, float*, hipStream_t, hipEvent_t);
+                                             float*, float*, hipStream_t, const hipEvent_t*);
 template hipError_t launch_bin_gather<double>(const double*, const double*,
                                               const double*, const double*, int,
                                               const Grid&, const BinArgs&, const double*,
                                               const double*, double*, double*,
-                                              hipStream_t, hipEvent_t);
+                                              hipStream_t, const hipEvent_t*);
 
 }  // namespace dpep

@@ -2,6 +2,7 @@
 // translation units of libdpep.so.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -9,6 +10,21 @@
 #include <type_traits>
 
 #include "dpep_device.h"
+
+// kern<<<grid, block, lds, s>>>(args...); with a profiling event pair (ev
+// non-null: ev[0], ev[1]) the same launch through hipExtLaunchKernelGGL, which
+// stamps the dispatch's own start and end into the two events, so a kernel's
+// interval is its own and nothing is recorded between launches.  The kernel
+// is passed in parentheses (a template's commas): DPEP_LAUNCH(ev, (k<T, L>), ...).
+#define DPEP_UNPAREN(...) __VA_ARGS__
+#define DPEP_LAUNCH(ev, kern, grid, block, lds, s, ...)                                   \
+    do {                                                                                  \
+        if (ev)                                                                           \
+            hipExtLaunchKernelGGL(DPEP_UNPAREN kern, dim3(grid), dim3(block),              \
+                                  (unsigned)(lds), s, (ev)[0], (ev)[1], 0u, __VA_ARGS__); \
+        else                                                                              \
+            DPEP_UNPAREN kern<<<dim3(grid), dim3(block), (lds), s>>>(__VA_ARGS__);         \
+    } while (0)
 
 namespace dpep {
 
@@ -55,13 +71,15 @@ inline size_t post_elems(int L) { return 2 * (size_t)(L / 2 + 1); }
 template <typename T>
 hipError_t launch_tables(int L, T* tw, T* post, hipStream_t s);
 
-// Launchers (return hipError_t of the launch).  T = float or double.
+// Launchers (return hipError_t of the launch).  T = float or double.  ev:
+// null, or the profiling event pair (start, end) of the pass's kernel.
 template <typename T>
 hipError_t launch_col_pass(const SpectralArgs& a, const T* Tt, T* Ux, T* Uy,
-                           hipStream_t s);
+                           hipStream_t s, const hipEvent_t* ev = nullptr);
 template <typename T>
 hipError_t launch_row_inv(const SpectralArgs& a, const T* Ux, const T* Uy,
-                          T* fx, T* fy, T* phi, hipStream_t s);
+                          T* fx, T* fy, T* phi, hipStream_t s,
+                          const hipEvent_t* ev = nullptr);
 // ---------------------------------------------------------------------------
 // Strip binning (kernels in dpep_bin.h)
 // ---------------------------------------------------------------------------
@@ -333,20 +351,20 @@ inline hipError_t with_cpt(int cpt, Fn&& fn)
 
 // Strip-binned scatter (K1 unless `once`, K3, K4; K4 also runs the row DCT,
 // writing T) and gather (G1, G2); the scatter's ev (nullable) receives 3
-// events: after K1 (at the start when `once`), K3, K4; the gather's ev
-// (nullable) is recorded between G1 and G2.  `once` needs the counts of a
-// previous step (parity b.par ^ 1) on the same buffers and an overflow pool
-// of 2 * nc records (pool_cap).
+// ev (nullable): profiling event pairs (start, end), the scatter's for K1,
+// K3 and K4 (six events; K1's unused when `once`), the gather's for G1 and G2
+// (four).  `once` needs the counts of a previous step (parity b.par ^ 1) on
+// the same buffers and an overflow pool of 2 * nc records (pool_cap).
 template <typename T>
 hipError_t launch_bin_scatter(const T* px, const T* py, const T* sx,
                               const T* sy, int nc, const Grid& g, BinArgs b,
                               const SpectralArgs& a, const T* d0n, T* dens, T* Tt,
-                              bool once, hipStream_t s, hipEvent_t* ev);
+                              bool once, hipStream_t s, const hipEvent_t* ev);
 template <typename T>
 hipError_t launch_bin_gather(const T* px, const T* py, const T* sx,
                              const T* sy, int nc, const Grid& g,
                              const BinArgs& b, const T* fx, const T* fy,
-                             T* gx, T* gy, hipStream_t s, hipEvent_t ev);
+                             T* gx, T* gy, hipStream_t s, const hipEvent_t* ev);
 
 // D0n = target_density * exact overlap of n fixed cells / bin area, through
 // the side map B (left at zero).

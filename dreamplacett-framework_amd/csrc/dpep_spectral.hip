@@ -67,27 +67,28 @@ hipError_t launch_tables(int L, T* tw, T* post, hipStream_t s)
 
 template <typename T>
 hipError_t launch_col_pass(const SpectralArgs& a, const T* Tt, T* Ux, T* Uy,
-                           hipStream_t s)
+                           hipStream_t s, const hipEvent_t* ev)
 {
     return dispatch_len<T>(a.M, [&](auto lc) -> hipError_t {
         constexpr int L = decltype(lc)::value;
         constexpr int F = fpw<T>(L);
         const dim3 grid(a.N / (2 * F)), block(col_threads<T>(L));
-        k_col_pass<T, L, F><<<grid, block, lds_bytes<T, L>(), s>>>(a, Tt, Ux, Uy);
+        DPEP_LAUNCH(ev, (k_col_pass<T, L, F>), grid, block, (lds_bytes<T, L>()), s, a, Tt, Ux, Uy);
         return hipGetLastError();
     });
 }
 
 template <typename T>
 hipError_t launch_row_inv(const SpectralArgs& a, const T* Ux, const T* Uy,
-                          T* fx, T* fy, T* phi, hipStream_t s)
+                          T* fx, T* fy, T* phi, hipStream_t s, const hipEvent_t* ev)
 {
     return dispatch_len<T>(a.N, [&](auto lc) -> hipError_t {
         constexpr int L = decltype(lc)::value;
         constexpr int F = fpw<T>(L);
         const int groups = a.M / (2 * F);
         const dim3 grid(groups * (a.potential ? 3 : 2)), block(row_threads<T>(L));
-        k_row_inv<T, L, F><<<grid, block, lds_bytes<T, L>(), s>>>(a, Ux, Uy, fx, fy, phi);
+        DPEP_LAUNCH(ev, (k_row_inv<T, L, F>), grid, block, (lds_bytes<T, L>()), s, a, Ux, Uy, fx,
+                    fy, phi);
         return hipGetLastError();
     });
 }
@@ -134,14 +135,14 @@ hipError_t spectral_prepare()
 template hipError_t launch_tables<float>(int, float*, float*, hipStream_t);
 template hipError_t launch_tables<double>(int, double*, double*, hipStream_t);
 template hipError_t launch_col_pass<float>(const SpectralArgs&, const float*,
-                                           float*, float*, hipStream_t);
+                                           float*, float*, hipStream_t, const hipEvent_t*);
 template hipError_t launch_col_pass<double>(const SpectralArgs&, const double*,
-                                            double*, double*, hipStream_t);
+                                            double*, double*, hipStream_t, const hipEvent_t*);
 template hipError_t launch_row_inv<float>(const SpectralArgs&, const float*,
                                           const float*, float*, float*, float*,
-                                          hipStream_t);
+                                          hipStream_t, const hipEvent_t*);
 template hipError_t launch_row_inv<double>(const SpectralArgs&, const double*,
                                            const double*, double*, double*,
-                                           double*, hipStream_t);
+                                           double*, hipStream_t, const hipEvent_t*);
 
 }  // namespace dpep

@@ -251,7 +251,8 @@ int dpep_get_kernel_times(dpep_ctx* ctx, float* out, int n);
 int dpep_get_binning_stats(dpep_ctx* ctx, long long* out, int n);
 
 /* slots > 0 enables per-kernel event timing for a ring of `slots` steps
- * (adds one event between launches); 0 disables (the default). */
+ * (each kernel of a profiled step is launched with a start/end event pair
+ * stamped by its own dispatch); 0 disables (the default). */
 int dpep_set_profiling(dpep_ctx* ctx, int slots);
 
 #ifdef __cplusplus
