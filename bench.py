@@ -519,6 +519,28 @@ def main():
         ms, _, _ = sequence_run(w, dtype, potential, walk_dev, args.steps,
                                 two_pass=args.two_pass)
 
+    # per-kernel times right after the timed region, while the GPU still runs
+    # at its sustained clocks (the host-path steps below leave it idle between
+    # copies)
+    kt = None
+    if not args.no_profile:
+        if walk_dev is None:
+            # K steps again, each kernel launched with a start/end event pair
+            # its dispatch stamps: per-kernel average durations.  The ring
+            # keeps the last K of K + 20 steps (the first ones follow the
+            # pause of creating the events)
+            ctx.set_profiling(args.steps)
+            for _ in range(args.steps + 20):
+                ctx.compute()
+            ctx.sync()
+            kt = ctx.kernel_times_us()
+            ctx.set_profiling(0)
+        else:
+            _, _, kt = sequence_run(w, dtype, potential, walk_dev, args.steps,
+                                    two_pass=args.two_pass, profile=True)
+            _, per, _ = sequence_run(w, dtype, potential, walk_dev, args.steps,
+                                     two_pass=args.two_pass, stats=True)
+            walk_stats = overflow_summary(per)
     # PCIe-inclusive rate (host buffers in and out): never `value`.  The
     # pageable figure is every output to fresh numpy arrays; host_path() the
     # staged ones.
@@ -533,23 +555,6 @@ def main():
                 round((time.perf_counter() - t0) * 1e3 / n_host, 3)}
         ctx.set_cells(px, py, sx, sy)
 
-    kt = None
-    if not args.no_profile:
-        if walk_dev is None:
-            # same K steps again with HIP events between launches on the
-            # context's stream: per-kernel average durations
-            ctx.set_profiling(args.steps)
-            for _ in range(args.steps):
-                ctx.compute()
-            ctx.sync()
-            kt = ctx.kernel_times_us()
-            ctx.set_profiling(0)
-        else:
-            _, _, kt = sequence_run(w, dtype, potential, walk_dev, args.steps,
-                                    two_pass=args.two_pass, profile=True)
-            _, per, _ = sequence_run(w, dtype, potential, walk_dev, args.steps,
-                                     two_pass=args.two_pass, stats=True)
-            walk_stats = overflow_summary(per)
     ctx.close()
     if walk_dev is not None:
         walk_dev.free()
