@@ -346,29 +346,35 @@ __device__ __forceinline__ int count_cells(const BinArgs& b, int nc, int& c0, in
     return ob & (kCountSlots - 1);
 }
 
-// The CPT cells of thread tid in the one-pass block [c0, cend) (cend > c0
-// unless the block is empty; slots past cend hold copies of cell cend - 1,
-// which the caller skips).  Every load is unconditional (clamped index), so
-// no per-cell branch holds the loads back.
+// The CPT cells of thread tid in the one-pass block [c0, cend) (slots past
+// cend hold copies of cell cend - 1, which the caller skips).  Every load is
+// unconditional (clamped index), so no per-cell branch holds the loads back.
+// An empty block (a step of no cells, whose cell pointers may be null) reads
+// the word at `spare` (any valid device address) instead, for cells the
+// caller skips all the same; choosing the pointers, not the loads, keeps the
+// values in registers (a branch around the loads made the compiler keep some
+// of them in scratch memory).
 template <typename T, int NT, int CPT>
 __device__ __forceinline__ void load_block_cells(const T* __restrict__ px,
                                                  const T* __restrict__ py,
                                                  const T* __restrict__ sx,
                                                  const T* __restrict__ sy, int c0, int cend,
-                                                 int tid, T* cx, T* cy, T* cw, T* ch)
+                                                 int tid, const void* spare, T* cx, T* cy,
+                                                 T* cw, T* ch)
 {
-    if (cend > c0) {
+    const bool any = cend > c0;
+    const T* qx = any ? px : static_cast<const T*>(spare);
+    const T* qy = any ? py : static_cast<const T*>(spare);
+    const T* qw = any ? sx : static_cast<const T*>(spare);
+    const T* qh = any ? sy : static_cast<const T*>(spare);
+    const int last = any ? cend - 1 : 0;
 #pragma unroll
-        for (int j = 0; j < CPT; ++j) {
-            const int i = min(c0 + tid + j * NT, cend - 1);
-            cx[j] = px[i];
-            cy[j] = py[i];
-            cw[j] = sx[i];
-            ch[j] = sy[i];
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < CPT; ++j) cx[j] = cy[j] = cw[j] = ch[j] = (T)0;
+    for (int j = 0; j < CPT; ++j) {
+        const int i = min(c0 + tid + j * NT, last);
+        cx[j] = qx[i];
+        cy[j] = qy[i];
+        cw[j] = qw[i];
+        ch[j] = qh[i];
     }
 }
 
@@ -1188,7 +1194,7 @@ __global__ __launch_bounds__(kOnceThreads, (once_waves<T, CPT>())) void k_bin_fi
     unsigned* xrow = counts_of(b, b.par) + (size_t)(blockIdx.x & (kCountSlots - 1)) * S;
     // the cells' loads are issued first: their latency overlaps the plan
     T cx[CPT], cy[CPT], cw[CPT], chh[CPT];
-    load_block_cells<T, NT, CPT>(px, py, sx, sy, c0, cend, tid, cx, cy, cw, chh);
+    load_block_cells<T, NT, CPT>(px, py, sx, sy, c0, cend, tid, b.recg, cx, cy, cw, chh);
     once_offsets<NT>(b, start, room, cnt, tmp);
     __syncthreads();
     for (int s = tid; s < S; s += NT) cnt[s] = 0u;
