@@ -1348,9 +1348,16 @@ __global__ __launch_bounds__(kOnceThreads, (once_waves<T, CPT>())) void k_bin_fi
 // One record's partial force over rows [ka', kb'] = its rows within
 // [kg0, kg1] (a row group of its strip with first row k0): row(k, c) gives
 // the bins of row k from column c on, indexable by q, each an (fx, fy)
-// pair.  G1 reads the pairs from its LDS copy of the rows, the overflow
-// records' pass from the field maps: the same values in the same order, so
-// the same partial.
+// pair.  G1 reads the pairs from its LDS copy of the rows, for the strip's
+// records and its overflow records alike: the same values in the same order,
+// so the same partial.
+// The first four columns of a row are read unconditionally, with weight zero
+// where the record has no positive overlap (a column past its last, or a row
+// or column it only touches): those terms add a signed zero, which leaves
+// every sum bitwise as if they were skipped.  Branching around each read
+// instead made every read wait for its own LDS round trip.  So row(k, c)[q]
+// must be readable and finite for q <= 3 past any column c of a row k: the
+// next row's bins, or (after the last row) padding (kGatherPadBins).
 template <typename T, typename Row>
 __device__ __forceinline__ vec2_t<T> record_partial(const vec4_t<T>& rg, unsigned rm, int k0,
                                                     int kg0, int kg1, int N, int stretch, T ba,
@@ -1359,25 +1366,29 @@ __device__ __forceinline__ vec2_t<T> record_partial(const vec4_t<T>& rg, unsigne
     const RecView<T> rv = rec_view<T>(rg, rm, k0, stretch, N);
     const T xr = rv.xr, yr = rv.yr, dx = rv.dx, dy = rv.dy;
     const int ka = max(rv.bxl, kg0), kb = min(rv.bxl + rv.nx, kg1);
-    // y overlaps of the (usual) first 4 columns, shared by the rows
+    // y overlaps of the (usual) first 4 columns, shared by the rows (zero
+    // where not positive)
     T tyv[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-        tyv[q] = q <= rv.ny ? min(yr, (T)(q + 1)) - max(dy, (T)q) : (T)0;
+    for (int q = 0; q < 4; ++q) {
+        const T t = min(yr, (T)(q + 1)) - max(dy, (T)q);
+        tyv[q] = (q <= rv.ny && t > (T)0) ? t : (T)0;
+    }
     T ax = (T)0, ay = (T)0;
     for (int k = ka; k <= kb; ++k) {
         const T jx = (T)(k - rv.bxl);
-        const T tx = min(xr, jx + (T)1) - max(dx, jx);
-        if (!(tx > (T)0)) continue;
+        const T t = min(xr, jx + (T)1) - max(dx, jx);
+        const T tx = t > (T)0 ? t : (T)0;
         const auto rf = row(k, rv.byl);
+        vec2_t<T> f4[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) f4[q] = rf[q];
         T sx_ = (T)0, sy_ = (T)0;
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            if (tyv[q] > (T)0) {
-                const vec2_t<T> f = rf[q];
-                sx_ += tyv[q] * f.x;
-                sy_ += tyv[q] * f.y;
-            }
+        for (int q = 0; q < 4; ++q) {
+            sx_ += tyv[q] * f4[q].x;
+            sy_ += tyv[q] * f4[q].y;
+        }
         for (int q = 4; q <= rv.ny; ++q) {
             const T ty = min(yr, (T)(q + 1)) - max(dy, (T)q);
             if (!(ty > (T)0)) continue;
@@ -1693,16 +1704,25 @@ __host__ __device__ constexpr int gather_rows(int R, int N)
     return rg;
 }
 
-// G1's LDS: the staged rows of both field maps, then the overflow run table.
+// G1's LDS: the staged rows of both field maps, kGatherPadBins zero (fx, fy)
+// pairs (record_partial reads up to 3 bins past a record's first column,
+// also in the last staged row), then the overflow run table.
+constexpr int kGatherPadBins = 4;
+
 template <typename T>
 __host__ __device__ constexpr size_t gather_lds_fields(int R, int N)
 {
     return (size_t)gather_rows<T>(R, N) * N * 2 * sizeof(T);
 }
 template <typename T>
+__host__ __device__ constexpr size_t gather_lds_runs(int R, int N)
+{
+    return gather_lds_fields<T>(R, N) + (size_t)kGatherPadBins * 2 * sizeof(T);
+}
+template <typename T>
 __host__ __device__ constexpr size_t gather_lds(int R, int N)
 {
-    return gather_lds_fields<T>(R, N) + (size_t)kRunBatch * sizeof(uint2);
+    return gather_lds_runs<T>(R, N) + (size_t)kRunBatch * sizeof(uint2);
 }
 
 template <typename T, bool kGuess>
@@ -1736,7 +1756,9 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
         // both fields of a bin side by side: one 2-element LDS read per bin;
         // then the overflow run table
         vec2_t<T>* lf = reinterpret_cast<vec2_t<T>*>(smem);
-        uint2* lrun = reinterpret_cast<uint2*>(smem + gather_lds_fields<T>(R, N));
+        uint2* lrun = reinterpret_cast<uint2*>(smem + gather_lds_runs<T>(R, N));
+        if (tid < kGatherPadBins)               // written before the loop's first barrier
+            lf[(size_t)RG * N + tid] = vec2_t<T>{(T)0, (T)0};
         vec4_t<T> rg0{};
         unsigned rm0 = 0u, rn0 = 0u;
         if (e0 + tid < e1) {                    // the first record, before the rows
