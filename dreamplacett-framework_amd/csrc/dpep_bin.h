@@ -390,6 +390,17 @@ __device__ __forceinline__ unsigned long long to_fixed(float v, float scale)
     return (unsigned long long)__float2uint_rn(v * scale);
 }
 
+// The same conversions of a value already scaled.
+__device__ __forceinline__ unsigned long long to_fixed(double v)
+{
+    return (unsigned long long)__double2ull_rn(v);
+}
+
+__device__ __forceinline__ unsigned long long to_fixed(float v)
+{
+    return (unsigned long long)__float2uint_rn(v);
+}
+
 // ---------------------------------------------------------------------------
 // The plan: regions of the (slot, strip) pairs and the K4 / G1 work items.
 // ---------------------------------------------------------------------------
@@ -1050,12 +1061,15 @@ __global__ __launch_bounds__(kBinThreads, 5) void k_bin_fill_staged(
 }
 
 // One record's fixed-point contributions to the bins of rows [k0, k1] (its
-// strip): add(row, column, value) for each bin it overlaps.  K4 adds them
-// into its LDS tile; an overflow record's go into the side map B, the same
-// values in either place.
-template <typename T, typename Add>
+// strip), added into K4's LDS tile (row - k0, column) at tile[(row - k0) * N
+// + column] (for the strip's records and its overflow records alike).  The
+// scale fs is a power of two, so folding it into the row's weight (rat * tx
+// * fs, exact) rounds each value as (rat * tx * ty) * fs would; a row's
+// address is formed once, its columns are immediate offsets from it.
+template <typename T>
 __device__ __forceinline__ void record_density(const vec4_t<T>& rg, unsigned rm, int k0,
-                                               int k1, int N, int stretch, T fs, Add&& add)
+                                               int k1, int N, int stretch, T fs,
+                                               unsigned long long* tile)
 {
     const RecView<T> rv = rec_view<T>(rg, rm, k0, stretch, N);
     const T xr = rv.xr, yr = rv.yr, rat = rv.rat, dx = rv.dx, dy = rv.dy;
@@ -1069,14 +1083,15 @@ __device__ __forceinline__ void record_density(const vec4_t<T>& rg, unsigned rm,
         const T jx = (T)(k - rv.bxl);
         const T tx = min(xr, jx + (T)1) - max(dx, jx);
         if (!(tx > (T)0)) continue;
-        const T rtx = rat * tx;
+        const T rtxs = (rat * tx) * fs;
+        unsigned long long* row = tile + ((k - k0) * N + rv.byl);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            if (tyv[q] > (T)0) add(k, rv.byl + q, to_fixed(rtx * tyv[q], fs));
+            if (tyv[q] > (T)0) atomicAdd(row + q, to_fixed(rtxs * tyv[q]));
         for (int q = 4; q <= rv.ny; ++q) {
             const T ty = min(yr, (T)(q + 1)) - max(dy, (T)q);
             if (!(ty > (T)0)) continue;
-            add(k, rv.byl + q, to_fixed(rtx * ty, fs));
+            atomicAdd(row + q, to_fixed(rtxs * ty));
         }
     }
 }
@@ -1502,17 +1517,14 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
             rgn = recg[r];
             rmn = rec_m<T>(b, r);
         }
-        record_density<T>(rg, rm, k0, k1, N, g.stretch, fs,
-                          [&](int k, int q, A v) { atomicAdd(&tile[(k - k0) * N + q], v); });
+        record_density<T>(rg, rm, k0, k1, N, g.stretch, fs, tile);
     }
     // the strip's overflow list (records past their region's room), by the
     // strip's first chunk, added into the tile like the others
     for_overflow_records(b, s, item, tid, reinterpret_cast<uint2*>(tile + RN + 2),
                          [&](unsigned r) {
                              record_density<T>(recg[r], rec_m<T>(b, r), k0, k1, N, g.stretch, fs,
-                                               [&](int k, int q, A v) {
-                                                   atomicAdd(&tile[(k - k0) * N + q], v);
-                                               });
+                                               tile);
                          });
     __syncthreads();
 
