@@ -1065,7 +1065,8 @@ __global__ __launch_bounds__(kBinThreads, 5) void k_bin_fill_staged(
 // + column] (for the strip's records and its overflow records alike).  The
 // scale fs is a power of two, so folding it into the row's weight (rat * tx
 // * fs, exact) rounds each value as (rat * tx * ty) * fs would; a row's
-// address is formed once, its columns are immediate offsets from it.
+// address steps by N, its columns are immediate offsets from it, and its x
+// overlap is formed as in record_partial (bitwise the same value).
 template <typename T>
 __device__ __forceinline__ void record_density(const vec4_t<T>& rg, unsigned rm, int k0,
                                                int k1, int N, int stretch, T fs,
@@ -1079,12 +1080,12 @@ __device__ __forceinline__ void record_density(const vec4_t<T>& rg, unsigned rm,
 #pragma unroll
     for (int q = 0; q < 4; ++q)
         tyv[q] = q <= rv.ny ? min(yr, (T)(q + 1)) - max(dy, (T)q) : (T)0;
-    for (int k = ka; k <= kb; ++k) {
-        const T jx = (T)(k - rv.bxl);
-        const T tx = min(xr, jx + (T)1) - max(dx, jx);
+    unsigned long long* row = tile + ((ka - k0) * N + rv.byl);
+    T jx = (T)(ka - rv.bxl);
+    for (int k = ka; k <= kb; ++k, row += N, jx += (T)1) {
+        const T tx = min(xr - jx, (T)1) - max(dx - jx, (T)0);
         if (!(tx > (T)0)) continue;
         const T rtxs = (rat * tx) * fs;
-        unsigned long long* row = tile + ((k - k0) * N + rv.byl);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
             if (tyv[q] > (T)0) atomicAdd(row + q, to_fixed(rtxs * tyv[q]));
@@ -1361,22 +1362,26 @@ __global__ __launch_bounds__(kOnceThreads, (once_waves<T, CPT>())) void k_bin_fi
 }
 
 // One record's partial force over rows [ka', kb'] = its rows within
-// [kg0, kg1] (a row group of its strip with first row k0): row(k, c) gives
-// the bins of row k from column c on, indexable by q, each an (fx, fy)
-// pair.  G1 reads the pairs from its LDS copy of the rows, for the strip's
-// records and its overflow records alike: the same values in the same order,
-// so the same partial.
+// [kg0, kg1] (a row group of its strip with first row k0) from rows, row kg0
+// of the group's (fx, fy) pairs in LDS with rows N pairs apart.  G1 takes
+// the strip's records and its overflow records alike through it: the same
+// values in the same order, so the same partial.
 // The first four columns of a row are read unconditionally, with weight zero
 // where the record has no positive overlap (a column past its last, or a row
 // or column it only touches): those terms add a signed zero, which leaves
 // every sum bitwise as if they were skipped.  Branching around each read
-// instead made every read wait for its own LDS round trip.  So row(k, c)[q]
-// must be readable and finite for q <= 3 past any column c of a row k: the
-// next row's bins, or (after the last row) padding (kGatherPadBins).
-template <typename T, typename Row>
+// instead made every read wait for its own LDS round trip.  So up to 3 pairs
+// past any column of a row must be readable and finite: the next row's
+// pairs, or (after the last row) padding (kGatherPadBins).
+// A row's x overlap is min(xr - jx, 1) - max(dx - jx, 0) for the row jx
+// rows past the record's first: xr - jx is exact for every row the record
+// spans (jx is an integer no larger than xr) and dx - jx is negative past the
+// first row, so the overlap equals min(xr, jx + 1) - max(dx, jx) bit for bit
+// with a float counter and no conversion per row.
+template <typename T>
 __device__ __forceinline__ vec2_t<T> record_partial(const vec4_t<T>& rg, unsigned rm, int k0,
                                                     int kg0, int kg1, int N, int stretch, T ba,
-                                                    Row&& row)
+                                                    const vec2_t<T>* rows)
 {
     const RecView<T> rv = rec_view<T>(rg, rm, k0, stretch, N);
     const T xr = rv.xr, yr = rv.yr, dx = rv.dx, dy = rv.dy;
@@ -1390,11 +1395,11 @@ __device__ __forceinline__ vec2_t<T> record_partial(const vec4_t<T>& rg, unsigne
         tyv[q] = (q <= rv.ny && t > (T)0) ? t : (T)0;
     }
     T ax = (T)0, ay = (T)0;
-    for (int k = ka; k <= kb; ++k) {
-        const T jx = (T)(k - rv.bxl);
-        const T t = min(xr, jx + (T)1) - max(dx, jx);
+    const vec2_t<T>* rf = rows + ((ka - kg0) * N + rv.byl);
+    T jx = (T)(ka - rv.bxl);
+    for (int k = ka; k <= kb; ++k, rf += N, jx += (T)1) {
+        const T t = min(xr - jx, (T)1) - max(dx - jx, (T)0);
         const T tx = t > (T)0 ? t : (T)0;
-        const auto rf = row(k, rv.byl);
         vec2_t<T> f4[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) f4[q] = rf[q];
@@ -1833,9 +1838,7 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
                     rgn = recg[rn];
                     rmn = rec_m<T>(b, rn);
                 }
-                vec2_t<T> v = record_partial<T>(
-                    rg, rm, k0, kg0, kg1, N, g.stretch, ba,
-                    [&](int k, int c) { return lf + (k - kg0) * N + c; });
+                vec2_t<T> v = record_partial<T>(rg, rm, k0, kg0, kg1, N, g.stretch, ba, lf);
                 if (!first) {
                     const vec2_t<T> o = out[r];
                     v.x += o.x;
@@ -1846,9 +1849,8 @@ __global__ __launch_bounds__(kAccThreads) void k_gather_bin(
             // the strip's overflow list, by the strip's first chunk, from
             // the same rows in LDS and in the same order of row groups
             for_overflow_records(b, s, item, tid, lrun, [&](unsigned r) {
-                vec2_t<T> v = record_partial<T>(
-                    recg[r], rec_m<T>(b, r), k0, kg0, kg1, N, g.stretch, ba,
-                    [&](int k, int c) { return lf + (k - kg0) * N + c; });
+                vec2_t<T> v = record_partial<T>(recg[r], rec_m<T>(b, r), k0, kg0, kg1, N,
+                                                g.stretch, ba, lf);
                 if (!first) {
                     const vec2_t<T> o = out[r];
                     v.x += o.x;
