@@ -1075,12 +1075,14 @@ __device__ __forceinline__ void record_density(const vec4_t<T>& rg, unsigned rm,
     const RecView<T> rv = rec_view<T>(rg, rm, k0, stretch, N);
     const T xr = rv.xr, yr = rv.yr, rat = rv.rat, dx = rv.dx, dy = rv.dy;
     const int ka = max(rv.bxl, k0), kb = min(rv.bxl + rv.nx, k1);
-    // y overlaps of the (usual) first 4 columns, shared by the rows
+    // y overlaps of the (usual) first 4 columns, shared by the rows; yr
+    // clamped to the grid's last column edge gives the columns past it no
+    // positive overlap and the others their own
+    const T yrc = min(yr, (T)(N - rv.byl));
     T tyv[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-        tyv[q] = q <= rv.ny ? min(yr, (T)(q + 1)) - max(dy, (T)q) : (T)0;
-    unsigned long long* row = tile + ((ka - k0) * N + rv.byl);
+    for (int q = 0; q < 4; ++q) tyv[q] = min(yrc, (T)(q + 1)) - max(dy, (T)q);
+    unsigned long long* row = tile + (__umul24((unsigned)(ka - k0), (unsigned)N) + (unsigned)rv.byl);
     T jx = (T)(ka - rv.bxl);
     for (int k = ka; k <= kb; ++k, row += N, jx += (T)1) {
         const T tx = min(xr - jx, (T)1) - max(dx - jx, (T)0);
@@ -1387,15 +1389,15 @@ __device__ __forceinline__ vec2_t<T> record_partial(const vec4_t<T>& rg, unsigne
     const T xr = rv.xr, yr = rv.yr, dx = rv.dx, dy = rv.dy;
     const int ka = max(rv.bxl, kg0), kb = min(rv.bxl + rv.nx, kg1);
     // y overlaps of the (usual) first 4 columns, shared by the rows (zero
-    // where not positive)
+    // where not positive); yr clamped to the grid's last column edge gives
+    // the columns past it no positive overlap and the others their own
+    const T yrc = min(yr, (T)(N - rv.byl));
     T tyv[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const T t = min(yr, (T)(q + 1)) - max(dy, (T)q);
-        tyv[q] = (q <= rv.ny && t > (T)0) ? t : (T)0;
-    }
+    for (int q = 0; q < 4; ++q) tyv[q] = max(min(yrc, (T)(q + 1)) - max(dy, (T)q), (T)0);
     T ax = (T)0, ay = (T)0;
-    const vec2_t<T>* rf = rows + ((ka - kg0) * N + rv.byl);
+    // row offsets below 2^24 (rows < 8, N <= 8192): a 24-bit multiply
+    const vec2_t<T>* rf = rows + (__umul24((unsigned)(ka - kg0), (unsigned)N) + (unsigned)rv.byl);
     T jx = (T)(ka - rv.bxl);
     for (int k = ka; k <= kb; ++k, rf += N, jx += (T)1) {
         const T t = min(xr - jx, (T)1) - max(dx - jx, (T)0);

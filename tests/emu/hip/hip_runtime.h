@@ -93,6 +93,10 @@ inline unsigned long long __float2ull_rn(float x)
 {
     return (unsigned long long)std::nearbyint(x);
 }
+inline unsigned __umul24(unsigned a, unsigned b)
+{
+    return (a & 0xFFFFFFu) * (b & 0xFFFFFFu);
+}
 template <class T>
 inline T unsafeAtomicAdd(T* p, T v)
 {
