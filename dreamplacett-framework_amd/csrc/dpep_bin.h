@@ -1443,12 +1443,6 @@ __device__ __forceinline__ void flush_value(unsigned long long v, size_t gi,
 // adds its tile into the strip's rows of the side map B; the last chunk to
 // finish reads them back and completes the strip.
 // ---------------------------------------------------------------------------
-__host__ __device__ constexpr int strip_rows(int N)
-{
-    int R = 8;
-    while (R > 1 && (size_t)R * N * 8 > kTileBytes) R >>= 1;
-    return R;
-}
 
 // Elements per thread of K4's row DCT: the fewest (8 or more) that keep the
 // strip's R / 2 FFTs within the workgroup, so every thread takes part.

@@ -44,7 +44,7 @@ struct Tiles {
 // once) and TX, doubled until a tile fills a 128-byte cache line (P2 reads
 // whole tiles: a half-line tile costs a second line fetch; at 4096 x 4096
 // float32, 4-row tiles doubled P2's fetched bytes).  At most M.
-inline int t_tile_rows(int R, int TX, int TV, size_t esz, int M)
+__host__ __device__ constexpr int t_tile_rows(int R, int TX, int TV, size_t esz, int M)
 {
     int t = R > TX ? R : TX;
     while ((size_t)t * TV * esz < 128 && t < M) t *= 2;
@@ -204,6 +204,15 @@ inline void make_grid(Grid& g, int M, int N, double xl, double yl, double xh, do
 // Host-side sizing of the binning buffers (shared with the CPU emulator).
 constexpr size_t kTileBytes = 131072;  // LDS tile of K4 (uint64 words) and G1
 
+// Rows per strip of an N-column grid: K4's LDS tile of R rows of N uint64
+// words holds at most kTileBytes.
+__host__ __device__ constexpr int strip_rows(int N)
+{
+    int R = 8;
+    while (R > 1 && (size_t)R * N * 8 > kTileBytes) R >>= 1;
+    return R;
+}
+
 struct BinPlan {
     int S, R, lgR, G1max;
     size_t cap;             // records (2 per cell)
@@ -234,8 +243,7 @@ inline BinPlan make_bin_plan(int M, int N, int nc_max, size_t elem_bytes)
     BinPlan p{};
     p.geo_bytes = 4 * elem_bytes;
     p.span_bytes = elem_bytes == 4 ? 0 : sizeof(unsigned);
-    int R = 8;
-    while (R > 1 && (size_t)R * N * 8 > kTileBytes) R >>= 1;
+    int R = strip_rows(N);
     if (R > M) R = M;
     p.R = R;
     p.lgR = 0;
@@ -255,9 +263,7 @@ inline void make_spectral_args(SpectralArgs& a, const Grid& g, int dtype, bool p
     a.M = g.M; a.N = g.N;
     a.tiles.TX = 2 * spectral_fpw(g.N, dtype);
     a.tiles.TV = 2 * spectral_fpw(g.M, dtype);
-    int R = 8;   // rows per strip, as make_bin_plan sizes them
-    while (R > 1 && (size_t)R * g.N * 8 > kTileBytes) R >>= 1;
-    a.tiles.TXT = t_tile_rows(R, a.tiles.TX, a.tiles.TV, esz, g.M);
+    a.tiles.TXT = t_tile_rows(strip_rows(g.N), a.tiles.TX, a.tiles.TV, esz, g.M);
     a.wu_step = 2.0 * M_PI / g.M;
     a.wv_step = 2.0 * M_PI / g.N * (g.bsx / g.bsy);
     a.potential = potential ? 1 : 0;

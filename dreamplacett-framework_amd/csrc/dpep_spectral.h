@@ -94,6 +94,33 @@ __host__ __device__ constexpr int row_threads(int L)
     return fpw<T>(L) * (L / row_e<T>(L));
 }
 
+// Tile extents of a square L x L grid, as make_spectral_args sets them.
+// The passes compiled for square grids (kSq) take them as constants, so their
+// tile offsets become constant shifts and immediate offsets instead of
+// shifts by amounts loaded at run time.
+template <typename T, int L>
+__host__ __device__ constexpr Tiles square_tiles()
+{
+    Tiles t{};
+    t.TX = 2 * fpw<T>(L);
+    t.TV = 2 * fpw<T>(L);
+    t.TXT = t_tile_rows(strip_rows(L), t.TX, t.TV, sizeof(T), L);
+    return t;
+}
+
+// Square grids of at least kSquareMin bins a side run the passes compiled
+// with their tile extents as constants; other grids, and smaller squares (one
+// form fewer to compile per length), read them from the args.
+constexpr int kSquareMin = 512;
+
+template <typename T, int L>
+inline bool square_form(const SpectralArgs& a)
+{
+    constexpr Tiles kT = square_tiles<T, L>();
+    return L >= kSquareMin && a.M == L && a.N == L && a.tiles.TX == kT.TX &&
+           a.tiles.TV == kT.TV && a.tiles.TXT == kT.TXT;
+}
+
 template <typename T>
 __device__ __forceinline__ T& comp(vec2_t<T>& c, int which)
 {
@@ -188,11 +215,12 @@ __device__ __forceinline__ vec2_t<T> pack2(vec2_t<T> v1, vec2_t<T> v2)
 // P2: per pair of v-rows of T: DCT-II along x, spectral weights, then the
 // three inverse transforms along x; writes Ux, Uy and Up (Up over T) tiled.
 // ---------------------------------------------------------------------------
-template <typename T, int L, int F>
+template <typename T, int L, int F, bool kSq>
 __global__ __launch_bounds__(col_threads<T>(L)) void k_col_pass(
     SpectralArgs a, const T* __restrict__ Tt, T* __restrict__ Ux,
     T* __restrict__ Uy)
 {
+    constexpr Tiles kT = square_tiles<T, L>();
     using C = vec2_t<T>;
     constexpr int E = col_e<T>(L), TPF = L / E, NT = F * TPF, LP = lds_len(L);
     constexpr int TV = 2 * F;
@@ -200,12 +228,12 @@ __global__ __launch_bounds__(col_threads<T>(L)) void k_col_pass(
     C* sb = reinterpret_cast<C*>(smem);
     const int tid = threadIdx.x, f = tid / TPF, t = tid % TPF;
     C* buf = sb + f * LP;
-    const int TX = a.tiles.TX;            // Ux, Uy tiles (stores)
+    const int TX = kSq ? kT.TX : a.tiles.TX;      // Ux, Uy tiles (stores)
     const int lgTX = __builtin_ctz(TX);
-    const int TXT = a.tiles.TXT;          // T tiles (loads)
+    const int TXT = kSq ? kT.TXT : a.tiles.TXT;   // T tiles (loads)
     const int lgTXT = __builtin_ctz(TXT);
     // tile offsets by shifts: every tile extent and N are powers of two
-    const int lgNBV = __builtin_ctz(a.N) - __builtin_ctz(TV);
+    const int lgNBV = __builtin_ctz(kSq ? L : a.N) - __builtin_ctz(TV);
     const int b2 = blockIdx.x;
     const int v0 = b2 * TV;
     constexpr int lgTV = __builtin_ctz(TV);
@@ -341,11 +369,21 @@ __global__ __launch_bounds__(col_threads<T>(L)) void k_col_pass(
 // of a group are consecutive in XCD-logical order, so the Uy rows the
 // type-B block re-reads are still in that XCD's L2.
 // ---------------------------------------------------------------------------
-template <typename T, int L, int F>
-__global__ __launch_bounds__(row_threads<T>(L)) void k_row_inv(
+// Waves per SIMD P3 is compiled for: four at float32 (128 VGPRs, which the
+// pass fits), so a CU holds the four workgroups of 2048-point FFTs its LDS
+// allows; float64 takes what it needs.
+template <typename T>
+__host__ __device__ constexpr int row_waves()
+{
+    return sizeof(T) == 4 ? 4 : 1;
+}
+
+template <typename T, int L, int F, bool kSq>
+__global__ __launch_bounds__(row_threads<T>(L), row_waves<T>()) void k_row_inv(
     SpectralArgs a, const T* __restrict__ Ux, const T* __restrict__ Uy,
     T* __restrict__ fx, T* __restrict__ fy, T* __restrict__ phi)
 {
+    constexpr Tiles kT = square_tiles<T, L>();
     using C = vec2_t<T>;
     constexpr int E = row_e<T>(L), TPF = L / E, NT = F * TPF, LP = lds_len(L);
     constexpr int TX = 2 * F;
@@ -353,7 +391,7 @@ __global__ __launch_bounds__(row_threads<T>(L)) void k_row_inv(
     C* sb = reinterpret_cast<C*>(smem);
     const int tid = threadIdx.x, f = tid / TPF, t = tid % TPF;
     C* buf = sb + f * LP;
-    const int TV = a.tiles.TV;
+    const int TV = kSq ? kT.TV : a.tiles.TV;
     const int lgTV = __builtin_ctz(TV);
     const int lgNBV = __builtin_ctz(L) - lgTV;
     const C* post = reinterpret_cast<const C*>(a.postN);

@@ -73,7 +73,12 @@ hipError_t launch_col_pass(const SpectralArgs& a, const T* Tt, T* Ux, T* Uy,
         constexpr int L = decltype(lc)::value;
         constexpr int F = fpw<T>(L);
         const dim3 grid(a.N / (2 * F)), block(col_threads<T>(L));
-        DPEP_LAUNCH(ev, (k_col_pass<T, L, F>), grid, block, (lds_bytes<T, L>()), s, a, Tt, Ux, Uy);
+        if (square_form<T, L>(a))
+            DPEP_LAUNCH(ev, (k_col_pass<T, L, F, true>), grid, block,
+                        (lds_bytes<T, L>()), s, a, Tt, Ux, Uy);
+        else
+            DPEP_LAUNCH(ev, (k_col_pass<T, L, F, false>), grid, block, (lds_bytes<T, L>()), s,
+                        a, Tt, Ux, Uy);
         return hipGetLastError();
     });
 }
@@ -87,8 +92,12 @@ hipError_t launch_row_inv(const SpectralArgs& a, const T* Ux, const T* Uy,
         constexpr int F = fpw<T>(L);
         const int groups = a.M / (2 * F);
         const dim3 grid(groups * (a.potential ? 3 : 2)), block(row_threads<T>(L));
-        DPEP_LAUNCH(ev, (k_row_inv<T, L, F>), grid, block, (lds_bytes<T, L>()), s, a, Ux, Uy, fx,
-                    fy, phi);
+        if (square_form<T, L>(a))
+            DPEP_LAUNCH(ev, (k_row_inv<T, L, F, true>), grid, block,
+                        (lds_bytes<T, L>()), s, a, Ux, Uy, fx, fy, phi);
+        else
+            DPEP_LAUNCH(ev, (k_row_inv<T, L, F, false>), grid, block, (lds_bytes<T, L>()), s, a,
+                        Ux, Uy, fx, fy, phi);
         return hipGetLastError();
     });
 }
@@ -99,11 +108,20 @@ static hipError_t prepare_len()
     constexpr int F = fpw<T>(L);
     const int bytes = (int)lds_bytes<T, L>();
     hipError_t e;
-    if ((e = hipFuncSetAttribute((const void*)k_col_pass<T, L, F>,
+    constexpr bool kSq = L >= kSquareMin;
+    if ((e = hipFuncSetAttribute((const void*)k_col_pass<T, L, F, false>,
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, bytes)) ||
+        (e = hipFuncSetAttribute((const void*)k_row_inv<T, L, F, false>,
                                  hipFuncAttributeMaxDynamicSharedMemorySize, bytes)))
         return e;
-    return hipFuncSetAttribute((const void*)k_row_inv<T, L, F>,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if constexpr (kSq) {
+        if ((e = hipFuncSetAttribute((const void*)k_col_pass<T, L, F, true>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, bytes)))
+            return e;
+        return hipFuncSetAttribute((const void*)k_row_inv<T, L, F, true>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    }
+    return hipSuccess;
 }
 
 template <typename T>

@@ -101,6 +101,25 @@ static std::vector<T> table(int L, bool post)
     return v;
 }
 
+// The spectral passes in the form launch_col_pass / launch_row_inv pick:
+// tile extents compiled in for square grids of kSquareMin and more.
+template <typename T, int L, int F>
+static void col_pass_as_launched(const dpep::SpectralArgs& a, const T* Tt, T* Ux, T* Uy)
+{
+    using namespace dpep;
+    if (square_form<T, L>(a)) k_col_pass<T, L, F, true>(a, Tt, Ux, Uy);
+    else k_col_pass<T, L, F, false>(a, Tt, Ux, Uy);
+}
+
+template <typename T, int L, int F>
+static void row_inv_as_launched(const dpep::SpectralArgs& a, const T* Ux, const T* Uy, T* fx,
+                                T* fy, T* phi)
+{
+    using namespace dpep;
+    if (square_form<T, L>(a)) k_row_inv<T, L, F, true>(a, Ux, Uy, fx, fy, phi);
+    else k_row_inv<T, L, F, false>(a, Ux, Uy, fx, fy, phi);
+}
+
 template <typename T, int LM, int LN>
 static int run(int nc, bool det, bool pot, int ch, bool tall, bool force_stage, bool off)
 {
@@ -226,13 +245,13 @@ static int run(int nc, bool det, bool pot, int ch, bool tall, bool force_stage, 
         {
             constexpr int F = fpw<T>(LM);
             const size_t shm = (size_t)F * lds_len(LM) * sizeof(vec2_t<T>);
-            launch(N / (2 * F), col_threads<T>(LM), shm, [&] { k_col_pass<T, LM, F>(a, Tt, Ux, Uy); });
+            launch(N / (2 * F), col_threads<T>(LM), shm, [&] { col_pass_as_launched<T, LM, F>(a, Tt, Ux, Uy); });
         }
         {
             constexpr int F = fpw<T>(LN);
             const size_t shm = (size_t)F * lds_len(LN) * sizeof(vec2_t<T>);
             const unsigned grid = (M / (2 * F)) * (pot ? 3 : 2);
-            launch(grid, row_threads<T>(LN), shm, [&] { k_row_inv<T, LN, F>(a, Ux, Uy, fx, fy, phi); });
+            launch(grid, row_threads<T>(LN), shm, [&] { row_inv_as_launched<T, LN, F>(a, Ux, Uy, fx, fy, phi); });
         }
         if (nc > 0) {
             const size_t glds = gather_lds<T>(p.R, N);
@@ -368,13 +387,13 @@ static int run_spectral()
     {
         constexpr int F = fpw<T>(LM);
         const size_t shm = (size_t)F * lds_len(LM) * sizeof(vec2_t<T>);
-        launch(N / (2 * F), col_threads<T>(LM), shm, [&] { k_col_pass<T, LM, F>(a, Tt, Ux, Uy); });
+        launch(N / (2 * F), col_threads<T>(LM), shm, [&] { col_pass_as_launched<T, LM, F>(a, Tt, Ux, Uy); });
     }
     {
         constexpr int F = fpw<T>(LN);
         const size_t shm = (size_t)F * lds_len(LN) * sizeof(vec2_t<T>);
         launch((M / (2 * F)) * 3, row_threads<T>(LN), shm,
-               [&] { k_row_inv<T, LN, F>(a, Ux, Uy, fx, fy, phi); });
+               [&] { row_inv_as_launched<T, LN, F>(a, Ux, Uy, fx, fy, phi); });
     }
     std::vector<double> rphi(mn), rfx(mn), rfy(mn);
     oracle_solve_fft(rho.data(), M, N, bsx, bsy, rphi.data(), rfx.data(), rfy.data());
@@ -399,6 +418,7 @@ static int dispatch_spectral(int M, int N)
 {
 #define CASE(a, b) if (M == a && N == b) return run_spectral<T, a, b>();
     CASE(2048, 16) CASE(4096, 32) CASE(16, 2048) CASE(32, 4096) CASE(1024, 64)
+    CASE(512, 512) CASE(1024, 1024)
     if constexpr (sizeof(T) == 4) { CASE(8192, 8) CASE(8, 8192) }
 #undef CASE
     fprintf(stderr, "unsupported shape\n");

@@ -75,7 +75,9 @@ def test_kernels_in_bounds_and_accurate(emu, case):
 # 8192 the largest LDS use), against the oracle's FFT solve of the same density.
 SPECTRAL = ["f32 2048 16", "f32 4096 32", "f32 16 2048", "f32 32 4096", "f32 8192 8",
             "f32 8 8192", "f32 1024 64", "f64 2048 16", "f64 4096 32", "f64 1024 64",
-            "f64 16 2048", "f64 32 4096"]
+            "f64 16 2048", "f64 32 4096",
+            # square grids: the passes with their tile extents compiled in
+            "f32 512 512", "f64 512 512", "f32 1024 1024"]
 
 
 @pytest.mark.parametrize("case", SPECTRAL)
