@@ -1066,22 +1066,15 @@ __global__ __launch_bounds__(kBinThreads, 5) void k_bin_fill_staged(
 // scale fs is a power of two, so folding it into the row's weight (rat * tx
 // * fs, exact) rounds each value as (rat * tx * ty) * fs would; a row's
 // address steps by N, its columns are immediate offsets from it, and its x
-// overlap is formed as in record_partial (bitwise the same value).
-template <typename T>
-__device__ __forceinline__ void record_density(const vec4_t<T>& rg, unsigned rm, int k0,
-                                               int k1, int N, int stretch, T fs,
-                                               unsigned long long* tile)
+// overlap is formed as in record_partial (bitwise the same value).  The
+// first Q columns' adds are unrolled (each under its own lane mask), Q = 4
+// where a lane of the wave has a record spanning four or more columns and 3
+// otherwise (float64: 4), as in G1.
+template <typename T, int Q>
+__device__ __forceinline__ void density_rows(const RecView<T>& rv, const T* tyv, int ka, int kb,
+                                             int k0, int N, T fs, unsigned long long* tile)
 {
-    const RecView<T> rv = rec_view<T>(rg, rm, k0, stretch, N);
     const T xr = rv.xr, yr = rv.yr, rat = rv.rat, dx = rv.dx, dy = rv.dy;
-    const int ka = max(rv.bxl, k0), kb = min(rv.bxl + rv.nx, k1);
-    // y overlaps of the (usual) first 4 columns, shared by the rows; yr
-    // clamped to the grid's last column edge gives the columns past it no
-    // positive overlap and the others their own
-    const T yrc = min(yr, (T)(N - rv.byl));
-    T tyv[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) tyv[q] = min(yrc, (T)(q + 1)) - max(dy, (T)q);
     unsigned long long* row = tile + (__umul24((unsigned)(ka - k0), (unsigned)N) + (unsigned)rv.byl);
     T jx = (T)(ka - rv.bxl);
     for (int k = ka; k <= kb; ++k, row += N, jx += (T)1) {
@@ -1089,14 +1082,34 @@ __device__ __forceinline__ void record_density(const vec4_t<T>& rg, unsigned rm,
         if (!(tx > (T)0)) continue;
         const T rtxs = (rat * tx) * fs;
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+        for (int q = 0; q < Q; ++q)
             if (tyv[q] > (T)0) atomicAdd(row + q, to_fixed(rtxs * tyv[q]));
-        for (int q = 4; q <= rv.ny; ++q) {
+        for (int q = Q; q <= rv.ny; ++q) {
             const T ty = min(yr, (T)(q + 1)) - max(dy, (T)q);
             if (!(ty > (T)0)) continue;
             atomicAdd(row + q, to_fixed(rtxs * ty));
         }
     }
+}
+
+template <typename T>
+__device__ __forceinline__ void record_density(const vec4_t<T>& rg, unsigned rm, int k0,
+                                               int k1, int N, int stretch, T fs,
+                                               unsigned long long* tile)
+{
+    const RecView<T> rv = rec_view<T>(rg, rm, k0, stretch, N);
+    const int ka = max(rv.bxl, k0), kb = min(rv.bxl + rv.nx, k1);
+    // y overlaps of the (usual) first 4 columns, shared by the rows; yr
+    // clamped to the grid's last column edge gives the columns past it no
+    // positive overlap and the others their own
+    const T yrc = min(rv.yr, (T)(N - rv.byl));
+    T tyv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) tyv[q] = min(yrc, (T)(q + 1)) - max(rv.dy, (T)q);
+    if (sizeof(T) == 8 || __any(rv.ny >= 3))    // uniform (float64: Q = 4, as G1)
+        density_rows<T, 4>(rv, tyv, ka, kb, k0, N, fs, tile);
+    else
+        density_rows<T, 3>(rv, tyv, ka, kb, k0, N, fs, tile);
 }
 
 // Threads per team that handles one tall cell (K3's side-map adds, G2's
@@ -1368,33 +1381,27 @@ __global__ __launch_bounds__(kOnceThreads, (once_waves<T, CPT>())) void k_bin_fi
 // of the group's (fx, fy) pairs in LDS with rows N pairs apart.  G1 takes
 // the strip's records and its overflow records alike through it: the same
 // values in the same order, so the same partial.
-// The first four columns of a row are read unconditionally, with weight zero
-// where the record has no positive overlap (a column past its last, or a row
-// or column it only touches): those terms add a signed zero, which leaves
-// every sum bitwise as if they were skipped.  Branching around each read
-// instead made every read wait for its own LDS round trip.  So up to 3 pairs
-// past any column of a row must be readable and finite: the next row's
-// pairs, or (after the last row) padding (kGatherPadBins).
+// The first Q columns of a row are read unconditionally (float32: Q = 4 where
+// a lane of the wave has a record spanning four or more columns, the wave's
+// choice by __any, else 3; float64: 4), with weight zero where the record has no positive overlap
+// (a column past its last, or a row or column it only touches): those terms
+// add a signed zero, which leaves every sum bitwise as if they were skipped,
+// so either Q gives the same partial.  Branching around each read instead
+// made every read wait for its own LDS round trip; Q = 4 for every wave
+// measured slower where records span two or three columns (C3, C5), Q = 3
+// for every wave slower where many span four (C2).  So up to 3 pairs past
+// any column of a row must be readable and finite: the next row's pairs, or
+// (after the last row) padding (kGatherPadBins).
 // A row's x overlap is min(xr - jx, 1) - max(dx - jx, 0) for the row jx
 // rows past the record's first: xr - jx is exact for every row the record
 // spans (jx is an integer no larger than xr) and dx - jx is negative past the
 // first row, so the overlap equals min(xr, jx + 1) - max(dx, jx) bit for bit
 // with a float counter and no conversion per row.
-template <typename T>
-__device__ __forceinline__ vec2_t<T> record_partial(const vec4_t<T>& rg, unsigned rm, int k0,
-                                                    int kg0, int kg1, int N, int stretch, T ba,
-                                                    const vec2_t<T>* rows)
+template <typename T, int Q>
+__device__ __forceinline__ vec2_t<T> partial_rows(const RecView<T>& rv, const T* tyv, int ka,
+                                                  int kb, int kg0, int N, const vec2_t<T>* rows)
 {
-    const RecView<T> rv = rec_view<T>(rg, rm, k0, stretch, N);
     const T xr = rv.xr, yr = rv.yr, dx = rv.dx, dy = rv.dy;
-    const int ka = max(rv.bxl, kg0), kb = min(rv.bxl + rv.nx, kg1);
-    // y overlaps of the (usual) first 4 columns, shared by the rows (zero
-    // where not positive); yr clamped to the grid's last column edge gives
-    // the columns past it no positive overlap and the others their own
-    const T yrc = min(yr, (T)(N - rv.byl));
-    T tyv[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) tyv[q] = max(min(yrc, (T)(q + 1)) - max(dy, (T)q), (T)0);
     T ax = (T)0, ay = (T)0;
     // row offsets below 2^24 (rows < 8, N <= 8192): a 24-bit multiply
     const vec2_t<T>* rf = rows + (__umul24((unsigned)(ka - kg0), (unsigned)N) + (unsigned)rv.byl);
@@ -1402,16 +1409,16 @@ __device__ __forceinline__ vec2_t<T> record_partial(const vec4_t<T>& rg, unsigne
     for (int k = ka; k <= kb; ++k, rf += N, jx += (T)1) {
         const T t = min(xr - jx, (T)1) - max(dx - jx, (T)0);
         const T tx = t > (T)0 ? t : (T)0;
-        vec2_t<T> f4[4];
+        vec2_t<T> fq[Q];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) f4[q] = rf[q];
+        for (int q = 0; q < Q; ++q) fq[q] = rf[q];
         T sx_ = (T)0, sy_ = (T)0;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            sx_ += tyv[q] * f4[q].x;
-            sy_ += tyv[q] * f4[q].y;
+        for (int q = 0; q < Q; ++q) {
+            sx_ += tyv[q] * fq[q].x;
+            sy_ += tyv[q] * fq[q].y;
         }
-        for (int q = 4; q <= rv.ny; ++q) {
+        for (int q = Q; q <= rv.ny; ++q) {
             const T ty = min(yr, (T)(q + 1)) - max(dy, (T)q);
             if (!(ty > (T)0)) continue;
             const vec2_t<T> f = rf[q];
@@ -1421,8 +1428,29 @@ __device__ __forceinline__ vec2_t<T> record_partial(const vec4_t<T>& rg, unsigne
         ax += tx * sx_;
         ay += tx * sy_;
     }
+    return vec2_t<T>{ax, ay};
+}
+
+template <typename T>
+__device__ __forceinline__ vec2_t<T> record_partial(const vec4_t<T>& rg, unsigned rm, int k0,
+                                                    int kg0, int kg1, int N, int stretch, T ba,
+                                                    const vec2_t<T>* rows)
+{
+    const RecView<T> rv = rec_view<T>(rg, rm, k0, stretch, N);
+    const int ka = max(rv.bxl, kg0), kb = min(rv.bxl + rv.nx, kg1);
+    // y overlaps of the (usual) first 4 columns, shared by the rows (zero
+    // where not positive); yr clamped to the grid's last column edge gives
+    // the columns past it no positive overlap and the others their own
+    const T yrc = min(rv.yr, (T)(N - rv.byl));
+    T tyv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) tyv[q] = max(min(yrc, (T)(q + 1)) - max(rv.dy, (T)q), (T)0);
+    // float64 keeps Q = 4 (the choice measured +1.2 us at 1.1M cells, 2048^2)
+    const vec2_t<T> a = (sizeof(T) == 8 || __any(rv.ny >= 3))   // uniform
+                            ? partial_rows<T, 4>(rv, tyv, ka, kb, kg0, N, rows)
+                            : partial_rows<T, 3>(rv, tyv, ka, kb, kg0, N, rows);
     const T sc = rv.rat * ba;
-    return vec2_t<T>{sc * ax, sc * ay};
+    return vec2_t<T>{sc * a.x, sc * a.y};
 }
 
 // rho = D0 + fixed-point sum, rounded once to T.

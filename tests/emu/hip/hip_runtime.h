@@ -85,6 +85,9 @@ inline unsigned long long __double2ull_rn(double x)
     return (unsigned long long)std::nearbyint(x);
 }
 #define __builtin_amdgcn_rcpf(x) (1.0f / (x))
+// a wave vote decided per lane: the kernels only use it to choose between
+// forms that give the same results
+#define __any(p) (p)
 inline unsigned __float2uint_rn(float x)
 {
     return (unsigned)std::nearbyint(x);
