@@ -1482,14 +1482,33 @@ __host__ __device__ constexpr int acc_e(int L, int R)
 }
 
 template <typename T, int L>
-__host__ __device__ constexpr size_t acc_lds_bytes()
+__host__ __device__ constexpr size_t acc_lds_main()
 {
     constexpr int R = strip_rows(L);
     // the tile, the split-strip flag (16 bytes), the overflow run table
     const size_t tile = (size_t)R * L * sizeof(unsigned long long) + 16 +
                         (size_t)kRunBatch * sizeof(uint2);
     const size_t fft = (size_t)(R / 2) * lds_len(L) * sizeof(vec2_t<T>);
-    return tile > fft ? tile : fft;
+    return ((tile > fft ? tile : fft) + 15) / 16 * 16;
+}
+
+// Whether K4 copies the table of W^m (m < L) into LDS at its start, beside
+// the tile (float32, where a CU still holds as many K4 workgroups): the row
+// DCT then reads its twiddles from LDS, with no global-load latency between
+// the flush and the FFT.
+template <typename T, int L>
+__host__ __device__ constexpr bool acc_twiddles_in_lds()
+{
+    constexpr size_t kLds = 163840, main = acc_lds_main<T, L>();
+    constexpr size_t with = main + (size_t)L * sizeof(vec2_t<T>);
+    return sizeof(T) == 4 && with <= kLds && kLds / with == kLds / main;
+}
+
+template <typename T, int L>
+__host__ __device__ constexpr size_t acc_lds_bytes()
+{
+    return acc_lds_main<T, L>() +
+           (acc_twiddles_in_lds<T, L>() ? (size_t)L * sizeof(vec2_t<T>) : 0);
 }
 
 template <typename T, int L>
@@ -1525,6 +1544,12 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     // than two ahead)
     StripMap sm;
     strip_map(b, s, sm);
+    constexpr bool kTwL = acc_twiddles_in_lds<T, L>();
+    C* twl = reinterpret_cast<C*>(smem + acc_lds_main<T, L>());   // kTwL: W^m, m < L
+    if constexpr (kTwL) {   // read at the row DCT, many barriers on
+        const C* tw = reinterpret_cast<const C*>(a.twN);
+        for (int e = tid; e < L; e += kAccThreads) twl[e] = tw[e];
+    }
     for (int e = tid; e < RN; e += kAccThreads) tile[e] = 0ull;
     unsigned e0, e1;                            // this chunk's records
     item_range(item, sm, e0, e1);
@@ -1660,7 +1685,7 @@ __global__ __launch_bounds__(kAccThreads) void k_strip_acc(
     FftTw<T, L, E> twp;
     C pst[E / 2];
     if constexpr (sizeof(T) == 4) {
-        fft_tw_fetch<T, L, E>(twp, t, reinterpret_cast<const C*>(a.twN));
+        fft_tw_fetch<T, L, E>(twp, t, kTwL ? twl : reinterpret_cast<const C*>(a.twN));
 #pragma unroll
         for (int i = 0; i < E / 2; ++i) pst[i] = post_of<T, L>(post, t + TPF * i);
     }
